@@ -1,0 +1,578 @@
+/*
+ * pb_oracle.c -- CPU restatement of promptboot's decode-step sampler.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This file is the checker for the HIP sampler in
+ * promptboot_amd/csrc.  Only tests/, __graft_entry__.smoke() and the
+ * cpu_baseline leg of bench.py may load it, and only as the checker or as the
+ * reported single-core CPU baseline; the product path never calls it.
+ *
+ * It restates, in plain C with scalar SSE IEEE-754 binary32/binary64
+ * arithmetic (round-to-nearest-even, no flush-to-zero, no FMA contraction),
+ * the reference functions below.  Each function cites the reference file:line
+ * it follows (paths are relative to the promptboot repository root):
+ *
+ *   crates/promptboot-core/src/inference.rs:737-965    validation, PRNG, API
+ *   crates/promptboot-core/src/fp32_sse2.rs:147-345    scalar IEEE ops
+ *   crates/promptboot-core/src/fp32_sse2.rs:378-469    scalbnf / expf
+ *   crates/promptboot-core/src/fp32_sse2.rs:848-867    MXCSR 0x1f80 scope
+ *   crates/promptboot-core/src/fp32_sse2.rs:1772-1876  argmax, top-k/top-p
+ *                                                      draw, repetition penalty
+ *
+ * Pinning (see tests/test_oracle_*.py): PRNG states after 8 and 41 draws, the
+ * 16 expf edge pairs and a 1-ulp bound against correctly rounded exp, the
+ * penalty vectors, the dominant-EOS and bounded rows, the real Qwen "hello"
+ * row known answer (token 9707), the llama.cpp top-8 lists of the three real
+ * rows, the error tuples, a stable-sort brute force of the top-20, an
+ * independent float64 softmax, and an exhaustive sweep of all 2^24 uniforms
+ * against the categorical CDF.
+ *
+ * Build: oracle/Makefile (gcc -O2 -msse2 -mfpmath=sse -ffp-contract=off).
+ */
+#include <math.h>
+#include <pthread.h>
+#include <stddef.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+#include <xmmintrin.h>
+
+#if defined(__FMA__) || defined(__FAST_MATH__)
+#error "the oracle must be built without FMA contraction or fast-math"
+#endif
+
+#define PBO_VOCAB 151936u
+#define PBO_TOP_K 20
+#define PBO_SEEN_BYTES ((PBO_VOCAB + 7u) / 8u)
+#define PBO_NO_LAYER 0xffffffffu
+#define PBO_NO_TENSOR 0xffffffffu
+
+/* InferenceStatus / InferenceDomain / InferenceFieldKind values
+ * (crates/promptboot-core/src/inference.rs:155-212). */
+enum { ST_OK = 0, ST_TOKEN_ID = 3, ST_CAPACITY = 4, ST_NONFINITE_OUTPUT = 7 };
+enum { DOM_LOGITS = 18, DOM_ARGMAX = 19 };
+enum { FK_TOKEN = 2, FK_BYTES = 4, FK_FINITE = 7, FK_LOGITS = 12 };
+
+/* Row flags reported beside each draw (not part of the reference). */
+#define PBO_FLAG_DRAW_BOUNDARY 1u   /* target within 1e-6*kept_total of a CDF step */
+#define PBO_FLAG_CUTOFF_BOUNDARY 2u /* top-p cutoff within 1e-6*total of a prefix */
+
+typedef struct {
+    uint64_t state;
+    uint64_t draws;
+} pbo_state; /* inference.rs:772-776, 16 bytes */
+
+typedef struct {
+    uint32_t status, domain, layer, position, tensor_id, reserved;
+    uint64_t needed, available, detail;
+} pbo_error; /* inference.rs:226-237, 48 bytes */
+
+typedef struct {
+    uint32_t token;
+    uint32_t logit_bits;
+} pbo_top_logit; /* inference.rs:767-770 */
+
+/* Everything the top-k/top-p stage knows about one row. */
+typedef struct {
+    uint32_t ids[PBO_TOP_K];        /* rank order: value desc, id asc */
+    uint32_t value_bits[PBO_TOP_K]; /* penalised logits of those ids */
+    uint32_t weight_bits[PBO_TOP_K];/* expf((v - max) / 0.7) */
+    float probs[PBO_TOP_K];         /* w[i] / kept_total for i < kept, else 0 */
+    uint32_t kept;                  /* survivors after top-p, 1..20 */
+    uint32_t rank;                  /* rank of the drawn token, < kept */
+    uint32_t flags;                 /* PBO_FLAG_* */
+    uint32_t token;
+} pbo_detail;
+
+static inline float fb(uint32_t bits) {
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+static inline uint32_t bf(float f) {
+    uint32_t b;
+    memcpy(&b, &f, 4);
+    return b;
+}
+
+/* MXCSR scope: round-to-nearest-even, no FTZ/DAZ, all exceptions masked
+ * (fp32_sse2.rs:848-867). */
+static inline unsigned int enter_fp(void) {
+    unsigned int previous = _mm_getcsr();
+    _mm_setcsr(0x1f80u);
+    return previous;
+}
+static inline void exit_fp(unsigned int previous) { _mm_setcsr(previous); }
+
+/* ---- PRNG: xorshift64* with draw counter (inference.rs:779-810) ---- */
+
+void pbo_state_new(pbo_state *s, uint64_t seed) {
+    s->state = seed == 0 ? 0x9e3779b97f4a7c15ull : seed;
+    s->draws = 0;
+}
+
+uint32_t pbo_next_24(pbo_state *s) {
+    uint64_t v = s->state;
+    v ^= v >> 12;
+    v ^= v << 25;
+    v ^= v >> 27;
+    s->state = v;
+    s->draws += 1;
+    return (uint32_t)((v * 0x2545f4914f6cdd1dull) >> 40);
+}
+
+/* ---- scalbnf / expf (fp32_sse2.rs:378-469; FreeBSD e_expf method via
+ * rust-lang/libm 0.2.11, Sun Microsystems notice retained below) ---- */
+
+static float scalbnf_ref(float value, int32_t exponent) {
+    const float two127 = fb(0x7f000000u);
+    const float two_m102 = fb(0x00800000u) * fb(0x4b800000u); /* 2^-126 * 2^24 */
+    if (exponent > 127) {
+        value = value * two127;
+        exponent -= 127;
+        if (exponent > 127) {
+            value = value * two127;
+            exponent -= 127;
+            if (exponent > 127) exponent = 127;
+        }
+    } else if (exponent < -126) {
+        value = value * two_m102;
+        exponent += 126 - 24;
+        if (exponent < -126) {
+            value = value * two_m102;
+            exponent += 126 - 24;
+            if (exponent < -126) exponent = -126;
+        }
+    }
+    return value * fb((uint32_t)(0x7f + exponent) << 23);
+}
+
+/*
+ * ====================================================
+ * Copyright (C) 1993 by Sun Microsystems, Inc. All rights reserved.
+ *
+ * Developed at SunPro, a Sun Microsystems, Inc. business.
+ * Permission to use, copy, modify, and distribute this
+ * software is freely granted, provided that this notice
+ * is preserved.
+ * ====================================================
+ * Method: k = round(x/ln2), r = x - k*ln2 split as hi - lo, a degree-2
+ * rational approximation of exp(r), then a scale by 2^k.
+ */
+static float expf_ref(float x) {
+    const uint32_t xb = bf(x);
+    const uint32_t magnitude = xb & 0x7fffffffu;
+    const uint32_t sign = xb >> 31;
+    if (magnitude >= 0x42aeac50u) {
+        if (magnitude > 0x7f800000u) return x;                          /* NaN */
+        if (magnitude >= 0x42b17218u && sign == 0) return x * fb(0x7f000000u); /* overflow */
+        if (sign != 0 && magnitude >= 0x42cff1b5u) return 0.0f;          /* underflow */
+    }
+    int32_t k;
+    float hi, lo;
+    if (magnitude > 0x3eb17218u) {
+        if (magnitude > 0x3f851592u) {
+            const float half = sign == 0 ? fb(0x3f000000u) : fb(0xbf000000u);
+            const float scaled = fb(0x3fb8aa3bu) * x; /* x / ln2 */
+            k = (int32_t)(scaled + half);             /* truncation toward zero */
+        } else {
+            k = 1 - (int32_t)sign - (int32_t)sign;
+        }
+        const float kf = (float)k;
+        const float khi = kf * fb(0x3f317200u); /* k * ln2_hi */
+        hi = x - khi;
+        lo = kf * fb(0x35bfbe8eu);              /* k * ln2_lo */
+        x = hi - lo;
+    } else if (magnitude > 0x39000000u) {
+        k = 0;
+        hi = x;
+        lo = 0.0f;
+    } else {
+        return fb(0x3f800000u) + x;
+    }
+    const float xx = x * x;
+    const float poly = fb(0x3e2aaa8fu) + xx * fb(0xbb355215u);
+    const float c = x - xx * poly;
+    const float num = x * c;
+    const float den = fb(0x40000000u) - c;
+    const float frac = num / den;
+    const float inner = (frac - lo) + hi;
+    const float y = fb(0x3f800000u) + inner;
+    return k == 0 ? y : scalbnf_ref(y, k);
+}
+
+uint32_t pbo_expf_bits(uint32_t x) {
+    const unsigned int saved = enter_fp();
+    const uint32_t r = bf(expf_ref(fb(x)));
+    exit_fp(saved);
+    return r;
+}
+
+/* Strict IEEE "greater": ucomiss + seta, false on unordered (fp32_sse2.rs:263-275). */
+static inline int greater(uint32_t left, uint32_t right) { return fb(left) > fb(right); }
+
+static inline int finite_bits(uint32_t bits) { return (bits & 0x7f800000u) != 0x7f800000u; }
+
+/* ---- repetition penalty (fp32_sse2.rs:1848-1876) ---- */
+
+static void apply_repetition_penalty(uint32_t *logits, const uint32_t *tokens, size_t count,
+                                     uint8_t *seen) {
+    const float penalty = fb(0x3f8ccccdu); /* 1.1f */
+    for (size_t at = 0; at < count; ++at) {
+        const uint32_t token = tokens[at];
+        uint8_t *byte = seen + token / 8;
+        const uint8_t bit = (uint8_t)(1u << (token & 7));
+        if ((*byte & bit) == 0) {
+            *byte |= bit;
+            const uint32_t score = logits[token];
+            float adjusted;
+            if ((score & 0x80000000u) != 0 && (score & 0x7fffffffu) != 0)
+                adjusted = fb(score) * penalty;
+            else
+                adjusted = fb(score) / penalty;
+            logits[token] = bf(adjusted);
+        }
+    }
+    for (size_t at = 0; at < count; ++at) {
+        const uint32_t token = tokens[at];
+        seen[token / 8] &= (uint8_t)~(1u << (token & 7));
+    }
+}
+
+void pbo_apply_repetition_penalty(uint32_t *logits, const uint32_t *tokens, size_t count,
+                                  uint8_t *seen) {
+    const unsigned int saved = enter_fp();
+    apply_repetition_penalty(logits, tokens, count, seen);
+    exit_fp(saved);
+}
+
+/* ---- top-k 20 / temperature 0.7 / top-p 0.8 / draw (fp32_sse2.rs:1786-1846) ---- */
+
+static uint32_t sample_top_k_top_p(const uint32_t *logits, size_t words, uint32_t random_24,
+                                   pbo_detail *detail) {
+    const float temperature = fb(0x3f333333u); /* 0.7f */
+    const float top_p = fb(0x3f4ccccdu);       /* 0.8f */
+    const float two_pow_24 = fb(0x4b800000u);
+    uint32_t ids[PBO_TOP_K];
+    uint32_t values[PBO_TOP_K];
+    for (int at = 0; at < PBO_TOP_K; ++at) {
+        ids[at] = 0xffffffffu;
+        values[at] = 0xff800000u;
+    }
+    /* Ascending-id scan; a value is inserted in front of the first empty slot or
+     * the first slot it strictly exceeds, so equal values keep ascending ids. */
+    for (size_t token = 0; token < words; ++token) {
+        const uint32_t value = logits[token];
+        int insertion = PBO_TOP_K;
+        for (int at = 0; at < PBO_TOP_K; ++at) {
+            if (ids[at] == 0xffffffffu || greater(value, values[at])) {
+                insertion = at;
+                break;
+            }
+        }
+        if (insertion < PBO_TOP_K) {
+            for (int at = PBO_TOP_K - 1; at > insertion; --at) {
+                ids[at] = ids[at - 1];
+                values[at] = values[at - 1];
+            }
+            ids[insertion] = (uint32_t)token;
+            values[insertion] = value;
+        }
+    }
+
+    const float maximum = fb(values[0]);
+    float weights[PBO_TOP_K];
+    double total = 0.0;
+    for (int at = 0; at < PBO_TOP_K; ++at) {
+        const float shifted = fb(values[at]) - maximum;
+        weights[at] = expf_ref(shifted / temperature);
+        total = total + (double)weights[at];
+    }
+    const float cutoff = (float)total * top_p;
+    int kept = PBO_TOP_K;
+    double kept_total = 0.0;
+    double prefix[PBO_TOP_K];
+    double running = 0.0;
+    for (int at = 0; at < PBO_TOP_K; ++at) {
+        running = running + (double)weights[at];
+        prefix[at] = running;
+    }
+    for (int at = 0; at < PBO_TOP_K; ++at) {
+        kept_total = kept_total + (double)weights[at];
+        if (!(cutoff > (float)kept_total)) {
+            kept = at + 1;
+            break;
+        }
+    }
+
+    const float unit = (float)(random_24 & 0x00ffffffu) / two_pow_24;
+    const float target = (float)kept_total * unit;
+    int rank = kept - 1;
+    double cumulative = 0.0;
+    for (int at = 0; at < kept; ++at) {
+        cumulative = cumulative + (double)weights[at];
+        if ((float)cumulative > target) {
+            rank = at;
+            break;
+        }
+    }
+
+    if (detail) {
+        uint32_t flags = 0;
+        const double draw_tol = 1e-6 * (double)(float)kept_total;
+        for (int at = 0; at < kept; ++at) {
+            if (fabs((double)(float)prefix[at] - (double)target) <= draw_tol)
+                flags |= PBO_FLAG_DRAW_BOUNDARY;
+        }
+        const double cut_tol = 1e-6 * (double)(float)total;
+        for (int at = 0; at < PBO_TOP_K; ++at) {
+            if (fabs((double)(float)prefix[at] - (double)cutoff) <= cut_tol)
+                flags |= PBO_FLAG_CUTOFF_BOUNDARY;
+        }
+        for (int at = 0; at < PBO_TOP_K; ++at) {
+            detail->ids[at] = ids[at];
+            detail->value_bits[at] = values[at];
+            detail->weight_bits[at] = bf(weights[at]);
+            detail->probs[at] = at < kept ? (float)((double)weights[at] / kept_total) : 0.0f;
+        }
+        detail->kept = (uint32_t)kept;
+        detail->rank = (uint32_t)rank;
+        detail->flags = flags;
+        detail->token = ids[rank];
+    }
+    return ids[rank];
+}
+
+uint32_t pbo_sample_top_k_top_p(const uint32_t *logits, size_t words, uint32_t random_24,
+                                pbo_detail *detail) {
+    const unsigned int saved = enter_fp();
+    const uint32_t r = sample_top_k_top_p(logits, words, random_24, detail);
+    exit_fp(saved);
+    return r;
+}
+
+/* ---- argmax, lowest id on ties (fp32_sse2.rs:1772-1784) ---- */
+
+static uint32_t argmax(const uint32_t *logits, size_t words) {
+    size_t selected = 0;
+    uint32_t best = logits[0];
+    for (size_t index = 1; index < words; ++index) {
+        if (greater(logits[index], best)) {
+            best = logits[index];
+            selected = index;
+        }
+    }
+    return (uint32_t)selected;
+}
+
+/* ---- errors and validation (inference.rs:239-264, 737-757, 883-903) ---- */
+
+static void set_error(pbo_error *e, uint32_t status, uint32_t domain, uint64_t needed,
+                      uint64_t available, uint32_t kind, uint32_t sub) {
+    if (!e) return;
+    e->status = status;
+    e->domain = domain;
+    e->layer = PBO_NO_LAYER;
+    e->position = 0;
+    e->tensor_id = PBO_NO_TENSOR;
+    e->reserved = 0;
+    e->needed = needed;
+    e->available = available;
+    e->detail = ((uint64_t)kind << 32) | sub;
+}
+
+static void clear_error(pbo_error *e) {
+    if (e) memset(e, 0, sizeof *e);
+}
+
+static int validate_sample_logits(const uint32_t *logits, size_t len, pbo_error *err) {
+    if (len != PBO_VOCAB) {
+        set_error(err, ST_CAPACITY, DOM_LOGITS, PBO_VOCAB, len, FK_LOGITS, 0);
+        return ST_CAPACITY;
+    }
+    for (size_t index = 0; index < len; ++index) {
+        if (!finite_bits(logits[index])) {
+            set_error(err, ST_NONFINITE_OUTPUT, DOM_ARGMAX, 0, logits[index], FK_FINITE,
+                      (uint32_t)index);
+            return ST_NONFINITE_OUTPUT;
+        }
+    }
+    return ST_OK;
+}
+
+/* sample_token (inference.rs:914-917). */
+int pbo_sample_token(const uint32_t *logits, size_t len, pbo_state *state, uint32_t *out,
+                     pbo_error *err) {
+    clear_error(err);
+    int status = validate_sample_logits(logits, len, err);
+    if (status != ST_OK) return status;
+    const uint32_t r = pbo_next_24(state);
+    *out = pbo_sample_top_k_top_p(logits, len, r, NULL);
+    return ST_OK;
+}
+
+/* sample_token_with_repetition (inference.rs:919-965): validate, check the
+ * scratch bitmap length and every history id, penalise in place, then draw. */
+int pbo_sample_token_with_repetition(uint32_t *logits, size_t len, const uint32_t *tokens,
+                                     size_t count, uint8_t *seen, size_t seen_len,
+                                     pbo_state *state, uint32_t *out, pbo_error *err,
+                                     pbo_detail *detail) {
+    clear_error(err);
+    int status = validate_sample_logits(logits, len, err);
+    if (status != ST_OK) return status;
+    const size_t needed = (len + 7) / 8;
+    if (seen_len < needed) {
+        set_error(err, ST_CAPACITY, DOM_ARGMAX, needed, seen_len, FK_BYTES, 2);
+        return ST_CAPACITY;
+    }
+    for (size_t at = 0; at < count; ++at) {
+        if (tokens[at] >= len) {
+            set_error(err, ST_TOKEN_ID, DOM_ARGMAX, len, tokens[at], FK_TOKEN, 0);
+            return ST_TOKEN_ID;
+        }
+    }
+    pbo_apply_repetition_penalty(logits, tokens, count, seen);
+    const uint32_t r = pbo_next_24(state);
+    *out = pbo_sample_top_k_top_p(logits, len, r, detail);
+    return ST_OK;
+}
+
+/* greedy_token (inference.rs:861-881). */
+int pbo_greedy_token(const uint32_t *logits, size_t len, uint32_t *out, pbo_error *err) {
+    clear_error(err);
+    int status = validate_sample_logits(logits, len, err);
+    if (status != ST_OK) return status;
+    const unsigned int saved = enter_fp();
+    *out = argmax(logits, len);
+    exit_fp(saved);
+    return ST_OK;
+}
+
+/* top_logits_8 (inference.rs:814-859): insertion from the back, moving past
+ * strictly smaller values only; the output is untouched on error. */
+int pbo_top_logits_8(const uint32_t *logits, size_t len, pbo_top_logit *output, pbo_error *err) {
+    clear_error(err);
+    if (len != PBO_VOCAB) {
+        set_error(err, ST_CAPACITY, DOM_LOGITS, PBO_VOCAB, len, FK_LOGITS, 0);
+        return ST_CAPACITY;
+    }
+    pbo_top_logit staged[8];
+    memset(staged, 0, sizeof staged);
+    size_t used = 0;
+    const unsigned int saved = enter_fp();
+    for (size_t token = 0; token < len; ++token) {
+        const uint32_t bits = logits[token];
+        if (!finite_bits(bits)) {
+            exit_fp(saved);
+            set_error(err, ST_NONFINITE_OUTPUT, DOM_ARGMAX, 0, bits, FK_FINITE, (uint32_t)token);
+            return ST_NONFINITE_OUTPUT;
+        }
+        size_t insertion = used;
+        while (insertion != 0 && greater(bits, staged[insertion - 1].logit_bits)) {
+            if (insertion < 8) staged[insertion] = staged[insertion - 1];
+            insertion -= 1;
+        }
+        if (insertion < 8) {
+            staged[insertion].token = (uint32_t)token;
+            staged[insertion].logit_bits = bits;
+        }
+        used = used + 1 < 8 ? used + 1 : 8;
+    }
+    exit_fp(saved);
+    memcpy(output, staged, sizeof staged);
+    return ST_OK;
+}
+
+/* ---- batched driver for tests and the CPU baseline ----
+ *
+ * Row r: copy logits[r*ld .. r*ld+vocab) into private scratch, run
+ * sample_token_with_repetition with history hist[r*hist_ld .. +hist_len[r])
+ * and the given 24-bit uniform random_24[r] (the caller advanced one
+ * SamplingState per row).  On error the token is 0xffffffff and err[r] holds
+ * the tuple.  When penalized_out is not NULL the penalised row is written
+ * there (same layout as logits).  threads <= 1 runs on the calling thread. */
+
+typedef struct {
+    const uint32_t *logits;
+    size_t ld, vocab;
+    const uint32_t *hist;
+    size_t hist_ld;
+    const uint32_t *hist_len;
+    const uint32_t *random_24;
+    uint32_t *token;
+    pbo_detail *detail;
+    pbo_error *err;
+    uint32_t *penalized_out;
+    uint32_t row_begin, row_end;
+} batch_job;
+
+static void run_row(const batch_job *job, uint32_t r, uint32_t *row, uint8_t *seen) {
+    const uint32_t *src = job->logits + (size_t)r * job->ld;
+    memcpy(row, src, job->vocab * 4);
+    const uint32_t *hist = job->hist ? job->hist + (size_t)r * job->hist_ld : NULL;
+    const size_t count = job->hist_len ? job->hist_len[r] : 0;
+    pbo_error e;
+    clear_error(&e);
+    int status = validate_sample_logits(row, job->vocab, &e);
+    if (status == ST_OK) {
+        for (size_t at = 0; at < count; ++at) {
+            if (hist[at] >= job->vocab) {
+                set_error(&e, ST_TOKEN_ID, DOM_ARGMAX, job->vocab, hist[at], FK_TOKEN, 0);
+                status = ST_TOKEN_ID;
+                break;
+            }
+        }
+    }
+    uint32_t token = 0xffffffffu;
+    if (status == ST_OK) {
+        const unsigned int saved = enter_fp();
+        apply_repetition_penalty(row, hist, count, seen);
+        token = sample_top_k_top_p(row, job->vocab, job->random_24[r],
+                                   job->detail ? job->detail + r : NULL);
+        exit_fp(saved);
+        if (job->penalized_out) memcpy(job->penalized_out + (size_t)r * job->ld, row, job->vocab * 4);
+    } else if (job->detail) {
+        memset(job->detail + r, 0xff, sizeof(pbo_detail));
+    }
+    job->token[r] = token;
+    if (job->err) job->err[r] = e;
+}
+
+static void *batch_worker(void *arg) {
+    const batch_job *job = (const batch_job *)arg;
+    uint32_t *row = (uint32_t *)malloc(job->vocab * 4);
+    uint8_t *seen = (uint8_t *)calloc((job->vocab + 7) / 8, 1);
+    for (uint32_t r = job->row_begin; r < job->row_end; ++r) run_row(job, r, row, seen);
+    free(seen);
+    free(row);
+    return NULL;
+}
+
+int pbo_sample_batch(const uint32_t *logits, size_t ld, size_t vocab, uint32_t rows,
+                     const uint32_t *hist, size_t hist_ld, const uint32_t *hist_len,
+                     const uint32_t *random_24, uint32_t *token, pbo_detail *detail,
+                     pbo_error *err, uint32_t *penalized_out, int threads) {
+    if (threads < 1) threads = 1;
+    if ((uint32_t)threads > rows) threads = rows ? (int)rows : 1;
+    batch_job base = {logits, ld, vocab, hist, hist_ld, hist_len, random_24, token,
+                      detail, err, penalized_out, 0, rows};
+    if (threads == 1) {
+        batch_worker(&base);
+        return 0;
+    }
+    pthread_t tid[256];
+    batch_job jobs[256];
+    if (threads > 256) threads = 256;
+    for (int t = 0; t < threads; ++t) {
+        jobs[t] = base;
+        jobs[t].row_begin = (uint32_t)((uint64_t)rows * t / threads);
+        jobs[t].row_end = (uint32_t)((uint64_t)rows * (t + 1) / threads);
+        pthread_create(&tid[t], NULL, batch_worker, &jobs[t]);
+    }
+    for (int t = 0; t < threads; ++t) pthread_join(tid[t], NULL);
+    return 0;
+}
+
+/* Layout probes so the Python side can check struct sizes. */
+size_t pbo_sizeof_detail(void) { return sizeof(pbo_detail); }
+size_t pbo_sizeof_error(void) { return sizeof(pbo_error); }
+size_t pbo_sizeof_state(void) { return sizeof(pbo_state); }
