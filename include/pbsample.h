@@ -1,0 +1,214 @@
+/*
+ * pbsample.h -- C ABI of the MI355X (gfx950) decode-step token sampler.
+ *
+ * Drop-in for promptboot's sampler path.  Reference interfaces replaced (paths
+ * relative to the promptboot repository root):
+ *
+ *   SamplingState, new/state/draws/next_24 crates/promptboot-core/src/inference.rs:772-810
+ *   sample_token_with_repetition          crates/promptboot-core/src/inference.rs:919-965
+ *   sample_token                          crates/promptboot-core/src/inference.rs:914-917
+ *   greedy_token                          crates/promptboot-core/src/inference.rs:861-881
+ *   top_logits_8                          crates/promptboot-core/src/inference.rs:814-859
+ *   InferenceError / status / domain /    crates/promptboot-core/src/inference.rs:155-264
+ *   field-kind codes
+ *   policy constants                      crates/promptboot-core/src/inference.rs:16-23
+ *
+ * Conventions kept from the reference: floats never cross the ABI (logits are
+ * binary32 bit patterns in uint32_t words, fp32_sse2.rs:1-6); every call
+ * returns an InferenceStatus value and fills a 48-byte error record; errors
+ * are transactional (logits, the `seen` scratch and the sampling state are
+ * left untouched and no draw is consumed).  The host keeps the xorshift64*
+ * generator; devices only ever see 24-bit uniforms.
+ *
+ * Entry points:
+ *   - host single-row drop-ins (pointers to host memory, one GPU call each):
+ *     pb_sample_token_with_repetition, pb_sample_token, pb_greedy_token,
+ *     pb_top_logits_8;
+ *   - batched device entry points (pointers to device memory, asynchronous on
+ *     the given HIP stream): pb_sample_batch, pb_sample_batch_inplace;
+ *   - host PRNG helpers: pb_sampling_state_new, pb_next_24, pb_fill_random_24.
+ */
+#ifndef PBSAMPLE_H
+#define PBSAMPLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PB_VOCAB 151936u                   /* LOGIT_WORDS, inference.rs:16 */
+#define PB_TOP_K 20u                       /* SAMPLING_TOP_K, inference.rs:20 */
+#define PB_SEEN_BYTES ((PB_VOCAB + 7u) / 8u) /* 18,992 */
+#define PB_SAMPLING_TEMPERATURE_MILLI 700u /* inference.rs:19 */
+#define PB_SAMPLING_TOP_P_MILLI 800u       /* inference.rs:21 */
+#define PB_SAMPLING_REPETITION_PENALTY_MILLI 1100u /* inference.rs:22 */
+#define PB_SAMPLING_POLICY "temperature_0p7_top_k_20_top_p_0p8_repetition_penalty_1p1"
+#define PB_NO_LAYER 0xffffffffu
+#define PB_NO_TENSOR 0xffffffffu
+#define PB_NO_TOKEN 0xffffffffu
+
+/* InferenceStatus (inference.rs:155-169). */
+enum pb_status {
+  PB_OK = 0, PB_STATE = 1, PB_CONTEXT = 2, PB_TOKEN_ID = 3, PB_CAPACITY = 4,
+  PB_ALIGNMENT = 5, PB_NONFINITE_INPUT = 6, PB_NONFINITE_OUTPUT = 7, PB_MODEL = 8,
+  PB_ARITHMETIC = 9, PB_FAULTED = 10,
+  /* Not in the reference: the HIP runtime failed (no device, launch error). */
+  PB_DEVICE = 0x100
+};
+/* InferenceDomain values used by the sampler (inference.rs:171-194). */
+enum pb_domain { PB_DOMAIN_NONE = 0, PB_DOMAIN_LOGITS = 18, PB_DOMAIN_ARGMAX = 19 };
+/* InferenceFieldKind values used by the sampler (inference.rs:196-212). */
+enum pb_field_kind {
+  PB_FIELD_NONE = 0, PB_FIELD_TOKEN = 2, PB_FIELD_BYTES = 4, PB_FIELD_ALIGNMENT = 5,
+  PB_FIELD_FINITE = 7, PB_FIELD_LOGITS = 12
+};
+
+/* SamplingState (inference.rs:772-776): 16 bytes, repr(C). */
+typedef struct pb_sampling_state {
+  uint64_t state;
+  uint64_t draws;
+} pb_sampling_state;
+
+/* InferenceError (inference.rs:226-237): 48 bytes, detail = kind << 32 | sub. */
+typedef struct pb_inference_error {
+  uint32_t status, domain, layer, position, tensor_id, reserved;
+  uint64_t needed, available, detail;
+} pb_inference_error;
+
+/* TopLogit (inference.rs:767-770). */
+typedef struct pb_top_logit {
+  uint32_t token;
+  uint32_t logit_bits;
+} pb_top_logit;
+
+/* Per-row evidence beside each draw.  Not in the reference (it returns only the
+ * token): the top-20 in rank order, their penalised logits and softmax
+ * weights, the kept-survivor probabilities w[i]/kept_total (0 past `kept`),
+ * the top-p survivor count, the drawn rank and boundary flags
+ * (PB_FLAG_*).  On a row error every byte is 0xff. */
+typedef struct pb_sample_detail {
+  uint32_t ids[PB_TOP_K];
+  uint32_t value_bits[PB_TOP_K];
+  uint32_t weight_bits[PB_TOP_K];
+  float probs[PB_TOP_K];
+  uint32_t kept;
+  uint32_t rank;
+  uint32_t flags;
+  uint32_t token;
+} pb_sample_detail;
+
+#define PB_FLAG_DRAW_BOUNDARY 1u   /* target within 1e-6 * kept_total of a CDF step */
+#define PB_FLAG_CUTOFF_BOUNDARY 2u /* top-p cutoff within 1e-6 * total of a prefix */
+
+/* ---- host PRNG (inference.rs:779-810) ---- */
+
+/* SamplingState::new: seed 0 is replaced by 0x9e3779b97f4a7c15. */
+void pb_sampling_state_new(pb_sampling_state *state, uint64_t seed);
+/* SamplingState::next_24 (crate-private in the reference): one xorshift64*
+ * step, draws += 1, returns the top 24 bits of the scrambled state. */
+uint32_t pb_next_24(pb_sampling_state *state);
+/* One next_24 per row: out[i] = pb_next_24(&states[i]). */
+void pb_fill_random_24(pb_sampling_state *states, uint32_t rows, uint32_t *out);
+
+/* ---- single-row drop-ins (host memory, synchronous) ----
+ * They run on the library's default context (the current HIP device).  The
+ * logits row, history and (for the drop-in with repetition) the penalised
+ * write-back are staged through pinned buffers; all selection arithmetic runs
+ * on the GPU.  Returns the InferenceStatus; *err is always written. */
+
+/* sample_token_with_repetition (inference.rs:919-965).  On success `logits`
+ * holds the penalised row (once per unique history id, in place), `seen` is
+ * returned with the history bits cleared, the state advanced by one draw. */
+uint32_t pb_sample_token_with_repetition(uint32_t *logits, size_t logits_len,
+                                         const uint32_t *tokens, size_t tokens_len,
+                                         uint8_t *seen, size_t seen_len,
+                                         pb_sampling_state *state, uint32_t *out_token,
+                                         pb_inference_error *err);
+
+/* sample_token (inference.rs:914-917): no penalty; logits are not modified. */
+uint32_t pb_sample_token(const uint32_t *logits, size_t logits_len, pb_sampling_state *state,
+                         uint32_t *out_token, pb_inference_error *err);
+
+/* greedy_token (inference.rs:861-881): argmax, lowest id on ties. */
+uint32_t pb_greedy_token(const uint32_t *logits, size_t logits_len, uint32_t *out_token,
+                         pb_inference_error *err);
+
+/* top_logits_8 (inference.rs:814-859): output untouched on error. */
+uint32_t pb_top_logits_8(const uint32_t *logits, size_t logits_len, pb_top_logit output[8],
+                         pb_inference_error *err);
+
+/* ---- batched device sampler ---- */
+
+typedef struct pb_context pb_context;
+
+/* Creates a context on `device` (-1 = current device).  The context owns the
+ * inter-kernel workspace and the staging buffers of the drop-ins. */
+uint32_t pb_context_create(int device, pb_context **out);
+void pb_context_destroy(pb_context *ctx);
+
+/*
+ * Samples `rows` independent rows.  All pointers are device pointers; the
+ * call only enqueues work on `stream` (a hipStream_t, NULL = default stream).
+ *
+ *   d_logits     rows x ld binary32 words; vocab must be PB_VOCAB; ld >= vocab,
+ *                ld % 4 == 0, 16-byte aligned.  Not modified.
+ *   d_hist       rows x hist_ld token ids (may be NULL when every length is 0),
+ *   d_hist_len   valid ids per row (NULL = 0); lengths above hist_ld are clamped.
+ *   d_random_24  one next_24 value per row (the host advanced one
+ *                SamplingState per row; only the low 24 bits are used).
+ *   d_token      out: selected id, PB_NO_TOKEN on a row error.
+ *   d_detail     out (optional): pb_sample_detail per row.
+ *   d_err        out (optional): pb_inference_error per row (all-zero on success).
+ *
+ * Row semantics are sample_token_with_repetition's: non-finite logit ->
+ * NONFINITE_OUTPUT (first index), else history id >= vocab -> TOKEN_ID (first
+ * position), else penalty + top-k/top-p draw.  A failing row consumes no
+ * draw: the caller restores that row's SamplingState.
+ * Returns PB_OK when the work was enqueued, else a status with *err filled
+ * (err may be NULL) and nothing enqueued.
+ */
+uint32_t pb_sample_batch(pb_context *ctx, const uint32_t *d_logits, size_t vocab, size_t ld,
+                         uint32_t rows, const uint32_t *d_hist, size_t hist_ld,
+                         const uint32_t *d_hist_len, const uint32_t *d_random_24,
+                         uint32_t *d_token, pb_sample_detail *d_detail,
+                         pb_inference_error *d_err, void *stream, pb_inference_error *err);
+
+/* As pb_sample_batch, then applies the repetition penalty in place to every
+ * successful row (once per unique history id), as the reference mutates the
+ * caller's logits (fp32_sse2.rs:1848-1876).  d_seen (optional, rows x
+ * PB_SEEN_BYTES) is the per-row `seen` scratch: ids whose bit is already set
+ * are not penalised (the reference's dedupe), and the history bits are
+ * cleared on success rows. */
+uint32_t pb_sample_batch_inplace(pb_context *ctx, uint32_t *d_logits, size_t vocab, size_t ld,
+                                 uint32_t rows, const uint32_t *d_hist, size_t hist_ld,
+                                 const uint32_t *d_hist_len, const uint32_t *d_random_24,
+                                 uint8_t *d_seen, uint32_t *d_token,
+                                 pb_sample_detail *d_detail, pb_inference_error *d_err,
+                                 void *stream, pb_inference_error *err);
+
+/* Segments per row the batched sampler will use for `rows` (diagnostic). */
+uint32_t pb_segments_for_rows(uint32_t rows);
+
+/* Forces the number of row slices of this context's batched calls (0 = auto,
+ * otherwise clamped to 1..64).  For tuning and for testing both the
+ * single-workgroup and the multi-slice paths on the same rows. */
+void pb_context_set_segments(pb_context *ctx, uint32_t segments);
+
+/* ---- device arithmetic probes (verification hooks, no reference
+ * counterpart): evaluate, on the GPU, the exact binary32 routines the sampler
+ * uses, n words each, enqueued on `stream`:
+ *   expf:     the restated libm expf (fp32_sse2.rs:404-469)
+ *   penalize: the repetition penalty of one logit (fp32_sse2.rs:1860-1866) */
+uint32_t pb_device_expf_bits(const uint32_t *d_in, uint32_t *d_out, size_t n, void *stream);
+uint32_t pb_device_penalize_bits(const uint32_t *d_in, uint32_t *d_out, size_t n, void *stream);
+
+/* Library version string and build target ("gfx950"). */
+const char *pb_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PBSAMPLE_H */

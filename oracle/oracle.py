@@ -103,6 +103,8 @@ def lib() -> ctypes.CDLL:
         L.pbo_top_logits_8.argtypes = [vp, size_t, vp, ctypes.POINTER(Error)]
         L.pbo_sample_batch.argtypes = [vp, size_t, size_t, u32, vp, size_t, vp, vp,
                                        vp, vp, vp, vp, ctypes.c_int]
+        L.pbo_expf_array.argtypes = [vp, vp, size_t]
+        L.pbo_penalize_array.argtypes = [vp, vp, size_t]
         for name in ("pbo_sizeof_detail", "pbo_sizeof_error", "pbo_sizeof_state"):
             getattr(L, name).restype = size_t
         assert L.pbo_sizeof_detail() == DETAIL_DTYPE.itemsize
@@ -151,6 +153,21 @@ class SamplingState:
 
 def expf_bits(x: int) -> int:
     return lib().pbo_expf_bits(x & 0xFFFFFFFF)
+
+
+def expf_array(words) -> np.ndarray:
+    a = _u32(words)
+    out = np.empty_like(a)
+    lib().pbo_expf_array(_ptr(a), _ptr(out), a.size)
+    return out
+
+
+def penalize_array(words) -> np.ndarray:
+    """Repetition penalty of each word as a lone history id."""
+    a = _u32(words)
+    out = np.empty_like(a)
+    lib().pbo_penalize_array(_ptr(a), _ptr(out), a.size)
+    return out
 
 
 def apply_repetition_penalty(logits: np.ndarray, tokens, seen: np.ndarray) -> None:

@@ -572,6 +572,26 @@ int pbo_sample_batch(const uint32_t *logits, size_t ld, size_t vocab, uint32_t r
     return 0;
 }
 
+/* Element-wise restated expf / single-logit penalty over arrays (checkers
+ * for the device arithmetic). */
+void pbo_expf_array(const uint32_t *in, uint32_t *out, size_t n) {
+    const unsigned int saved = enter_fp();
+    for (size_t i = 0; i < n; ++i) out[i] = bf(expf_ref(fb(in[i])));
+    exit_fp(saved);
+}
+
+void pbo_penalize_array(const uint32_t *in, uint32_t *out, size_t n) {
+    const unsigned int saved = enter_fp();
+    for (size_t i = 0; i < n; ++i) {
+        uint32_t word = in[i];
+        uint8_t seen = 0;
+        const uint32_t token = 0;
+        apply_repetition_penalty(&word, &token, 1, &seen);
+        out[i] = word;
+    }
+    exit_fp(saved);
+}
+
 /* Layout probes so the Python side can check struct sizes. */
 size_t pbo_sizeof_detail(void) { return sizeof(pbo_detail); }
 size_t pbo_sizeof_error(void) { return sizeof(pbo_error); }

@@ -1,0 +1,530 @@
+// pb_api.cpp -- C ABI of the gfx950 decode-step sampler (include/pbsample.h).
+//
+// Host side of the drop-in.  Mirrors promptboot's sampler API
+// (crates/promptboot-core/src/inference.rs:737-965): argument meaning, error
+// tuples, error precedence (length, non-finite, scratch length, history ids)
+// and transactional failure (no mutation, no draw).  The selection itself
+// always runs on the GPU; there is no host fallback.
+#include <hip/hip_runtime.h>
+#include <string.h>
+
+#include <map>
+#include <mutex>
+
+#include "pb_internal.h"
+#include "pbsample.h"
+
+namespace {
+
+constexpr size_t kRowBytes = (size_t)PB_VOCAB * 4;
+
+void set_error(pb_inference_error* e, uint32_t status, uint32_t domain, uint64_t needed,
+               uint64_t available, uint32_t kind, uint32_t sub) {
+  if (!e) return;
+  e->status = status;
+  e->domain = domain;
+  e->layer = PB_NO_LAYER;
+  e->position = 0;
+  e->tensor_id = PB_NO_TENSOR;
+  e->reserved = 0;
+  e->needed = needed;
+  e->available = available;
+  e->detail = ((uint64_t)kind << 32) | sub;
+}
+
+void clear_error(pb_inference_error* e) {
+  if (e) memset(e, 0, sizeof *e);
+}
+
+uint32_t device_error(pb_inference_error* e, hipError_t code) {
+  set_error(e, PB_DEVICE, PB_DOMAIN_NONE, 0, (uint64_t)code, PB_FIELD_NONE, 0);
+  return PB_DEVICE;
+}
+
+// Restores the caller's current device on scope exit.
+struct DeviceGuard {
+  int saved = -1;
+  explicit DeviceGuard(int device) {
+    if (hipGetDevice(&saved) != hipSuccess) saved = -1;
+    if (device >= 0 && device != saved) (void)hipSetDevice(device);
+  }
+  ~DeviceGuard() {
+    int now = -1;
+    if (saved >= 0 && hipGetDevice(&now) == hipSuccess && now != saved) (void)hipSetDevice(saved);
+  }
+};
+
+}  // namespace
+
+struct pb_context {
+  int device = 0;
+  hipStream_t stream = nullptr;  // used by the single-row drop-ins
+  std::mutex mu;                 // serialises the drop-ins on this context
+
+  uint32_t forced_segments = 0;  // 0 = automatic slices per row
+  void* d_work = nullptr;  // inter-kernel workspace (segment top-20 lists)
+  size_t work_bytes = 0;
+
+  // single-row staging
+  uint32_t* d_row = nullptr;
+  uint32_t* d_hist = nullptr;
+  uint32_t* d_gather = nullptr;
+  size_t hist_cap = 0;
+  uint32_t* d_small = nullptr;  // [0] history length, [1] uniform, [2] token
+  pb_sample_detail* d_detail = nullptr;
+  pb_inference_error* d_err = nullptr;
+  uint8_t* d_seen = nullptr;
+  uint32_t* h_row = nullptr;    // pinned
+  uint32_t* h_hist = nullptr;   // pinned
+  uint32_t* h_gather = nullptr; // pinned
+  uint32_t* h_small = nullptr;  // pinned
+  pb_sample_detail* h_detail = nullptr;
+  pb_inference_error* h_err = nullptr;
+  uint8_t* h_seen = nullptr;
+};
+
+static hipError_t ensure_workspace(pb_context* ctx, size_t bytes) {
+  if (bytes <= ctx->work_bytes) return hipSuccess;
+  if (ctx->d_work) {
+    hipError_t e = hipFree(ctx->d_work);  // device-synchronising: no launch still reads it
+    ctx->d_work = nullptr;
+    ctx->work_bytes = 0;
+    if (e != hipSuccess) return e;
+  }
+  hipError_t e = hipMalloc(&ctx->d_work, bytes);
+  if (e == hipSuccess) ctx->work_bytes = bytes;
+  return e;
+}
+
+static hipError_t ensure_hist_capacity(pb_context* ctx, size_t ids) {
+  if (ids <= ctx->hist_cap) return hipSuccess;
+  size_t cap = ctx->hist_cap ? ctx->hist_cap : 1024;
+  while (cap < ids) cap *= 2;
+  if (ctx->d_hist) (void)hipFree(ctx->d_hist);
+  if (ctx->d_gather) (void)hipFree(ctx->d_gather);
+  if (ctx->h_hist) (void)hipHostFree(ctx->h_hist);
+  if (ctx->h_gather) (void)hipHostFree(ctx->h_gather);
+  ctx->d_hist = ctx->d_gather = ctx->h_hist = ctx->h_gather = nullptr;
+  ctx->hist_cap = 0;
+  hipError_t e;
+  if ((e = hipMalloc(&ctx->d_hist, cap * 4)) != hipSuccess) return e;
+  if ((e = hipMalloc(&ctx->d_gather, cap * 4)) != hipSuccess) return e;
+  if ((e = hipHostMalloc(&ctx->h_hist, cap * 4, hipHostMallocDefault)) != hipSuccess) return e;
+  if ((e = hipHostMalloc(&ctx->h_gather, cap * 4, hipHostMallocDefault)) != hipSuccess) return e;
+  ctx->hist_cap = cap;
+  return hipSuccess;
+}
+
+static void release(pb_context* ctx) {
+  if (!ctx) return;
+  DeviceGuard guard(ctx->device);
+  if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+  void* dev[] = {ctx->d_work, ctx->d_row, ctx->d_hist, ctx->d_gather, ctx->d_small,
+                 ctx->d_detail, ctx->d_err, ctx->d_seen};
+  for (void* p : dev)
+    if (p) (void)hipFree(p);
+  void* host[] = {ctx->h_row, ctx->h_hist, ctx->h_gather, ctx->h_small, ctx->h_detail,
+                  ctx->h_err, ctx->h_seen};
+  for (void* p : host)
+    if (p) (void)hipHostFree(p);
+  if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
+  delete ctx;
+}
+
+extern "C" {
+
+// ---- PRNG: xorshift64* with draw counter (inference.rs:779-810) ----
+
+void pb_sampling_state_new(pb_sampling_state* state, uint64_t seed) {
+  state->state = seed == 0 ? 0x9e3779b97f4a7c15ull : seed;
+  state->draws = 0;
+}
+
+uint32_t pb_next_24(pb_sampling_state* state) {
+  uint64_t v = state->state;
+  v ^= v >> 12;
+  v ^= v << 25;
+  v ^= v >> 27;
+  state->state = v;
+  state->draws += 1;
+  return (uint32_t)((v * 0x2545f4914f6cdd1dull) >> 40);
+}
+
+void pb_fill_random_24(pb_sampling_state* states, uint32_t rows, uint32_t* out) {
+  for (uint32_t r = 0; r < rows; ++r) out[r] = pb_next_24(&states[r]);
+}
+
+const char* pb_version(void) { return "pbsample 0.1 gfx950"; }
+
+uint32_t pb_segments_for_rows(uint32_t rows) {
+  uint32_t segs = 0, seg_f4 = 0;
+  pb::plan_segments(rows, 0, &segs, &seg_f4);
+  return segs;
+}
+
+void pb_context_set_segments(pb_context* ctx, uint32_t segments) {
+  ctx->forced_segments = segments > 64 ? 64 : segments;
+}
+
+uint32_t pb_device_expf_bits(const uint32_t* d_in, uint32_t* d_out, size_t n, void* stream) {
+  return pb::launch_probe(0, d_in, d_out, n, static_cast<hipStream_t>(stream)) == hipSuccess
+             ? PB_OK
+             : PB_DEVICE;
+}
+
+uint32_t pb_device_penalize_bits(const uint32_t* d_in, uint32_t* d_out, size_t n, void* stream) {
+  return pb::launch_probe(1, d_in, d_out, n, static_cast<hipStream_t>(stream)) == hipSuccess
+             ? PB_OK
+             : PB_DEVICE;
+}
+
+uint32_t pb_context_create(int device, pb_context** out) {
+  *out = nullptr;
+  if (device < 0 && hipGetDevice(&device) != hipSuccess) return PB_DEVICE;
+  DeviceGuard guard(device);
+  pb_context* ctx = new pb_context();
+  ctx->device = device;
+  hipError_t e = hipSuccess;
+  if (e == hipSuccess) e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
+  if (e == hipSuccess) e = hipMalloc(&ctx->d_row, kRowBytes);
+  if (e == hipSuccess) e = hipMalloc(&ctx->d_small, 16);
+  if (e == hipSuccess) e = hipMalloc(&ctx->d_detail, sizeof(pb_sample_detail));
+  if (e == hipSuccess) e = hipMalloc(&ctx->d_err, sizeof(pb_inference_error));
+  if (e == hipSuccess) e = hipMalloc(&ctx->d_seen, PB_SEEN_BYTES);
+  if (e == hipSuccess) e = hipHostMalloc(&ctx->h_row, kRowBytes, hipHostMallocDefault);
+  if (e == hipSuccess) e = hipHostMalloc(&ctx->h_small, 16, hipHostMallocDefault);
+  if (e == hipSuccess)
+    e = hipHostMalloc(&ctx->h_detail, sizeof(pb_sample_detail), hipHostMallocDefault);
+  if (e == hipSuccess)
+    e = hipHostMalloc(&ctx->h_err, sizeof(pb_inference_error), hipHostMallocDefault);
+  if (e == hipSuccess) e = hipHostMalloc(&ctx->h_seen, PB_SEEN_BYTES, hipHostMallocDefault);
+  if (e == hipSuccess) e = ensure_hist_capacity(ctx, 4096);
+  if (e != hipSuccess) {
+    release(ctx);
+    return PB_DEVICE;
+  }
+  *out = ctx;
+  return PB_OK;
+}
+
+void pb_context_destroy(pb_context* ctx) { release(ctx); }
+
+}  // extern "C"
+
+// Validates and enqueues one batched sample (both variants).
+static uint32_t enqueue_sample(pb_context* ctx, const uint32_t* d_logits, size_t vocab, size_t ld,
+                               uint32_t rows, const uint32_t* d_hist, size_t hist_ld,
+                               const uint32_t* d_hist_len, const uint32_t* d_random_24,
+                               const uint8_t* d_excl, uint32_t* d_token,
+                               pb_sample_detail* d_detail, pb_inference_error* d_err,
+                               hipStream_t stream, pb_inference_error* err) {
+  clear_error(err);
+  if (vocab != PB_VOCAB) {
+    // logits_error (inference.rs:737-754)
+    set_error(err, PB_CAPACITY, PB_DOMAIN_LOGITS, PB_VOCAB, vocab, PB_FIELD_LOGITS, 0);
+    return PB_CAPACITY;
+  }
+  if (ld < vocab) {
+    set_error(err, PB_CAPACITY, PB_DOMAIN_LOGITS, vocab, ld, PB_FIELD_LOGITS, 1);
+    return PB_CAPACITY;
+  }
+  if ((ld & 3u) != 0 || ((uintptr_t)d_logits & 15u) != 0) {
+    set_error(err, PB_ALIGNMENT, PB_DOMAIN_LOGITS, 16, ((uintptr_t)d_logits & 15u) | (ld & 3u),
+              PB_FIELD_ALIGNMENT, 0);
+    return PB_ALIGNMENT;
+  }
+  if (rows == 0) return PB_OK;
+  if (d_logits == nullptr || d_random_24 == nullptr || d_token == nullptr ||
+      (d_hist_len != nullptr && d_hist == nullptr)) {
+    set_error(err, PB_CAPACITY, PB_DOMAIN_ARGMAX, 1, 0, PB_FIELD_BYTES, 3);
+    return PB_CAPACITY;
+  }
+  pb::RowParams p;
+  p.logits = d_logits;
+  p.ld = ld;
+  p.rows = rows;
+  p.hist = d_hist_len ? d_hist : nullptr;
+  p.hist_ld = hist_ld;
+  p.hist_len = d_hist_len;
+  p.excl = d_excl;
+  p.random_24 = d_random_24;
+  p.token = d_token;
+  p.detail = d_detail;
+  p.err = d_err;
+  p.hist_vec4 = (p.hist != nullptr && (hist_ld & 3u) == 0 && ((uintptr_t)d_hist & 15u) == 0);
+  pb::plan_segments(rows, ctx->forced_segments, &p.segs, &p.seg_f4);
+  p.part_keys = nullptr;
+  p.part_meta = nullptr;
+  DeviceGuard guard(ctx->device);
+  if (p.segs > 1) {
+    const size_t slots = (size_t)rows * p.segs;
+    const size_t key_bytes = slots * PB_TOP_K * 8;
+    hipError_t e = ensure_workspace(ctx, key_bytes + slots * 8);
+    if (e != hipSuccess) return device_error(err, e);
+    p.part_keys = static_cast<uint64_t*>(ctx->d_work);
+    p.part_meta = reinterpret_cast<uint32_t*>(static_cast<char*>(ctx->d_work) + key_bytes);
+  }
+  hipError_t e = pb::launch_sample(p, stream);
+  if (e != hipSuccess) return device_error(err, e);
+  return PB_OK;
+}
+
+extern "C" {
+
+uint32_t pb_sample_batch(pb_context* ctx, const uint32_t* d_logits, size_t vocab, size_t ld,
+                         uint32_t rows, const uint32_t* d_hist, size_t hist_ld,
+                         const uint32_t* d_hist_len, const uint32_t* d_random_24,
+                         uint32_t* d_token, pb_sample_detail* d_detail,
+                         pb_inference_error* d_err, void* stream, pb_inference_error* err) {
+  return enqueue_sample(ctx, d_logits, vocab, ld, rows, d_hist, hist_ld, d_hist_len, d_random_24,
+                        nullptr, d_token, d_detail, d_err, static_cast<hipStream_t>(stream), err);
+}
+
+uint32_t pb_sample_batch_inplace(pb_context* ctx, uint32_t* d_logits, size_t vocab, size_t ld,
+                                 uint32_t rows, const uint32_t* d_hist, size_t hist_ld,
+                                 const uint32_t* d_hist_len, const uint32_t* d_random_24,
+                                 uint8_t* d_seen, uint32_t* d_token,
+                                 pb_sample_detail* d_detail, pb_inference_error* d_err,
+                                 void* stream, pb_inference_error* err) {
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  uint32_t st = enqueue_sample(ctx, d_logits, vocab, ld, rows, d_hist, hist_ld, d_hist_len,
+                               d_random_24, d_seen, d_token, d_detail, d_err, s, err);
+  if (st != PB_OK || rows == 0 || d_hist_len == nullptr) return st;
+  pb::WritebackParams w;
+  w.logits = d_logits;
+  w.ld = ld;
+  w.rows = rows;
+  w.hist = d_hist;
+  w.hist_ld = hist_ld;
+  w.hist_len = d_hist_len;
+  w.seen = d_seen;
+  w.token = d_token;
+  w.gather = nullptr;
+  DeviceGuard guard(ctx->device);
+  hipError_t e = pb::launch_writeback(w, s);
+  if (e != hipSuccess) return device_error(err, e);
+  return PB_OK;
+}
+
+}  // extern "C"
+
+// ---- single-row drop-ins on the default context ----
+
+static std::mutex g_contexts_mu;
+static std::map<int, pb_context*> g_contexts;
+
+static pb_context* default_context(pb_inference_error* err) {
+  int device = 0;
+  hipError_t e = hipGetDevice(&device);
+  if (e != hipSuccess) {
+    device_error(err, e);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_contexts_mu);
+  auto it = g_contexts.find(device);
+  if (it != g_contexts.end()) return it->second;
+  pb_context* ctx = nullptr;
+  if (pb_context_create(device, &ctx) != PB_OK) {
+    set_error(err, PB_DEVICE, PB_DOMAIN_NONE, 0, 0, PB_FIELD_NONE, 1);
+    return nullptr;
+  }
+  g_contexts[device] = ctx;
+  return ctx;
+}
+
+enum RowMode { kSample = 0, kSampleWithHistory = 1 };
+
+// Runs one row through the batched kernels on the context's own stream.
+// Fills ctx->h_small[2] (token), ctx->h_detail and ctx->h_err; when
+// `history` is non-null also the penalised write-back values in h_gather and,
+// with `seen_dirty`, the updated scratch in h_seen.
+static uint32_t run_single_row(pb_context* ctx, const uint32_t* logits, const uint32_t* history,
+                               size_t history_len, const uint8_t* seen, bool seen_dirty,
+                               uint32_t random_24, pb_inference_error* err) {
+  DeviceGuard guard(ctx->device);
+  hipStream_t s = ctx->stream;
+  hipError_t e;
+  memcpy(ctx->h_row, logits, kRowBytes);
+  if ((e = hipMemcpyAsync(ctx->d_row, ctx->h_row, kRowBytes, hipMemcpyHostToDevice, s)) !=
+      hipSuccess)
+    return device_error(err, e);
+  if (history) {
+    if ((e = ensure_hist_capacity(ctx, history_len ? history_len : 1)) != hipSuccess)
+      return device_error(err, e);
+    if (history_len) {
+      memcpy(ctx->h_hist, history, history_len * 4);
+      if ((e = hipMemcpyAsync(ctx->d_hist, ctx->h_hist, history_len * 4, hipMemcpyHostToDevice,
+                              s)) != hipSuccess)
+        return device_error(err, e);
+    }
+    if (seen_dirty) {
+      memcpy(ctx->h_seen, seen, PB_SEEN_BYTES);
+      if ((e = hipMemcpyAsync(ctx->d_seen, ctx->h_seen, PB_SEEN_BYTES, hipMemcpyHostToDevice,
+                              s)) != hipSuccess)
+        return device_error(err, e);
+    }
+  }
+  ctx->h_small[0] = (uint32_t)history_len;
+  ctx->h_small[1] = random_24;
+  if ((e = hipMemcpyAsync(ctx->d_small, ctx->h_small, 8, hipMemcpyHostToDevice, s)) != hipSuccess)
+    return device_error(err, e);
+
+  const bool with_hist = history != nullptr && history_len > 0;
+  uint8_t* seen_dev = seen_dirty ? ctx->d_seen : nullptr;
+  pb_inference_error enqueue_err;
+  uint32_t st = enqueue_sample(ctx, ctx->d_row, PB_VOCAB, PB_VOCAB, 1,
+                               with_hist ? ctx->d_hist : nullptr, ctx->hist_cap,
+                               with_hist ? ctx->d_small : nullptr, ctx->d_small + 1, seen_dev,
+                               ctx->d_small + 2, ctx->d_detail, ctx->d_err, s, &enqueue_err);
+  if (st != PB_OK) {
+    if (err) *err = enqueue_err;
+    return st;
+  }
+  if (with_hist) {
+    pb::WritebackParams w;
+    w.logits = ctx->d_row;
+    w.ld = PB_VOCAB;
+    w.rows = 1;
+    w.hist = ctx->d_hist;
+    w.hist_ld = ctx->hist_cap;
+    w.hist_len = ctx->d_small;
+    w.seen = seen_dev;
+    w.token = ctx->d_small + 2;
+    w.gather = ctx->d_gather;
+    if ((e = pb::launch_writeback(w, s)) != hipSuccess) return device_error(err, e);
+    if ((e = hipMemcpyAsync(ctx->h_gather, ctx->d_gather, history_len * 4, hipMemcpyDeviceToHost,
+                            s)) != hipSuccess)
+      return device_error(err, e);
+    if (seen_dirty &&
+        (e = hipMemcpyAsync(ctx->h_seen, ctx->d_seen, PB_SEEN_BYTES, hipMemcpyDeviceToHost, s)) !=
+            hipSuccess)
+      return device_error(err, e);
+  }
+  if ((e = hipMemcpyAsync(ctx->h_small + 2, ctx->d_small + 2, 4, hipMemcpyDeviceToHost, s)) !=
+          hipSuccess ||
+      (e = hipMemcpyAsync(ctx->h_detail, ctx->d_detail, sizeof(pb_sample_detail),
+                          hipMemcpyDeviceToHost, s)) != hipSuccess ||
+      (e = hipMemcpyAsync(ctx->h_err, ctx->d_err, sizeof(pb_inference_error),
+                          hipMemcpyDeviceToHost, s)) != hipSuccess)
+    return device_error(err, e);
+  if ((e = hipStreamSynchronize(s)) != hipSuccess) return device_error(err, e);
+  return PB_OK;
+}
+
+static bool any_nonzero(const uint8_t* p, size_t n) {
+  for (size_t i = 0; i < n; ++i)
+    if (p[i]) return true;
+  return false;
+}
+
+extern "C" {
+
+uint32_t pb_sample_token_with_repetition(uint32_t* logits, size_t logits_len,
+                                         const uint32_t* tokens, size_t tokens_len,
+                                         uint8_t* seen, size_t seen_len,
+                                         pb_sampling_state* state, uint32_t* out_token,
+                                         pb_inference_error* err) {
+  clear_error(err);
+  if (logits_len != PB_VOCAB) {
+    set_error(err, PB_CAPACITY, PB_DOMAIN_LOGITS, PB_VOCAB, logits_len, PB_FIELD_LOGITS, 0);
+    return PB_CAPACITY;
+  }
+  pb_context* ctx = default_context(err);
+  if (!ctx) return PB_DEVICE;
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  const bool seen_ok = seen_len >= PB_SEEN_BYTES;
+  const bool seen_dirty = seen_ok && any_nonzero(seen, PB_SEEN_BYTES);
+  pb_sampling_state next = *state;
+  const uint32_t r24 = pb_next_24(&next);
+  // The history goes to the GPU even when `seen` is short: a non-finite logit
+  // takes precedence over the scratch-length error (inference.rs:925-938).
+  uint32_t st = run_single_row(ctx, logits, tokens, tokens_len, seen, seen_dirty, r24, err);
+  if (st != PB_OK) return st;
+  const pb_inference_error& row_err = *ctx->h_err;
+  if (row_err.status == PB_NONFINITE_OUTPUT) {
+    if (err) *err = row_err;
+    return row_err.status;
+  }
+  if (!seen_ok) {
+    set_error(err, PB_CAPACITY, PB_DOMAIN_ARGMAX, PB_SEEN_BYTES, seen_len, PB_FIELD_BYTES, 2);
+    return PB_CAPACITY;
+  }
+  if (row_err.status != PB_OK) {
+    if (err) *err = row_err;
+    return row_err.status;
+  }
+  // success: publish the in-place penalty, the cleared scratch and the draw
+  for (size_t q = 0; q < tokens_len; ++q) logits[tokens[q]] = ctx->h_gather[q];
+  if (seen_dirty) memcpy(seen, ctx->h_seen, PB_SEEN_BYTES);
+  *state = next;
+  *out_token = ctx->h_small[2];
+  return PB_OK;
+}
+
+uint32_t pb_sample_token(const uint32_t* logits, size_t logits_len, pb_sampling_state* state,
+                         uint32_t* out_token, pb_inference_error* err) {
+  clear_error(err);
+  if (logits_len != PB_VOCAB) {
+    set_error(err, PB_CAPACITY, PB_DOMAIN_LOGITS, PB_VOCAB, logits_len, PB_FIELD_LOGITS, 0);
+    return PB_CAPACITY;
+  }
+  pb_context* ctx = default_context(err);
+  if (!ctx) return PB_DEVICE;
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  pb_sampling_state next = *state;
+  const uint32_t r24 = pb_next_24(&next);
+  uint32_t st = run_single_row(ctx, logits, nullptr, 0, nullptr, false, r24, err);
+  if (st != PB_OK) return st;
+  if (ctx->h_err->status != PB_OK) {
+    if (err) *err = *ctx->h_err;
+    return ctx->h_err->status;
+  }
+  *state = next;
+  *out_token = ctx->h_small[2];
+  return PB_OK;
+}
+
+uint32_t pb_greedy_token(const uint32_t* logits, size_t logits_len, uint32_t* out_token,
+                         pb_inference_error* err) {
+  clear_error(err);
+  if (logits_len != PB_VOCAB) {
+    set_error(err, PB_CAPACITY, PB_DOMAIN_LOGITS, PB_VOCAB, logits_len, PB_FIELD_LOGITS, 0);
+    return PB_CAPACITY;
+  }
+  pb_context* ctx = default_context(err);
+  if (!ctx) return PB_DEVICE;
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  uint32_t st = run_single_row(ctx, logits, nullptr, 0, nullptr, false, 0, err);
+  if (st != PB_OK) return st;
+  if (ctx->h_err->status != PB_OK) {
+    if (err) *err = *ctx->h_err;
+    return ctx->h_err->status;
+  }
+  *out_token = ctx->h_detail->ids[0];
+  return PB_OK;
+}
+
+uint32_t pb_top_logits_8(const uint32_t* logits, size_t logits_len, pb_top_logit output[8],
+                         pb_inference_error* err) {
+  clear_error(err);
+  if (logits_len != PB_VOCAB) {
+    set_error(err, PB_CAPACITY, PB_DOMAIN_LOGITS, PB_VOCAB, logits_len, PB_FIELD_LOGITS, 0);
+    return PB_CAPACITY;
+  }
+  pb_context* ctx = default_context(err);
+  if (!ctx) return PB_DEVICE;
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  uint32_t st = run_single_row(ctx, logits, nullptr, 0, nullptr, false, 0, err);
+  if (st != PB_OK) return st;
+  if (ctx->h_err->status != PB_OK) {
+    if (err) *err = *ctx->h_err;
+    return ctx->h_err->status;
+  }
+  for (int i = 0; i < 8; ++i) {
+    output[i].token = ctx->h_detail->ids[i];
+    output[i].logit_bits = ctx->h_detail->value_bits[i];
+  }
+  return PB_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,223 @@
+// pb_device.h -- device-side building blocks of the gfx950 decode-step sampler.
+//
+// Arithmetic contract: every binary32/binary64 operation here is a single
+// IEEE-754 operation rounded to nearest-even with denormals preserved, in the
+// same order as promptboot's scalar SSE2 sampler (crates/promptboot-core/src/
+// fp32_sse2.rs:147-345 for the ops, :848-867 for the MXCSR 0x1f80 scope).
+// The file is compiled with -ffp-contract=off and declares
+// `#pragma clang fp contract(off)` so no multiply-add is ever fused, and
+// fp32 division uses the correctly rounded expansion (HIP's default).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#pragma clang fp contract(off)
+
+namespace pb {
+
+constexpr uint32_t kVocab = 151936u;
+constexpr int kTopK = 20;
+constexpr uint32_t kNone = 0xffffffffu;
+
+// Sampler constants as binary32 bit patterns (fp32_sse2.rs:1792-1795, 1855).
+constexpr uint32_t kTemperatureBits = 0x3f333333u;  // 0.7f
+constexpr uint32_t kTopPBits = 0x3f4ccccdu;         // 0.8f
+constexpr uint32_t kPenaltyBits = 0x3f8ccccdu;      // 1.1f
+constexpr uint32_t kTwoPow24Bits = 0x4b800000u;
+
+// Row flags (not part of the reference; reported beside each draw).
+constexpr uint32_t kFlagDrawBoundary = 1u;
+constexpr uint32_t kFlagCutoffBoundary = 2u;
+
+__device__ __forceinline__ float f_of(uint32_t b) { return __uint_as_float(b); }
+__device__ __forceinline__ uint32_t b_of(float f) { return __float_as_uint(f); }
+
+// ---- scalbnf / expf: FreeBSD e_expf method as adapted in
+// fp32_sse2.rs:378-469 (rust-lang/libm 0.2.11), one IEEE op per step. ----
+//
+// ====================================================
+// Copyright (C) 1993 by Sun Microsystems, Inc. All rights reserved.
+//
+// Developed at SunPro, a Sun Microsystems, Inc. business.
+// Permission to use, copy, modify, and distribute this
+// software is freely granted, provided that this notice
+// is preserved.
+// ====================================================
+__device__ __forceinline__ float scalbnf_ref(float value, int exponent) {
+  const float two127 = f_of(0x7f000000u);
+  const float two_m102 = f_of(0x0c800000u);  // 2^-126 * 2^24, exact
+  if (exponent > 127) {
+    value = value * two127;
+    exponent -= 127;
+    if (exponent > 127) {
+      value = value * two127;
+      exponent -= 127;
+      if (exponent > 127) exponent = 127;
+    }
+  } else if (exponent < -126) {
+    value = value * two_m102;
+    exponent += 126 - 24;
+    if (exponent < -126) {
+      value = value * two_m102;
+      exponent += 126 - 24;
+      if (exponent < -126) exponent = -126;
+    }
+  }
+  return value * f_of((uint32_t)(0x7f + exponent) << 23);
+}
+
+__device__ __forceinline__ float expf_ref(float x) {
+  const uint32_t xb = b_of(x);
+  const uint32_t magnitude = xb & 0x7fffffffu;
+  const uint32_t sign = xb >> 31;
+  if (magnitude >= 0x42aeac50u) {
+    if (magnitude > 0x7f800000u) return x;
+    if (magnitude >= 0x42b17218u && sign == 0) return x * f_of(0x7f000000u);
+    if (sign != 0 && magnitude >= 0x42cff1b5u) return 0.0f;
+  }
+  int k;
+  float hi, lo;
+  if (magnitude > 0x3eb17218u) {
+    if (magnitude > 0x3f851592u) {
+      const float half = sign == 0 ? f_of(0x3f000000u) : f_of(0xbf000000u);
+      const float scaled = f_of(0x3fb8aa3bu) * x;
+      k = (int)(scaled + half);  // v_cvt_i32_f32 truncates toward zero
+    } else {
+      k = 1 - (int)sign - (int)sign;
+    }
+    const float kf = (float)k;
+    const float khi = kf * f_of(0x3f317200u);
+    hi = x - khi;
+    lo = kf * f_of(0x35bfbe8eu);
+    x = hi - lo;
+  } else if (magnitude > 0x39000000u) {
+    k = 0;
+    hi = x;
+    lo = 0.0f;
+  } else {
+    return f_of(0x3f800000u) + x;
+  }
+  const float xx = x * x;
+  const float poly = f_of(0x3e2aaa8fu) + xx * f_of(0xbb355215u);
+  const float c = x - xx * poly;
+  const float num = x * c;
+  const float den = f_of(0x40000000u) - c;
+  const float frac = num / den;
+  const float inner = (frac - lo) + hi;
+  const float y = f_of(0x3f800000u) + inner;
+  return k == 0 ? y : scalbnf_ref(y, k);
+}
+
+// Repetition penalty of one logit (fp32_sse2.rs:1860-1866): negative non-zero
+// values are multiplied by 1.1f, everything else (positive, +0, -0) divided.
+// The result never exceeds the input in IEEE order.
+__device__ __forceinline__ uint32_t penalize_bits(uint32_t score) {
+  const float p = f_of(kPenaltyBits);
+  if ((score & 0x80000000u) != 0 && (score & 0x7fffffffu) != 0) return b_of(f_of(score) * p);
+  return b_of(f_of(score) / p);
+}
+
+// ---- 64-bit selection keys ----
+// key = ord(value) << 32 | (0x3ffff - id) << 1 | negzero.
+// ord is the order-preserving map of binary32 with -0 folded onto +0, so a
+// larger key means (larger value) or (equal value, smaller id): exactly the
+// reference's rank order (strict `>` insertion over an ascending-id scan,
+// fp32_sse2.rs:1797-1816).  The low bit keeps -0 recoverable; ids are below
+// 2^18, so no two elements share a key and 0 is never a key.
+__device__ __forceinline__ uint32_t ord_of(uint32_t bits) {
+  if (bits == 0x80000000u) bits = 0u;
+  return (bits & 0x80000000u) ? ~bits : (bits | 0x80000000u);
+}
+__device__ __forceinline__ uint64_t make_key(uint32_t value_bits, uint32_t id) {
+  const uint32_t low = ((0x3ffffu - id) << 1) | (value_bits == 0x80000000u ? 1u : 0u);
+  return ((uint64_t)ord_of(value_bits) << 32) | low;
+}
+__device__ __forceinline__ uint32_t key_id(uint64_t key) {
+  return 0x3ffffu - (((uint32_t)key >> 1) & 0x3ffffu);
+}
+__device__ __forceinline__ uint32_t key_value_bits(uint64_t key) {
+  const uint32_t ord = (uint32_t)(key >> 32);
+  uint32_t bits = (ord & 0x80000000u) ? (ord & 0x7fffffffu) : ~ord;
+  if (bits == 0u && (key & 1u)) bits = 0x80000000u;
+  return bits;
+}
+// Lowest float that can still reach `key` (its value, ties included).
+__device__ __forceinline__ float key_floor_value(uint64_t key) {
+  if (key == 0) return -__builtin_inff();
+  return f_of(key_value_bits(key));
+}
+
+// ---- wave (64-lane) primitives ----
+__device__ __forceinline__ uint32_t lane_id() {
+  return __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+}
+__device__ __forceinline__ uint32_t lanes_below(uint64_t mask) {
+  return __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
+                                   __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+}
+__device__ __forceinline__ uint64_t shfl_xor64(uint64_t v, int mask) {
+  const uint32_t lo = __shfl_xor((int)(uint32_t)v, mask, 64);
+  const uint32_t hi = __shfl_xor((int)(uint32_t)(v >> 32), mask, 64);
+  return ((uint64_t)hi << 32) | lo;
+}
+__device__ __forceinline__ uint64_t shfl64(uint64_t v, int src) {
+  const uint32_t lo = __shfl((int)(uint32_t)v, src, 64);
+  const uint32_t hi = __shfl((int)(uint32_t)(v >> 32), src, 64);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+// Bitonic sort of one key per lane, descending (lane 0 holds the maximum).
+__device__ __forceinline__ uint64_t wave_sort_desc(uint64_t key, uint32_t lane) {
+#pragma unroll
+  for (uint32_t k = 2; k <= 64; k <<= 1) {
+#pragma unroll
+    for (uint32_t j = k >> 1; j > 0; j >>= 1) {
+      const uint64_t other = shfl_xor64(key, (int)j);
+      const bool lower = (lane & j) == 0;
+      const bool desc = (lane & k) == 0;
+      const bool take_max = lower == desc;
+      const uint64_t hi = key > other ? key : other;
+      const uint64_t lo = key > other ? other : key;
+      key = take_max ? hi : lo;
+    }
+  }
+  return key;
+}
+
+// One merge round: the wave's current top-20 (LDS, sorted, 0 = empty) plus up
+// to 44 new keys from `src` are sorted; the best 20 become the new top.
+// Returns the new 20th key (0 while fewer than 20 real keys are held).
+template <typename SrcPtr>
+__device__ __forceinline__ uint64_t merge_round(uint64_t* top, SrcPtr src, uint32_t n,
+                                                uint32_t lane) {
+  uint64_t key = 0;
+  if (lane < (uint32_t)kTopK) {
+    key = top[lane];
+  } else if (lane - kTopK < n) {
+    key = src[lane - kTopK];
+  }
+  key = wave_sort_desc(key, lane);
+  __builtin_amdgcn_wave_barrier();
+  if (lane < (uint32_t)kTopK) top[lane] = key;
+  __builtin_amdgcn_wave_barrier();
+  return shfl64(key, kTopK - 1);
+}
+
+constexpr uint32_t kMergeTake = 64 - kTopK;  // 44 new keys per round
+
+// Merge `n` keys from src into top (any n), in rounds of 44.
+template <typename SrcPtr>
+__device__ __forceinline__ uint64_t merge_all(uint64_t* top, SrcPtr src, uint32_t n,
+                                              uint32_t lane) {
+  uint64_t thr = 0;
+  uint32_t done = 0;
+  while (done < n) {
+    const uint32_t take = (n - done) < kMergeTake ? (n - done) : kMergeTake;
+    thr = merge_round(top, src + done, take, lane);
+    done += take;
+  }
+  return thr;
+}
+
+}  // namespace pb

@@ -1,0 +1,54 @@
+// pb_internal.h -- launch parameters shared by the kernels and the C ABI layer.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "pbsample.h"
+
+namespace pb {
+
+// float4 per lane per streaming chunk (register-resident, double-buffered).
+constexpr int kChunkF4 = 8;
+
+struct RowParams {
+  const uint32_t* logits;  // rows x ld binary32 words
+  size_t ld;
+  uint32_t rows;
+  const uint32_t* hist;    // rows x hist_ld ids, or null
+  size_t hist_ld;
+  const uint32_t* hist_len;
+  const uint8_t* excl;     // rows x PB_SEEN_BYTES ids not to penalise, or null
+  const uint32_t* random_24;
+  uint32_t* token;
+  pb_sample_detail* detail;
+  pb_inference_error* err;
+  uint64_t* part_keys;     // rows x segs x 20 (segs > 1)
+  uint32_t* part_meta;     // rows x segs x {first non-finite index, first bad history position}
+  uint32_t segs;           // slices per row
+  uint32_t seg_f4;         // float4 per slice, multiple of 8
+  uint32_t hist_vec4;      // history rows are 16-byte aligned: load 4 ids at a time
+};
+
+struct WritebackParams {
+  uint32_t* logits;
+  size_t ld;
+  uint32_t rows;
+  const uint32_t* hist;
+  size_t hist_ld;
+  const uint32_t* hist_len;
+  uint8_t* seen;           // rows x PB_SEEN_BYTES, or null
+  const uint32_t* token;   // PB_NO_TOKEN marks a failed row
+  uint32_t* gather;        // rows x hist_ld final values at the history ids, or null
+};
+
+uint32_t segments_for_rows(uint32_t rows);
+// forced_segments == 0 picks segments_for_rows(rows).
+void plan_segments(uint32_t rows, uint32_t forced_segments, uint32_t* segs, uint32_t* seg_f4);
+hipError_t launch_sample(const RowParams& p, hipStream_t stream);
+hipError_t launch_writeback(const WritebackParams& p, hipStream_t stream);
+hipError_t launch_probe(int which, const uint32_t* in, uint32_t* out, size_t n,
+                        hipStream_t stream);
+
+}  // namespace pb

@@ -1,0 +1,135 @@
+"""Seeded synthetic sampler workloads (the shapes promptboot's sampler sees).
+
+Every workload is a batch of independent decode-step rows over the Qwen2.5
+vocabulary (151,936 logits): fp32 logits, a padded uint32 history matrix
+with per-row lengths, and one 24-bit uniform per row drawn with the
+reference's own xorshift64* generator (SamplingState::new(seed_r), one
+next_24; inference.rs:779-810).  Row r uses seed_r = base_seed + r.
+
+    single    B=1: logits N(0, 2.5^2) with 5 distinct ids boosted by +U(8, 15);
+              300 history ids ~ truncated Zipf(s=1.1) on [0, V); seed 42.
+    small     B=64: same logits; history length ~ U[16, 1024], Zipf ids.
+    large     B=4096: same logits; history length ~ U[16, 32768] (full
+              context), stored as a [4096, 32768] padded matrix.
+    flat      B=1024: logits N(0, 0.1^2) (top-p mass spread over all 20).
+    ties      B=1024: the `small` logits rounded to multiples of 0.25, so many
+              values tie at the rank-20 boundary.
+    dominant  B=1024: N(0, 2.5^2) with one id at +40.
+    half      B=1024: the `small` logits; each history is a shuffled set of
+              V/2 distinct ids (penalty on half the vocabulary).
+
+Generation is numpy with a fixed PCG64 seed, so every machine builds the
+same bytes.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+VOCAB = 151_936
+ZIPF_S = 1.1
+_ZIPF_CDF = None
+
+
+def next_24_stream(seeds: np.ndarray) -> np.ndarray:
+    """One next_24 per seed (vectorised xorshift64*, inference.rs:779-810)."""
+    s = np.asarray(seeds, dtype=np.uint64).copy()
+    s[s == 0] = np.uint64(0x9E3779B97F4A7C15)
+    with np.errstate(over="ignore"):
+        s ^= s >> np.uint64(12)
+        s ^= s << np.uint64(25)
+        s ^= s >> np.uint64(27)
+        out = (s * np.uint64(0x2545F4914F6CDD1D)) >> np.uint64(40)
+    return out.astype(np.uint32)
+
+
+def zipf_ids(rng: np.random.Generator, n: int) -> np.ndarray:
+    """n ids from P(k) proportional to (k+1)^-1.1 on [0, VOCAB)."""
+    global _ZIPF_CDF
+    if _ZIPF_CDF is None:
+        w = np.arange(1, VOCAB + 1, dtype=np.float64) ** -ZIPF_S
+        c = np.cumsum(w)
+        _ZIPF_CDF = c / c[-1]
+    u = rng.random(n)
+    return np.minimum(np.searchsorted(_ZIPF_CDF, u, side="right"), VOCAB - 1).astype(np.uint32)
+
+
+def boosted_normal(rng: np.random.Generator, rows: int, sigma: float = 2.5,
+                   boosts: int = 5) -> np.ndarray:
+    x = rng.standard_normal((rows, VOCAB), dtype=np.float32)
+    x *= np.float32(sigma)
+    for r in range(rows):
+        ids = rng.choice(VOCAB, boosts, replace=False)
+        x[r, ids] += rng.uniform(8.0, 15.0, boosts).astype(np.float32)
+    return x
+
+
+def zipf_history(rng: np.random.Generator, lengths: np.ndarray, hist_ld: int) -> np.ndarray:
+    rows = len(lengths)
+    hist = np.zeros((rows, hist_ld), np.uint32)
+    total = int(lengths.sum())
+    ids = zipf_ids(rng, total)
+    pos = 0
+    for r, L in enumerate(lengths):
+        hist[r, :L] = ids[pos:pos + L]
+        pos += L
+    return hist
+
+
+CONFIGS = {
+    "single": dict(rows=1),
+    "small": dict(rows=64),
+    "large": dict(rows=4096),
+    "flat": dict(rows=1024),
+    "ties": dict(rows=1024),
+    "dominant": dict(rows=1024),
+    "half": dict(rows=1024),
+}
+
+
+def make(name: str, rows: int | None = None, seed: int = 20240601, base_seed: int = 42) -> dict:
+    """Returns dict(logits float32 [B, V], hist uint32 [B, hist_ld],
+    hist_len uint32 [B], random_24 uint32 [B], seeds uint64 [B], name)."""
+    if name not in CONFIGS:
+        raise KeyError(name)
+    B = rows if rows is not None else CONFIGS[name]["rows"]
+    rng = np.random.default_rng([seed, list(CONFIGS).index(name)])
+    if name == "single":
+        logits = boosted_normal(rng, B)
+        lengths = np.full(B, 300, np.uint32)
+        hist = zipf_history(rng, lengths, 300)
+    elif name in ("small", "ties", "half"):
+        logits = boosted_normal(rng, B)
+        if name == "ties":
+            logits = (np.round(logits * np.float32(4.0)) / np.float32(4.0)).astype(np.float32)
+        if name == "half":
+            half = VOCAB // 2
+            lengths = np.full(B, half, np.uint32)
+            hist = np.empty((B, half), np.uint32)
+            for r in range(B):
+                hist[r] = rng.permutation(VOCAB)[:half].astype(np.uint32)
+        else:
+            lengths = rng.integers(16, 1025, B).astype(np.uint32)
+            hist = zipf_history(rng, lengths, 1024)
+    elif name == "large":
+        logits = boosted_normal(rng, B)
+        lengths = rng.integers(16, 32769, B).astype(np.uint32)
+        hist = zipf_history(rng, lengths, 32768)
+    elif name == "flat":
+        logits = rng.standard_normal((B, VOCAB), dtype=np.float32) * np.float32(0.1)
+        lengths = rng.integers(16, 1025, B).astype(np.uint32)
+        hist = zipf_history(rng, lengths, 1024)
+    elif name == "dominant":
+        logits = rng.standard_normal((B, VOCAB), dtype=np.float32) * np.float32(2.5)
+        logits[np.arange(B), rng.integers(0, VOCAB, B)] = np.float32(40.0)
+        lengths = rng.integers(16, 1025, B).astype(np.uint32)
+        hist = zipf_history(rng, lengths, 1024)
+    seeds = np.uint64(base_seed) + np.arange(B, dtype=np.uint64)
+    return dict(name=name, logits=logits, hist=hist, hist_len=lengths.astype(np.uint32),
+                random_24=next_24_stream(seeds), seeds=seeds)
+
+
+def algorithmic_bytes(hist_len: np.ndarray) -> int:
+    """HBM bytes the path must move per batch: every logit once, every valid
+    history id once, plus the per-row length, uniform and token words."""
+    rows = len(hist_len)
+    return rows * (4 * VOCAB + 12) + 4 * int(np.asarray(hist_len, np.int64).sum())

@@ -1,0 +1,148 @@
+"""Batched device sampler vs the oracle, row by row, every output bit-exact (GPU).
+
+Covers the workloads of promptboot_amd.workloads (B=1, 64, adversarial
+B=1024 cases, a B=4096 slice of full-context histories), both the
+single-workgroup path (one slice per row) and the multi-slice path with the
+cross-slice merge, error rows, and the in-place penalty variant.
+"""
+import numpy as np
+import pytest
+
+from oracle import oracle as o
+from promptboot_amd import sampler as s
+from promptboot_amd import workloads
+from tests.conftest import assert_rows_equal, to_dev
+
+pytestmark = pytest.mark.gpu
+
+V = s.VOCAB
+
+
+@pytest.fixture(scope="module")
+def sampler():
+    smp = s.BatchSampler(0)
+    yield smp
+    smp.close()
+
+
+def run_gpu(smp, w, segments=0, rows=None):
+    import torch
+
+    smp.set_segments(segments)
+    B = w["logits"].shape[0] if rows is None else rows
+    logits = to_dev(w["logits"][:B])
+    hist = to_dev(w["hist"][:B])
+    hl = to_dev(w["hist_len"][:B])
+    r24 = to_dev(w["random_24"][:B])
+    token = torch.empty(B, dtype=torch.int32, device="cuda:0")
+    det = torch.empty((B, s.DETAIL_DTYPE.itemsize // 4), dtype=torch.int32, device="cuda:0")
+    err = torch.empty((B, s.ERROR_DTYPE.itemsize // 4), dtype=torch.int32, device="cuda:0")
+    smp.sample(logits, r24, hist, hl, token=token, detail=det, err=err)
+    torch.cuda.synchronize()
+    smp.set_segments(0)
+    return (token.cpu().numpy().view(np.uint32), det.cpu().numpy().view(s.DETAIL_DTYPE).reshape(B),
+            err.cpu().numpy().view(s.ERROR_DTYPE).reshape(B))
+
+
+def run_oracle(w, rows=None):
+    B = w["logits"].shape[0] if rows is None else rows
+    tok, det, err, _ = o.sample_batch(w["logits"][:B], w["hist"][:B], w["hist_len"][:B],
+                                      w["random_24"][:B], threads=16)
+    return tok, det, err
+
+
+@pytest.mark.parametrize("name,rows", [("single", None), ("small", None), ("flat", 256),
+                                       ("ties", 256), ("dominant", 256), ("half", 128)])
+@pytest.mark.parametrize("segments", [0, 1, 7])
+def test_batch_matches_oracle(sampler, name, rows, segments):
+    w = workloads.make(name, rows=rows)
+    got = run_gpu(sampler, w, segments)
+    want = run_oracle(w)
+    assert_rows_equal(*got, *want)
+    assert (got[2]["status"] == 0).all()
+
+
+def test_large_rows_with_full_context_histories(sampler):
+    w = workloads.make("large", rows=512)
+    assert w["hist"].shape[1] == 32768 and w["hist_len"].max() > 30000
+    got = run_gpu(sampler, w)
+    want = run_oracle(w)
+    assert_rows_equal(*got, *want)
+
+
+@pytest.mark.parametrize("segments", [1, 2, 5, 64])
+def test_segment_counts_agree(sampler, segments):
+    w = workloads.make("small", rows=16)
+    assert_rows_equal(*run_gpu(sampler, w, segments), *run_oracle(w))
+
+
+def test_error_rows_and_precedence(sampler):
+    w = workloads.make("small", rows=12)
+    lg, hist, hl = w["logits"], w["hist"], w["hist_len"]
+    lg[1, 151_935] = np.nan                       # last element
+    lg[2, 0] = np.inf                             # first element
+    lg[3, [90_000, 7, 150_000]] = [np.nan, -np.inf, np.inf]  # first index wins
+    hist[4, 5] = V                                # first bad id position wins
+    hist[4, 9] = V + 100
+    hl[4] = max(hl[4], 10)
+    lg[5, 100] = np.nan                           # non-finite beats a bad id
+    hist[5, 0] = 0xFFFFFFFF
+    hl[6] = min(hl[6], hist.shape[1] - 1)
+    hist[6, hl[6]] = V + 1                        # beyond the length: ignored
+    lg[7, :] = np.float32(-3.4e38)                # penalty overflows to -inf
+    lg[8, :] = 0.0                                # all ties
+    lg[8, ::2] = np.float32(-0.0)
+    lg[9, :] = np.float32(1e-42)                  # subnormal logits
+    lg[10, 1000:1040] = np.float32(7.0)           # a tie block at the top
+    for segments in (0, 1, 3, 64):
+        assert_rows_equal(*run_gpu(sampler, w, segments), *run_oracle(w))
+    tok, det, err = run_gpu(sampler, w)
+    assert err["status"].tolist()[:6] == [0, 7, 7, 7, 3, 7]
+    assert err["detail"][3] == (7 << 32) | 7 and err["available"][4] == V
+    assert (tok[1:6] == s.NO_TOKEN).all()
+    assert (det[1:6]["ids"] == 0xFFFFFFFF).all()
+
+
+def test_inplace_variant_penalises_like_the_reference(sampler):
+    import torch
+
+    w = workloads.make("small", rows=24)
+    w["logits"][3, 17] = np.nan  # a failing row must stay untouched
+    B = 24
+    logits = to_dev(w["logits"])
+    seen = torch.zeros((B, s.SEEN_BYTES), dtype=torch.uint8, device="cuda:0")
+    token = torch.empty(B, dtype=torch.int32, device="cuda:0")
+    sampler.sample(logits, to_dev(w["random_24"]), to_dev(w["hist"]), to_dev(w["hist_len"]),
+                   token=token, inplace=True, seen=seen)
+    torch.cuda.synchronize()
+    rtok, _, rerr, pen = o.sample_batch(w["logits"], w["hist"], w["hist_len"], w["random_24"],
+                                        threads=8, want_penalized=True)
+    got = logits.cpu().numpy().view(np.uint32)
+    assert (token.cpu().numpy().view(np.uint32) == rtok).all()
+    ok = rerr["status"] == 0
+    assert (got[ok] == pen[ok]).all()
+    assert (got[~ok] == w["logits"][~ok].view(np.uint32)).all()
+    assert not seen.cpu().numpy().any()
+
+
+def test_rows_are_independent_of_batch_neighbours(sampler):
+    w = workloads.make("small", rows=64)
+    full = run_gpu(sampler, w)
+    for r in (0, 17, 63):
+        one = {k: (v[r:r + 1] if isinstance(v, np.ndarray) else v) for k, v in w.items()}
+        single = run_gpu(sampler, one)
+        assert single[0][0] == full[0][r]
+        assert (single[1][0]["ids"] == full[1][r]["ids"]).all()
+
+
+def test_sample_rows_is_transactional_per_row(sampler):
+    w = workloads.make("small", rows=6)
+    w["logits"][2, 5] = np.inf
+    states = [s.SamplingState(int(x)) for x in w["seeds"]]
+    tok, det, err = sampler.sample_rows(to_dev(w["logits"]), to_dev(w["hist"]),
+                                        to_dev(w["hist_len"]), states)
+    draws = [st.draws() for st in states]
+    assert draws == [1, 1, 0, 1, 1, 1]
+    assert states[2] == s.SamplingState(int(w["seeds"][2]))
+    rtok, _, _, _ = o.sample_batch(w["logits"], w["hist"], w["hist_len"], w["random_24"])
+    assert (tok == rtok).all()
