@@ -1,0 +1,260 @@
+#!/usr/bin/env python3
+"""Throughput of the batched decode-step sampler on one MI355X.
+
+One step = one pb_sample_batch call over a resident batch of synthetic rows
+(151,936 fp32 logits each, with histories and per-row uniforms): repetition
+penalty, top-20, temperature-0.7 softmax, top-p 0.8 and the draw for every
+row.  The headline workload is B=4096 rows with full-context histories
+(promptboot_amd.workloads "large"); B=1 and B=64 are timed the same way and
+reported under "by_batch".
+
+The printed JSON line also carries:
+  roofline      the segment kernel's algorithmic HBM bytes per launch over
+                its average launch time (HIP events on the launch stream)
+                against the 8 TB/s MI355X peak, and the measured HBM traffic
+                from the committed rocprofv3 counter summary when present;
+  cpu_baseline  the CPU oracle (a restatement of the reference sampler),
+                single-threaded and pinned to one CPU, on a bounded sample of
+                the same rows (first 1024 rows, 3 repetitions, median);
+  parity        token agreement with the oracle over every row of the batch.
+
+Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import pathlib
+import subprocess
+import sys
+import tempfile
+import time
+
+import numpy as np
+
+ROOT = pathlib.Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "sampled rows/s at vocab 151936 (B=1/64/4096); % of MI355X HBM roofline"
+PEAK_HBM_GBS = 8000.0
+CPU_SAMPLE_ROWS = 1024
+PMC_SUMMARY = ROOT / "profiles" / "segment_kernel_B4096_traffic.json"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def host_cores() -> dict:
+    cpus = pathlib.Path("/sys/devices/system/cpu")
+    physical = set()
+    for topo in cpus.glob("cpu[0-9]*/topology"):
+        try:
+            physical.add(((topo / "physical_package_id").read_text().strip(),
+                          (topo / "core_id").read_text().strip()))
+        except OSError:
+            pass
+    return {"physical": len(physical) or None, "logical": os.cpu_count(),
+            "online": os.sysconf("SC_NPROCESSORS_ONLN"),
+            "affinity": len(os.sched_getaffinity(0))}
+
+
+def cpu_worker(path: str) -> None:
+    """Child process pinned to one CPU: times the oracle on the sample rows."""
+    from oracle import oracle as o
+
+    assert len(os.sched_getaffinity(0)) == 1, "CPU baseline must see exactly one CPU"
+    d = np.load(path)
+    runs = []
+    tokens = None
+    for _ in range(3):
+        secs, tok = o.time_batch(d["logits"], d["hist"], d["hist_len"], d["seeds"])
+        runs.append(secs)
+        if tokens is not None:
+            assert (tok == tokens).all()
+        tokens = tok
+    print(json.dumps({"runs_s": runs, "rows": int(d["logits"].shape[0]),
+                      "tokens": tokens.tolist()}))
+
+
+def cpu_baseline(w: dict) -> dict:
+    cpu = sorted(os.sched_getaffinity(0))[0]
+    n = min(CPU_SAMPLE_ROWS, w["logits"].shape[0])
+    with tempfile.NamedTemporaryFile(suffix=".npz", dir="/dev/shm", delete=False) as f:
+        path = f.name
+    try:
+        np.savez(path, logits=w["logits"][:n], hist=w["hist"][:n], hist_len=w["hist_len"][:n],
+                 seeds=w["seeds"][:n])
+        out = subprocess.run(["taskset", "-c", str(cpu), sys.executable, str(ROOT / "bench.py"),
+                              "--cpu-worker", path], check=True, capture_output=True, text=True)
+    finally:
+        os.unlink(path)
+    res = json.loads(out.stdout.strip().splitlines()[-1])
+    runs = sorted(res["runs_s"])
+    med = runs[1]
+    return {"value": round(n / med, 2), "unit": "rows/s", "cores": 1, "kind": "port",
+            "sample": f"first {n} rows of the B=4096 workload, sample_token_with_repetition "
+                      f"per row, 3 repetitions (median), pinned to CPU {cpu}",
+            "runs_s": [round(r, 4) for r in res["runs_s"]],
+            "min_s": round(runs[0], 4), "median_s": round(med, 4), "max_s": round(runs[2], 4),
+            "host_cores": host_cores(), "_tokens": np.array(res["tokens"], np.uint32)}
+
+
+def time_batch(smp, w: dict, steps: int, warmup: int) -> dict:
+    import torch
+
+    from promptboot_amd import sampler as s
+    from promptboot_amd import workloads
+
+    dev = torch.device("cuda:0")
+
+    def t(a):
+        return torch.from_numpy(np.ascontiguousarray(a).view(np.int32)).to(dev)
+
+    B = w["logits"].shape[0]
+    logits, hist, hl, r24 = t(w["logits"]), t(w["hist"]), t(w["hist_len"]), t(w["random_24"])
+    token = torch.empty(B, dtype=torch.int32, device=dev)
+    det = torch.empty((B, s.DETAIL_DTYPE.itemsize // 4), dtype=torch.int32, device=dev)
+    stream = torch.cuda.current_stream(dev)
+
+    def step(with_detail=False):
+        smp.sample(logits, r24, hist, hl, token=token, detail=det if with_detail else None,
+                   stream=stream)
+
+    step(with_detail=True)
+    torch.cuda.synchronize()
+    tokens = token.cpu().numpy().view(np.uint32).copy()
+    detail = det.cpu().numpy().view(s.DETAIL_DTYPE).reshape(B).copy()
+    for _ in range(warmup):
+        step()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        starts[i].record(stream)
+        step()
+        ends[i].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    kernel_ms = float(np.mean([a.elapsed_time(b) for a, b in zip(starts, ends)]))
+    ms_per_step = wall / steps * 1e3
+    alg = workloads.algorithmic_bytes(w["hist_len"])
+    return {"rows": B, "ms_per_step": ms_per_step, "rows_per_s": B / (ms_per_step / 1e3),
+            "launch_ms": kernel_ms, "alg_bytes": alg,
+            "achieved_gbs": alg / (kernel_ms / 1e3) / 1e9,
+            "segments": int(s.lib().pb_segments_for_rows(B)),
+            "_tokens": tokens, "_detail": detail}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--batches", default="1,64,4096")
+    ap.add_argument("--cpu-worker", default=None, help=argparse.SUPPRESS)
+    args = ap.parse_args()
+    if args.cpu_worker:
+        cpu_worker(args.cpu_worker)
+        return 0
+    if args.gpus != 1:
+        print("bench.py measures one GPU only: the sampler shards rows across GPUs with no "
+              "exchange, so the whole-job rate at N GPUs is N independent copies of this "
+              "measurement; run with --gpus 1.", file=sys.stderr)
+        return 2
+
+    from promptboot_amd import workloads
+
+    names = {1: "single", 64: "small", 4096: "large"}
+    batches = [int(b) for b in args.batches.split(",")]
+    work = {}
+    for B in batches:
+        log(f"generating workload B={B}")
+        work[B] = workloads.make(names.get(B, "large"), rows=None if B in names else B)
+
+    cpu = None
+    head = max(batches)
+    if not args.no_cpu_baseline:
+        log("timing the CPU baseline (oracle, one pinned CPU)")
+        cpu = cpu_baseline(work[head])
+
+    import torch
+
+    from oracle import oracle as o
+    from promptboot_amd import sampler as s
+
+    torch.cuda.set_device(0)
+    smp = s.BatchSampler(0)
+    results = {}
+    for B in batches:
+        log(f"timing B={B}")
+        results[B] = time_batch(smp, work[B], args.steps, args.warmup)
+    smp.close()
+
+    main_res = results[head]
+    w = work[head]
+    log("checking tokens against the oracle")
+    rtok, rdet, _, _ = o.sample_batch(w["logits"], w["hist"], w["hist_len"], w["random_24"],
+                                      threads=min(16, len(os.sched_getaffinity(0))))
+    boundary = (main_res["_detail"]["flags"] != 0)
+    agree = main_res["_tokens"] == rtok
+    topk_agree = (main_res["_detail"]["ids"] == rdet["ids"]).all(axis=1)
+    parity = {"rows": int(len(rtok)), "token_agreement": float(agree.mean()),
+              "token_agreement_non_boundary": float(agree[~boundary].mean()),
+              "boundary_rows": int(boundary.sum()),
+              "top20_set_agreement": float(topk_agree.mean())}
+    if cpu is not None:
+        n = len(cpu["_tokens"])
+        parity["cpu_baseline_tokens_agree"] = bool((cpu["_tokens"] == main_res["_tokens"][:n]).all())
+        cpu.pop("_tokens")
+
+    traffic = None
+    if PMC_SUMMARY.exists():
+        traffic = json.loads(PMC_SUMMARY.read_text()).get("hbm_bytes_per_launch")
+    roof = {"bound": "hbm", "achieved": round(main_res["achieved_gbs"], 1), "peak": PEAK_HBM_GBS,
+            "unit": "GB/s", "frac": round(main_res["achieved_gbs"] / PEAK_HBM_GBS, 4),
+            "traffic": traffic, "kernel": "pb::segment_kernel<8, true>",
+            "alg_bytes_per_launch": main_res["alg_bytes"],
+            "launch_ms": round(main_res["launch_ms"], 4)}
+    by_batch = {}
+    for B, r in results.items():
+        by_batch[str(B)] = {"rows_per_s": round(r["rows_per_s"], 1),
+                            "ms_per_step": round(r["ms_per_step"], 4),
+                            "launch_ms": round(r["launch_ms"], 4),
+                            "achieved_gbs": round(r["achieved_gbs"], 1),
+                            "hbm_frac": round(r["achieved_gbs"] / PEAK_HBM_GBS, 4),
+                            "segments_per_row": r["segments"]}
+    out = {
+        "metric": METRIC,
+        "value": round(main_res["rows_per_s"], 1),
+        "unit": "rows/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(main_res["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": f"B={head} rows x 151936 fp32 logits N(0,2.5^2)+5 boosts, "
+                               "history lengths U[16,32768] of Zipf(1.1) ids in a padded "
+                               "[B,32768] uint32 matrix, one 24-bit uniform per row "
+                               "(SamplingState seeds 42+r); temp 0.7, top-k 20, top-p 0.8, "
+                               "repetition penalty 1.1",
+                   "rows": head, "vocab": 151936, "hist_ld": int(w["hist"].shape[1])},
+        "tokens_per_s": round(main_res["rows_per_s"], 1),
+        "by_batch": by_batch,
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "parity": parity,
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())

@@ -103,6 +103,8 @@ def lib() -> ctypes.CDLL:
         L.pbo_top_logits_8.argtypes = [vp, size_t, vp, ctypes.POINTER(Error)]
         L.pbo_sample_batch.argtypes = [vp, size_t, size_t, u32, vp, size_t, vp, vp,
                                        vp, vp, vp, vp, ctypes.c_int]
+        L.pbo_time_batch.argtypes = [vp, size_t, u32, vp, size_t, vp, vp, vp]
+        L.pbo_time_batch.restype = u64
         L.pbo_expf_array.argtypes = [vp, vp, size_t]
         L.pbo_penalize_array.argtypes = [vp, vp, size_t]
         for name in ("pbo_sizeof_detail", "pbo_sizeof_error", "pbo_sizeof_state"):
@@ -153,6 +155,19 @@ class SamplingState:
 
 def expf_bits(x: int) -> int:
     return lib().pbo_expf_bits(x & 0xFFFFFFFF)
+
+
+def time_batch(logits, hist, hist_len, seeds) -> tuple[float, np.ndarray]:
+    """Single-threaded timing of sample_token_with_repetition per row (seconds
+    summed over rows, timer boundary of validate_inference.rs:780-794)."""
+    lg = _u32(logits)
+    h = _u32(hist)
+    hl = _u32(hist_len)
+    sd = np.ascontiguousarray(seeds, dtype=np.uint64)
+    tok = np.zeros(lg.shape[0], np.uint32)
+    ns = lib().pbo_time_batch(_ptr(lg), lg.shape[1], lg.shape[0], _ptr(h), h.shape[1],
+                              _ptr(hl), _ptr(sd), _ptr(tok))
+    return ns * 1e-9, tok
 
 
 def expf_array(words) -> np.ndarray:

@@ -28,12 +28,14 @@
  *
  * Build: oracle/Makefile (gcc -O2 -msse2 -mfpmath=sse -ffp-contract=off).
  */
+#define _POSIX_C_SOURCE 199309L
 #include <math.h>
 #include <pthread.h>
 #include <stddef.h>
 #include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
+#include <time.h>
 #include <xmmintrin.h>
 
 #if defined(__FMA__) || defined(__FAST_MATH__)
@@ -570,6 +572,36 @@ int pbo_sample_batch(const uint32_t *logits, size_t ld, size_t vocab, uint32_t r
     }
     for (int t = 0; t < threads; ++t) pthread_join(tid[t], NULL);
     return 0;
+}
+
+/* Single-threaded CPU baseline timer.  For each row: copy the logits into a
+ * private buffer and clear the scratch (untimed), then time one
+ * sample_token_with_repetition call on them through its return, the timer
+ * boundary of crates/promptboot-core/examples/validate_inference.rs:780-794.
+ * The row's generator is SamplingState::new(seeds[r]).  Returns the summed
+ * nanoseconds; tokens[r] receives the draw. */
+uint64_t pbo_time_batch(const uint32_t *logits, size_t ld, uint32_t rows, const uint32_t *hist,
+                        size_t hist_ld, const uint32_t *hist_len, const uint64_t *seeds,
+                        uint32_t *tokens) {
+    uint32_t *row = (uint32_t *)malloc(PBO_VOCAB * 4);
+    uint8_t *seen = (uint8_t *)calloc(PBO_SEEN_BYTES, 1);
+    uint64_t total = 0;
+    for (uint32_t r = 0; r < rows; ++r) {
+        memcpy(row, logits + (size_t)r * ld, PBO_VOCAB * 4);
+        memset(seen, 0, PBO_SEEN_BYTES);
+        pbo_state st;
+        pbo_state_new(&st, seeds[r]);
+        pbo_error e;
+        struct timespec t0, t1;
+        clock_gettime(CLOCK_MONOTONIC, &t0);
+        pbo_sample_token_with_repetition(row, PBO_VOCAB, hist + (size_t)r * hist_ld, hist_len[r],
+                                         seen, PBO_SEEN_BYTES, &st, &tokens[r], &e, NULL);
+        clock_gettime(CLOCK_MONOTONIC, &t1);
+        total += (uint64_t)(t1.tv_sec - t0.tv_sec) * 1000000000ull + (uint64_t)(t1.tv_nsec - t0.tv_nsec);
+    }
+    free(seen);
+    free(row);
+    return total;
 }
 
 /* Element-wise restated expf / single-logit penalty over arrays (checkers
