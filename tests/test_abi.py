@@ -1,0 +1,110 @@
+"""C ABI checks that need no GPU: the library loads, exports every function
+include/pbsample.h declares, the Python binding covers exactly those, the
+structs have the reference's repr(C) layouts (inference.rs:226-291), and the
+host-only parts (PRNG, length validation) behave like the reference."""
+import pathlib
+import re
+import subprocess
+
+import numpy as np
+import pytest
+
+from promptboot_amd import sampler as s
+from tests.conftest import ROOT
+
+HEADER = ROOT / "include" / "pbsample.h"
+
+
+def declared_functions() -> set[str]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return set(re.findall(r"\b(pb_[a-z0-9_]+)\s*\(", text))
+
+
+def test_library_exports_every_declared_function():
+    names = declared_functions()
+    assert len(names) >= 16
+    out = subprocess.run(["nm", "-D", "--defined-only", str(s.LIB_PATH)], check=True,
+                         capture_output=True, text=True).stdout
+    exported = set(re.findall(r" T (pb_[a-z0-9_]+)$", out, flags=re.M))
+    assert names <= exported, names - exported
+    assert exported <= names, exported - names
+    assert set(s.EXPORTS) == names
+    lib = s.lib()
+    for n in names:
+        assert getattr(lib, n) is not None
+
+
+def test_struct_layouts_match_the_reference(tmp_path):
+    src = tmp_path / "layout.c"
+    src.write_text("""
+#include <stddef.h>
+#include <stdio.h>
+#include "pbsample.h"
+int main(void) {
+  printf("%zu %zu %zu %zu %zu %zu %zu %zu %zu\\n", sizeof(pb_inference_error),
+         _Alignof(pb_inference_error), offsetof(pb_inference_error, needed),
+         offsetof(pb_inference_error, detail), sizeof(pb_sampling_state),
+         sizeof(pb_top_logit), sizeof(pb_sample_detail),
+         offsetof(pb_sample_detail, kept), offsetof(pb_sample_detail, probs));
+  return 0;
+}
+""")
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c11", "-Wall", "-Werror", f"-I{HEADER.parent}", str(src), "-o",
+                    str(exe)], check=True)
+    vals = [int(v) for v in subprocess.run([str(exe)], check=True, capture_output=True,
+                                           text=True).stdout.split()]
+    # InferenceError: 48 bytes, align 8, needed at 24 (inference.rs:226-237, 287-288)
+    assert vals[:4] == [48, 8, 24, 40]
+    assert vals[4:6] == [16, 8]
+    assert vals[6:] == [s.DETAIL_DTYPE.itemsize, s.DETAIL_DTYPE.fields["kept"][1],
+                        s.DETAIL_DTYPE.fields["probs"][1]]
+
+
+def test_host_prng_matches_reference_states(known):
+    p = known["unit"]["prng"]
+    st = s.SamplingState(p["seed"])
+    for _ in range(8):
+        st.next_24()
+    assert (st.state(), st.draws()) == (p["state_after"], 8)
+    e = known["exact_host_oracle"]
+    st = s.SamplingState(e["seed"])
+    for _ in range(e["final_draws"]):
+        st.next_24()
+    assert st.state() == e["final_state"]
+    assert s.SamplingState(0).state() == p["zero_seed_state"]
+
+
+def test_fill_random_24_is_one_draw_per_row():
+    import ctypes
+
+    states = (s._State * 3)()
+    for i, seed in enumerate((42, 43, 0)):
+        s.lib().pb_sampling_state_new(ctypes.byref(states[i]), seed)
+    out = np.zeros(3, np.uint32)
+    s.lib().pb_fill_random_24(states, 3, out.ctypes.data_as(ctypes.c_void_p))
+    expect = [s.SamplingState(seed).next_24() for seed in (42, 43, 0)]
+    assert out.tolist() == expect
+    assert out[0] == 5_688_906
+    assert [st.draws for st in states] == [1, 1, 1]
+
+
+def test_length_errors_need_no_device(known):
+    t = known["unit"]["error_tuples"]
+    short = np.zeros(s.VOCAB - 1, np.uint32)
+    state = s.SamplingState(1)
+    for call in (lambda: s.sample_token(short, state), lambda: s.greedy_token(short),
+                 lambda: s.top_logits_8(short),
+                 lambda: s.sample_token_with_repetition(short.copy(), [], np.zeros(10, np.uint8),
+                                                        state)):
+        with pytest.raises(s.InferenceError) as ex:
+            call()
+        assert ex.value.tuple() == t["short"]
+    assert state.draws() == 0
+
+
+def test_version_and_segment_plan():
+    assert s.lib().pb_version().endswith(b"gfx950")
+    assert s.lib().pb_segments_for_rows(4096) == 1
+    assert 1 < s.lib().pb_segments_for_rows(64) <= 64
+    assert s.lib().pb_segments_for_rows(1) <= 64
