@@ -18,7 +18,10 @@ The printed JSON line also carries:
                 the same rows (first 1024 rows, 3 repetitions, median);
   parity        token agreement with the oracle over every row of the batch.
 
-Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5]
+Before the W warmup steps every batch size runs an untimed settle phase
+(the step repeated for 0.5 s) so the GPU is at its working clocks.
+
+Usage: python bench.py [--gpus 1] [--steps 200] [--warmup 5]
 """
 from __future__ import annotations
 
@@ -39,6 +42,7 @@ sys.path.insert(0, str(ROOT))
 METRIC = "sampled rows/s at vocab 151936 (B=1/64/4096); % of MI355X HBM roofline"
 PEAK_HBM_GBS = 8000.0
 CPU_SAMPLE_ROWS = 1024
+SETTLE_S = 0.5
 PMC_SUMMARY = ROOT / "profiles" / "segment_kernel_B4096_traffic.json"
 
 
@@ -126,6 +130,14 @@ def time_batch(smp, w: dict, steps: int, warmup: int) -> dict:
     torch.cuda.synchronize()
     tokens = token.cpu().numpy().view(np.uint32).copy()
     detail = det.cpu().numpy().view(s.DETAIL_DTYPE).reshape(B).copy()
+    # Untimed settle: repeat the step for SETTLE_S seconds so the GPU leaves
+    # its idle clocks (a cold MI355X runs the first tens of launches ~10 %
+    # slower), then the W warmup steps, then exactly K timed steps.
+    t_settle = time.perf_counter()
+    while time.perf_counter() - t_settle < SETTLE_S:
+        for _ in range(8):
+            step()
+        torch.cuda.synchronize()
     for _ in range(warmup):
         step()
     starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
@@ -144,17 +156,22 @@ def time_batch(smp, w: dict, steps: int, warmup: int) -> dict:
     return {"rows": B, "ms_per_step": ms_per_step, "rows_per_s": B / (ms_per_step / 1e3),
             "launch_ms": kernel_ms, "alg_bytes": alg,
             "achieved_gbs": alg / (kernel_ms / 1e3) / 1e9,
-            "segments": int(s.lib().pb_segments_for_rows(B)),
+            "segments": int(smp.segments or s.lib().pb_segments_for_rows(B)),
             "_tokens": tokens, "_detail": detail}
 
 
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--batches", default="1,64,4096")
+    ap.add_argument("--segments", type=int, default=0,
+                    help="force the slices per row (0 = the library's choice)")
+    ap.add_argument("--calibration-copy-mib", type=int, default=0,
+                    help="first run one device-to-device copy of this many MiB, so a "
+                         "rocprofv3 --pmc run can scale FETCH_SIZE/WRITE_SIZE to bytes")
     ap.add_argument("--cpu-worker", default=None, help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.cpu_worker:
@@ -187,7 +204,14 @@ def main() -> int:
     from promptboot_amd import sampler as s
 
     torch.cuda.set_device(0)
-    smp = s.BatchSampler(0)
+    if args.calibration_copy_mib:
+        n = args.calibration_copy_mib << 18  # float32 words
+        src = torch.ones(n, dtype=torch.float32, device="cuda:0")
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+    smp = s.BatchSampler(0, segments=args.segments)
     results = {}
     for B in batches:
         log(f"timing B={B}")

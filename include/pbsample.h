@@ -203,6 +203,9 @@ void pb_context_set_segments(pb_context *ctx, uint32_t segments);
  *   penalize: the repetition penalty of one logit (fp32_sse2.rs:1860-1866) */
 uint32_t pb_device_expf_bits(const uint32_t *d_in, uint32_t *d_out, size_t n, void *stream);
 uint32_t pb_device_penalize_bits(const uint32_t *d_in, uint32_t *d_out, size_t n, void *stream);
+/* One-wave self-test of the lane exchanges (DPP, permlane swaps) and wave
+ * reductions the selection uses; writes 11 x 64 words to d_out. */
+uint32_t pb_device_wave_selftest(uint32_t *d_out, void *stream);
 
 /* Library version string and build target ("gfx950"). */
 const char *pb_version(void);

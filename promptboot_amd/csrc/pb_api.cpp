@@ -62,8 +62,10 @@ struct pb_context {
   std::mutex mu;                 // serialises the drop-ins on this context
 
   uint32_t forced_segments = 0;  // 0 = automatic slices per row
-  void* d_work = nullptr;  // inter-kernel workspace (segment top-20 lists)
-  size_t work_bytes = 0;
+  void* d_work = nullptr;  // multi-slice workspace: row counters, slice top-20 lists
+  uint32_t counter_rows = 0;
+  size_t counter_bytes = 0;
+  size_t list_bytes = 0;
 
   // single-row staging
   uint32_t* d_row = nullptr;
@@ -83,17 +85,31 @@ struct pb_context {
   uint8_t* h_seen = nullptr;
 };
 
-static hipError_t ensure_workspace(pb_context* ctx, size_t bytes) {
-  if (bytes <= ctx->work_bytes) return hipSuccess;
+// Workspace of the multi-slice path: [per-row counters | slice keys + meta].
+// The counters live at a fixed offset so that they stay zero between launches
+// (each row's last slice resets its counter); they are zeroed with a kernel,
+// on the caller's stream, whenever the buffer is (re)allocated.
+static hipError_t ensure_workspace(pb_context* ctx, uint32_t rows, size_t list_bytes,
+                                   hipStream_t stream) {
+  if (rows <= ctx->counter_rows && list_bytes <= ctx->list_bytes) return hipSuccess;
+  const uint32_t counter_rows = rows > ctx->counter_rows ? rows : ctx->counter_rows;
+  const size_t lists = list_bytes > ctx->list_bytes ? list_bytes : ctx->list_bytes;
   if (ctx->d_work) {
     hipError_t e = hipFree(ctx->d_work);  // device-synchronising: no launch still reads it
     ctx->d_work = nullptr;
-    ctx->work_bytes = 0;
+    ctx->counter_rows = 0;
+    ctx->list_bytes = 0;
     if (e != hipSuccess) return e;
   }
-  hipError_t e = hipMalloc(&ctx->d_work, bytes);
-  if (e == hipSuccess) ctx->work_bytes = bytes;
-  return e;
+  const size_t counter_bytes = ((size_t)counter_rows * 4 + 255) & ~(size_t)255;
+  hipError_t e = hipMalloc(&ctx->d_work, counter_bytes + lists);
+  if (e != hipSuccess) return e;
+  e = pb::launch_zero(static_cast<uint32_t*>(ctx->d_work), counter_bytes / 4, stream);
+  if (e != hipSuccess) return e;
+  ctx->counter_rows = counter_rows;
+  ctx->counter_bytes = counter_bytes;
+  ctx->list_bytes = lists;
+  return hipSuccess;
 }
 
 static hipError_t ensure_hist_capacity(pb_context* ctx, size_t ids) {
@@ -178,6 +194,12 @@ uint32_t pb_device_penalize_bits(const uint32_t* d_in, uint32_t* d_out, size_t n
              : PB_DEVICE;
 }
 
+uint32_t pb_device_wave_selftest(uint32_t* d_out, void* stream) {
+  return pb::launch_wave_selftest(d_out, static_cast<hipStream_t>(stream)) == hipSuccess
+             ? PB_OK
+             : PB_DEVICE;
+}
+
 uint32_t pb_context_create(int device, pb_context** out) {
   *out = nullptr;
   if (device < 0 && hipGetDevice(&device) != hipSuccess) return PB_DEVICE;
@@ -255,14 +277,17 @@ static uint32_t enqueue_sample(pb_context* ctx, const uint32_t* d_logits, size_t
   pb::plan_segments(rows, ctx->forced_segments, &p.segs, &p.seg_f4);
   p.part_keys = nullptr;
   p.part_meta = nullptr;
+  p.row_done = nullptr;
   DeviceGuard guard(ctx->device);
   if (p.segs > 1) {
     const size_t slots = (size_t)rows * p.segs;
     const size_t key_bytes = slots * PB_TOP_K * 8;
-    hipError_t e = ensure_workspace(ctx, key_bytes + slots * 8);
+    hipError_t e = ensure_workspace(ctx, rows, key_bytes + slots * 8, stream);
     if (e != hipSuccess) return device_error(err, e);
-    p.part_keys = static_cast<uint64_t*>(ctx->d_work);
-    p.part_meta = reinterpret_cast<uint32_t*>(static_cast<char*>(ctx->d_work) + key_bytes);
+    char* base = static_cast<char*>(ctx->d_work);
+    p.row_done = reinterpret_cast<uint32_t*>(base);
+    p.part_keys = reinterpret_cast<uint64_t*>(base + ctx->counter_bytes);
+    p.part_meta = reinterpret_cast<uint32_t*>(base + ctx->counter_bytes + key_bytes);
   }
   hipError_t e = pb::launch_sample(p, stream);
   if (e != hipSuccess) return device_error(err, e);

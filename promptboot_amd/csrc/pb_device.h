@@ -156,15 +156,57 @@ __device__ __forceinline__ uint32_t lanes_below(uint64_t mask) {
   return __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
                                    __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
 }
+// Value of lane (lane ^ j) for j in {1, 2, 4, 8, 16, 32}, without the LDS
+// crossbar: DPP quad_perm for 1 and 2, DPP row rotations for 4 and 8 (a
+// 16-lane row rotated by 8 is lane ^ 8; rotations by 4 and 12 give the two
+// halves of lane ^ 4), and gfx950's v_permlane16_swap / v_permlane32_swap
+// for 16 and 32.  Every lane of the wave must be active.  `j` must fold to a
+// constant at each call site (unrolled loops).
+__device__ __forceinline__ uint32_t lane_xor(uint32_t v, uint32_t j, uint32_t lane) {
+  const int iv = (int)v;
+  switch (j) {
+    case 1:
+      return (uint32_t)__builtin_amdgcn_update_dpp(iv, iv, 0xB1, 0xF, 0xF, false);  // [1,0,3,2]
+    case 2:
+      return (uint32_t)__builtin_amdgcn_update_dpp(iv, iv, 0x4E, 0xF, 0xF, false);  // [2,3,0,1]
+    case 4: {
+      const uint32_t from_above = (uint32_t)__builtin_amdgcn_update_dpp(iv, iv, 0x12C, 0xF, 0xF, false);
+      const uint32_t from_below = (uint32_t)__builtin_amdgcn_update_dpp(iv, iv, 0x124, 0xF, 0xF, false);
+      return (lane & 4u) ? from_below : from_above;
+    }
+    case 8:
+      return (uint32_t)__builtin_amdgcn_update_dpp(iv, iv, 0x128, 0xF, 0xF, false);  // row_ror:8
+    case 16: {
+      const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+      return (lane & 16u) ? r[0] : r[1];
+    }
+    default: {
+      const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+      return (lane & 32u) ? r[0] : r[1];
+    }
+  }
+}
+
 __device__ __forceinline__ uint64_t shfl_xor64(uint64_t v, int mask) {
-  const uint32_t lo = __shfl_xor((int)(uint32_t)v, mask, 64);
-  const uint32_t hi = __shfl_xor((int)(uint32_t)(v >> 32), mask, 64);
+  const uint32_t lane = lane_id();
+  const uint32_t lo = lane_xor((uint32_t)v, (uint32_t)mask, lane);
+  const uint32_t hi = lane_xor((uint32_t)(v >> 32), (uint32_t)mask, lane);
   return ((uint64_t)hi << 32) | lo;
 }
-__device__ __forceinline__ uint64_t shfl64(uint64_t v, int src) {
-  const uint32_t lo = __shfl((int)(uint32_t)v, src, 64);
-  const uint32_t hi = __shfl((int)(uint32_t)(v >> 32), src, 64);
+// Broadcast from one lane; `src` must be the same in every lane (v_readlane).
+__device__ __forceinline__ uint32_t bcast32(uint32_t v, uint32_t src) {
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, (int)src);
+}
+__device__ __forceinline__ uint64_t shfl64(uint64_t v, uint32_t src) {
+  const uint32_t lo = bcast32((uint32_t)v, src);
+  const uint32_t hi = bcast32((uint32_t)(v >> 32), src);
   return ((uint64_t)hi << 32) | lo;
+}
+__device__ __forceinline__ float bcast_f32(float v, uint32_t src) {
+  return __uint_as_float(bcast32(__float_as_uint(v), src));
+}
+__device__ __forceinline__ double bcast_f64(double v, uint32_t src) {
+  return __builtin_bit_cast(double, shfl64(__builtin_bit_cast(uint64_t, v), src));
 }
 
 // Bitonic sort of one key per lane, descending (lane 0 holds the maximum).
@@ -206,6 +248,29 @@ __device__ __forceinline__ uint64_t merge_round(uint64_t* top, SrcPtr src, uint3
 
 constexpr uint32_t kMergeTake = 64 - kTopK;  // 44 new keys per round
 
+// Top-20 of two sorted (descending, 20 keys, 0 = empty) lists with one
+// bitonic merge: lanes 0..31 hold `a` descending (zero-padded), lanes 32..63
+// hold `b` ascending, so the 64 keys form a bitonic sequence and six
+// compare-exchange stages sort them.  Lane i < 20 returns the i-th best key.
+__device__ __forceinline__ uint64_t merge_two_lists(const uint64_t* a, const uint64_t* b,
+                                                    uint32_t lane) {
+  uint64_t key = 0;
+  if (lane < (uint32_t)kTopK) {
+    key = a[lane];
+  } else if (lane >= 64u - kTopK) {
+    key = b[63u - lane];
+  }
+#pragma unroll
+  for (uint32_t j = 32; j > 0; j >>= 1) {
+    const uint64_t other = shfl_xor64(key, (int)j);
+    const bool lower = (lane & j) == 0;
+    const uint64_t hi = key > other ? key : other;
+    const uint64_t lo = key > other ? other : key;
+    key = lower ? hi : lo;
+  }
+  return key;
+}
+
 // Merge `n` keys from src into top (any n), in rounds of 44.
 template <typename SrcPtr>
 __device__ __forceinline__ uint64_t merge_all(uint64_t* top, SrcPtr src, uint32_t n,
@@ -218,6 +283,36 @@ __device__ __forceinline__ uint64_t merge_all(uint64_t* top, SrcPtr src, uint32_
     done += take;
   }
   return thr;
+}
+
+__device__ __forceinline__ uint64_t wave_max64(uint64_t v) {
+#pragma unroll
+  for (int m = 32; m > 0; m >>= 1) {
+    const uint64_t o = shfl_xor64(v, m);
+    v = o > v ? o : v;
+  }
+  return v;
+}
+
+// Top-20 of up to 64 lists, each sorted descending with 20 keys (0 = empty),
+// list l at lists[l * 20].  One list per lane; 20 steps of "take the largest
+// head".  Lane i < 20 returns the i-th best key.  Keys are unique, so exactly
+// one lane owns each maximum.
+__device__ __forceinline__ uint64_t merge_sorted_lists(const uint64_t* lists, uint32_t nlists,
+                                                       uint32_t lane) {
+  uint32_t pos = 0;
+  uint64_t head = lane < nlists ? lists[lane * kTopK] : 0;
+  uint64_t mine = 0;
+#pragma unroll 1
+  for (int i = 0; i < kTopK; ++i) {
+    const uint64_t m = wave_max64(head);
+    if (lane == (uint32_t)i) mine = m;
+    if (m != 0 && head == m) {
+      ++pos;
+      head = pos < (uint32_t)kTopK ? lists[lane * kTopK + pos] : 0;
+    }
+  }
+  return mine;
 }
 
 }  // namespace pb

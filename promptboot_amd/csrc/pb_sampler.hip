@@ -18,9 +18,9 @@
 //                    running threshold: the penalty never raises a value, so
 //                    the unpenalised value is a valid upper bound.  With S == 1
 //                    the same workgroup finishes the row (softmax, top-p,
-//                    draw); otherwise it writes its 20 keys to the workspace.
-//   finalize_kernel  (S > 1) one wave per row merges the S x 20 keys and
-//                    finishes the row.
+//                    draw); otherwise it publishes its 20 keys and the last
+//                    slice of the row to finish (a per-row counter) merges
+//                    the S lists and finishes the row.
 //   writeback_kernel (in-place variant only) applies the penalty to the
 //                    caller's logits once per unique history id.
 //
@@ -44,6 +44,7 @@ constexpr uint32_t kWaves = kBlock / 64;
 constexpr uint32_t kRowF4 = kVocab / 4;             // 37,984 float4 per row
 constexpr uint32_t kRowWords = kVocab / 32;         // 4,748 bitmap words per row
 constexpr uint32_t kBufCap = 128;                   // candidate slots per wave
+constexpr uint32_t kMaxSegments = 32;               // slices per row, at most
 constexpr uint64_t kErrDetailFinite = (uint64_t)7 << 32;
 constexpr uint64_t kErrDetailToken = (uint64_t)2 << 32;
 
@@ -56,10 +57,18 @@ __device__ __forceinline__ uint32_t xcd_work_item(uint32_t block, uint32_t n) {
   return (block & 7u) * (n >> 3) + (block >> 3);
 }
 
+// Histories are Zipf-like: a few ids recur thousands of times, and atomics
+// to one LDS word serialise.  Testing the bit first leaves one atomic per
+// distinct id (plus the rare lanes that race on a fresh one).
+__device__ __forceinline__ void set_bit_once(uint32_t* word, uint32_t bit) {
+  if ((__hip_atomic_load(word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) & bit) == 0u)
+    atomicOr(word, bit);
+}
+
 __device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
 #pragma unroll
   for (int m = 32; m > 0; m >>= 1) {
-    const uint32_t o = (uint32_t)__shfl_xor((int)v, m, 64);
+    const uint32_t o = lane_xor(v, (uint32_t)m, lane_id());
     v = o < v ? o : v;
   }
   return v;
@@ -102,7 +111,7 @@ __device__ void finalize_row(const RowParams& p, uint32_t row, uint64_t key, uin
 
   const uint32_t id = key_id(key);
   const uint32_t vbits = key_value_bits(key);
-  const float maximum = f_of((uint32_t)__shfl((int)vbits, 0, 64));
+  const float maximum = f_of(bcast32(vbits, 0));
   float w = 0.0f;
   if (lane < (uint32_t)kTopK) {
     const float shifted = f_of(vbits) - maximum;
@@ -111,7 +120,7 @@ __device__ void finalize_row(const RowParams& p, uint32_t row, uint64_t key, uin
   double running = 0.0, mine = 0.0;
 #pragma unroll
   for (int i = 0; i < kTopK; ++i) {
-    const float wi = __shfl(w, i, 64);
+    const float wi = bcast_f32(w, (uint32_t)i);
     running = running + (double)wi;
     if (lane == (uint32_t)i) mine = running;
   }
@@ -119,13 +128,13 @@ __device__ void finalize_row(const RowParams& p, uint32_t row, uint64_t key, uin
   const float cutoff = (float)total * f_of(kTopPBits);
   const uint64_t stop = __ballot(lane < (uint32_t)kTopK && !(cutoff > (float)mine));
   const uint32_t kept = stop ? (uint32_t)__ffsll((unsigned long long)stop) : (uint32_t)kTopK;
-  const double kept_total = __shfl(mine, (int)kept - 1, 64);
+  const double kept_total = bcast_f64(mine, kept - 1);
   const uint32_t r24 = p.random_24[row];
   const float unit = (float)(r24 & 0x00ffffffu) / f_of(kTwoPow24Bits);
   const float target = (float)kept_total * unit;
   const uint64_t hit = __ballot(lane < kept && (float)mine > target);
   const uint32_t rank = hit ? (uint32_t)__ffsll((unsigned long long)hit) - 1 : kept - 1;
-  const uint32_t token = (uint32_t)__shfl((int)id, (int)rank, 64);
+  const uint32_t token = bcast32(id, rank);
 
   if (lane == 0) p.token[row] = token;
   if (p.err && lane < sizeof(pb_inference_error) / 4) {
@@ -156,6 +165,7 @@ __device__ void finalize_row(const RowParams& p, uint32_t row, uint64_t key, uin
 }
 
 typedef float v4f __attribute__((ext_vector_type(4)));
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 
 template <int F>
 __device__ __forceinline__ void load_chunk(v4f (&dst)[F], const v4f* __restrict__ rowp,
@@ -163,17 +173,19 @@ __device__ __forceinline__ void load_chunk(v4f (&dst)[F], const v4f* __restrict_
 #pragma unroll
   for (int j = 0; j < F; ++j) {
     const uint32_t f = base + (uint32_t)j * kBlock + tid;
-    dst[j] = f < f_hi ? rowp[f] : v4f{0.f, 0.f, 0.f, 0.f};
+    // Each logit is read exactly once: a non-temporal load keeps the stream
+    // from evicting the history and the workspace from the caches.
+    dst[j] = f < f_hi ? __builtin_nontemporal_load(rowp + f) : v4f{0.f, 0.f, 0.f, 0.f};
   }
 }
 
 template <int F, bool kFinalize>
 __global__ __launch_bounds__(kBlock) void segment_kernel(RowParams p) {
-  __shared__ uint32_t bm[kRowWords];
+  __shared__ __align__(16) uint32_t bm[kRowWords];
   __shared__ uint64_t top[kWaves][kTopK];
   __shared__ uint64_t buf[kWaves][kBufCap];
   __shared__ unsigned long long wg_thr;
-  __shared__ uint32_t bad_logit, bad_hist, nonfinite_seen;
+  __shared__ uint32_t bad_logit, bad_hist, nonfinite_seen, last_slice;
 
   const uint32_t n = p.rows * p.segs;
   const uint32_t item = xcd_work_item(blockIdx.x, n);
@@ -189,6 +201,14 @@ __global__ __launch_bounds__(kBlock) void segment_kernel(RowParams p) {
   const uint32_t e_span = (f_hi - f_lo) * 4u;
   const uint32_t nwords = e_span / 32u;
 
+  // The first chunk of logits is requested before the history is scanned, so
+  // the two streams overlap.
+  const v4f* __restrict__ rowp = reinterpret_cast<const v4f*>(p.logits + (size_t)row * p.ld);
+  const uint32_t chunk_f4 = kBlock * (uint32_t)F;
+  const uint32_t nchunks = (f_hi - f_lo + chunk_f4 - 1u) / chunk_f4;
+  v4f cur[F];
+  load_chunk<F>(cur, rowp, f_lo, f_hi, tid);
+
   // ---- phase 0: clear LDS state ----
   for (uint32_t i = tid; i < nwords; i += kBlock) bm[i] = 0u;
   if (tid < kWaves * kTopK) (&top[0][0])[tid] = 0u;
@@ -197,6 +217,7 @@ __global__ __launch_bounds__(kBlock) void segment_kernel(RowParams p) {
     bad_logit = kNone;
     bad_hist = kNone;
     nonfinite_seen = 0u;
+    last_slice = 0u;
   }
   __syncthreads();
 
@@ -210,20 +231,32 @@ __global__ __launch_bounds__(kBlock) void segment_kernel(RowParams p) {
   }
   uint32_t my_bad = kNone;
   if (p.hist_vec4) {
-    const uint4* h4 = reinterpret_cast<const uint4*>(hrow);
+    // kHistBatch uint4 loads per thread in flight at once: the scan is bound
+    // by HBM latency otherwise.
+    constexpr uint32_t kHistBatch = 8;
+    const v4u* h4 = reinterpret_cast<const v4u*>(hrow);
     const uint32_t n4 = (hist_len + 3u) / 4u;
-    for (uint32_t q4 = tid; q4 < n4; q4 += kBlock) {
-      const uint4 v = h4[q4];
-      const uint32_t ids[4] = {v.x, v.y, v.z, v.w};
+    for (uint32_t b4 = 0; b4 < n4; b4 += kHistBatch * kBlock) {
+      v4u v[kHistBatch];
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const uint32_t q = q4 * 4u + (uint32_t)c;
-        const uint32_t id = ids[c];
-        if (q < hist_len) {
-          if (id >= kVocab) {
-            my_bad = min(my_bad, q);
-          } else if (id - e_lo < e_span) {
-            atomicOr(&bm[(id - e_lo) >> 5], 1u << (id & 31u));
+      for (uint32_t u = 0; u < kHistBatch; ++u) {
+        const uint32_t q4 = b4 + u * kBlock + tid;
+        v[u] = q4 < n4 ? __builtin_nontemporal_load(h4 + q4) : v4u{0u, 0u, 0u, 0u};
+      }
+#pragma unroll
+      for (uint32_t u = 0; u < kHistBatch; ++u) {
+        const uint32_t q4 = b4 + u * kBlock + tid;
+        const uint32_t ids[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const uint32_t q = q4 * 4u + (uint32_t)c;
+          const uint32_t id = ids[c];
+          if (q < hist_len) {
+            if (id >= kVocab) {
+              my_bad = min(my_bad, q);
+            } else if (id - e_lo < e_span) {
+              set_bit_once(&bm[(id - e_lo) >> 5], 1u << (id & 31u));
+            }
           }
         }
       }
@@ -234,7 +267,7 @@ __global__ __launch_bounds__(kBlock) void segment_kernel(RowParams p) {
       if (id >= kVocab) {
         my_bad = min(my_bad, q);
       } else if (id - e_lo < e_span) {
-        atomicOr(&bm[(id - e_lo) >> 5], 1u << (id & 31u));
+        set_bit_once(&bm[(id - e_lo) >> 5], 1u << (id & 31u));
       }
     }
   }
@@ -249,17 +282,12 @@ __global__ __launch_bounds__(kBlock) void segment_kernel(RowParams p) {
   }
 
   // ---- phase 2: one streaming pass over the slice ----
-  const v4f* __restrict__ rowp = reinterpret_cast<const v4f*>(p.logits + (size_t)row * p.ld);
-  const uint32_t chunk_f4 = kBlock * (uint32_t)F;
-  const uint32_t nchunks = (f_hi - f_lo + chunk_f4 - 1u) / chunk_f4;
   uint64_t* my_top = top[wave];
   uint64_t* my_buf = buf[wave];
   uint64_t thr = 0;      // this wave's current 20th-best key (a lower bound)
   uint32_t cnt = 0;      // pending candidates in my_buf
   float nan_probe = 0.0f;
 
-  v4f cur[F];
-  load_chunk<F>(cur, rowp, f_lo, f_hi, tid);
   for (uint32_t c = 0; c < nchunks; ++c) {
     const uint32_t base = f_lo + c * chunk_f4;
     v4f nxt[F];
@@ -373,44 +401,74 @@ __global__ __launch_bounds__(kBlock) void segment_kernel(RowParams p) {
     __syncthreads();
   }
 
-  // ---- phase 3: workgroup top-20, then finish the row or publish the slice ----
-  if (wave == 0) {
-    merge_all(my_top, &top[1][0], (kWaves - 1) * (uint32_t)kTopK, lane);
-    const uint64_t key = lane < (uint32_t)kTopK ? my_top[lane] : 0;
-    if (kFinalize) {
-      finalize_row(p, row, key, bad_logit, bad_hist, lane);
-    } else {
-      const size_t slot = (size_t)row * p.segs + seg;
-      if (lane < (uint32_t)kTopK) p.part_keys[slot * kTopK + lane] = key;
-      if (lane == 0) {
-        p.part_meta[slot * 2 + 0] = bad_logit;
-        p.part_meta[slot * 2 + 1] = bad_hist;
-      }
+  // ---- phase 3: workgroup top-20 (two levels of bitonic merges) ----
+  uint64_t pair = 0;
+  if (wave < 2) pair = merge_two_lists(top[2 * wave], top[2 * wave + 1], lane);
+  __syncthreads();
+  if (wave < 2 && lane < (uint32_t)kTopK) top[wave][lane] = pair;
+  __syncthreads();
+  if (kFinalize) {
+    if (wave == 0) {
+      const uint64_t key = merge_two_lists(top[0], top[1], lane);
+      finalize_row(p, row, lane < (uint32_t)kTopK ? key : 0, bad_logit, bad_hist, lane);
     }
+    return;
+  }
+
+  // S > 1: publish this slice's top-20; the last slice of the row to finish
+  // merges all of them and finishes the row.  No workgroup ever waits for
+  // another: the per-row counter only elects which one does the merge.
+  // The slice lists cross XCDs (each XCD has its own L2), so they are written
+  // and read with agent-scope atomics, which go to the coherent level; the
+  // writer's release fence orders them before its counter increment, and the
+  // elected reader only loads them after seeing the final count.  No L2
+  // invalidation is needed, so the other slices keep their cached history.
+  if (wave == 0) {
+    const uint64_t key = merge_two_lists(top[0], top[1], lane);
+    const size_t slot = (size_t)row * p.segs + seg;
+    if (lane < (uint32_t)kTopK)
+      __hip_atomic_store(&p.part_keys[slot * kTopK + lane], key, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+    if (lane == 0) {
+      __hip_atomic_store(&p.part_meta[slot * 2 + 0], bad_logit, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(&p.part_meta[slot * 2 + 1], bad_hist, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    if (lane == 0) {
+      const uint32_t done = __hip_atomic_fetch_add(&p.row_done[row], 1u, __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_AGENT);
+      last_slice = done == p.segs - 1u ? 1u : 0u;
+    }
+  }
+  __syncthreads();
+  if (last_slice == 0u) return;
+  if (wave == 0) {
+    uint64_t* staged = reinterpret_cast<uint64_t*>(bm);  // the bitmap is no longer needed
+    const uint64_t* keys = p.part_keys + (size_t)row * p.segs * kTopK;
+    for (uint32_t i = lane; i < p.segs * (uint32_t)kTopK; i += 64)
+      staged[i] = __hip_atomic_load(&keys[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_wave_barrier();
+    const uint64_t merged = merge_sorted_lists(staged, p.segs, lane);
+    uint32_t first_bad = kNone;
+    for (uint32_t s = lane; s < p.segs; s += 64) {
+      const uint32_t b = __hip_atomic_load(&p.part_meta[((size_t)row * p.segs + s) * 2],
+                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      first_bad = b < first_bad ? b : first_bad;
+    }
+    first_bad = wave_min_u32(first_bad);
+    const uint32_t hist_bad = __hip_atomic_load(&p.part_meta[(size_t)row * p.segs * 2 + 1],
+                                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    finalize_row(p, row, lane < (uint32_t)kTopK ? merged : 0, first_bad, hist_bad, lane);
+    if (lane == 0)  // ready for the next launch
+      __hip_atomic_store(&p.row_done[row], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
-// One wave per row: merge the S published top-20 lists, then finish the row.
-__global__ __launch_bounds__(kBlock) void finalize_kernel(RowParams p) {
-  __shared__ uint64_t top[kWaves][kTopK];
-  const uint32_t lane = threadIdx.x & 63u;
-  const uint32_t wave = threadIdx.x >> 6;
-  const uint32_t row = blockIdx.x * kWaves + wave;
-  if (row >= p.rows) return;
-  const uint64_t* keys = p.part_keys + (size_t)row * p.segs * kTopK;
-  uint64_t* my_top = top[wave];
-  if (lane < (uint32_t)kTopK) my_top[lane] = keys[lane];
-  __builtin_amdgcn_wave_barrier();
-  merge_all(my_top, keys + kTopK, (p.segs - 1) * (uint32_t)kTopK, lane);
-  uint32_t bad_logit = kNone;
-  for (uint32_t s = lane; s < p.segs; s += 64) {
-    const uint32_t b = p.part_meta[((size_t)row * p.segs + s) * 2];
-    bad_logit = b < bad_logit ? b : bad_logit;
-  }
-  bad_logit = wave_min_u32(bad_logit);
-  const uint32_t bad_hist = p.part_meta[(size_t)row * p.segs * 2 + 1];
-  const uint64_t key = lane < (uint32_t)kTopK ? my_top[lane] : 0;
-  finalize_row(p, row, key, bad_logit, bad_hist, lane);
+__global__ __launch_bounds__(kBlock) void zero_kernel(uint32_t* words, size_t n) {
+  const size_t i = (size_t)blockIdx.x * kBlock + threadIdx.x;
+  if (i < n) words[i] = 0u;
 }
 
 // In-place penalty for successful rows (fp32_sse2.rs:1848-1876): the first
@@ -457,18 +515,18 @@ __global__ __launch_bounds__(kBlock) void writeback_kernel(WritebackParams p) {
 // ---- host-side launchers ----
 
 uint32_t segments_for_rows(uint32_t rows) {
-  // Enough workgroups to cover the 256 CUs several times over, but never more
-  // than 64 slices per row (the finalize merge grows with S).
+  // About 1024 workgroups for small batches (measured on MI355X: B=64 is
+  // fastest at 16 slices, B=1 at 32); one slice per row from B=1024 up.
   if (rows == 0) return 1;
-  uint32_t s = 2048u / rows;
+  uint32_t s = 1024u / rows;
   if (s < 1) s = 1;
-  if (s > 64) s = 64;
+  if (s > kMaxSegments) s = kMaxSegments;
   return s;
 }
 
 void plan_segments(uint32_t rows, uint32_t forced_segments, uint32_t* segs, uint32_t* seg_f4) {
   uint32_t s = forced_segments ? forced_segments : segments_for_rows(rows);
-  if (s > 64) s = 64;
+  if (s > kMaxSegments) s = kMaxSegments;
   uint32_t len = (kRowF4 + s - 1) / s;
   len = (len + 7u) & ~7u;  // slices start on a 32-element bitmap word
   *seg_f4 = len;
@@ -481,12 +539,47 @@ hipError_t launch_sample(const RowParams& p, hipStream_t stream) {
     hipLaunchKernelGGL((segment_kernel<kChunkF4, true>), dim3(blocks), dim3(kBlock), 0, stream, p);
   } else {
     hipLaunchKernelGGL((segment_kernel<kChunkF4, false>), dim3(blocks), dim3(kBlock), 0, stream, p);
-    hipLaunchKernelGGL(finalize_kernel, dim3((p.rows + kWaves - 1) / kWaves), dim3(kBlock), 0,
-                       stream, p);
   }
   return hipGetLastError();
 }
 
+hipError_t launch_zero(uint32_t* words, size_t n, hipStream_t stream) {
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(zero_kernel, dim3((uint32_t)((n + kBlock - 1) / kBlock)), dim3(kBlock), 0,
+                     stream, words, n);
+  return hipGetLastError();
+}
+
+// Lane-exchange and wave-reduction self-test (one wave): rows 0-5 hold the
+// value seen from lane ^ {1,2,4,8,16,32} for v = 7*lane + 3, rows 6-7 the
+// wave maximum of 64 distinct 64-bit keys, rows 8-9 those keys sorted
+// descending, row 10 the wave minimum of (13*lane mod 64) + 5.
+__global__ __launch_bounds__(64) void wave_selftest_kernel(uint32_t* out) {
+  const uint32_t lane = lane_id();
+  const uint32_t v = lane * 7u + 3u;
+  out[0 * 64 + lane] = lane_xor(v, 1, lane);
+  out[1 * 64 + lane] = lane_xor(v, 2, lane);
+  out[2 * 64 + lane] = lane_xor(v, 4, lane);
+  out[3 * 64 + lane] = lane_xor(v, 8, lane);
+  out[4 * 64 + lane] = lane_xor(v, 16, lane);
+  out[5 * 64 + lane] = lane_xor(v, 32, lane);
+  const uint64_t key = ((uint64_t)(lane * 2654435761u) << 32) | (lane ^ 0x55u);
+  const uint64_t m = wave_max64(key);
+  out[6 * 64 + lane] = (uint32_t)m;
+  out[7 * 64 + lane] = (uint32_t)(m >> 32);
+  const uint64_t s = wave_sort_desc(key, lane);
+  out[8 * 64 + lane] = (uint32_t)s;
+  out[9 * 64 + lane] = (uint32_t)(s >> 32);
+  out[10 * 64 + lane] = wave_min_u32((lane * 13u) % 64u + 5u);
+}
+
+hipError_t launch_wave_selftest(uint32_t* out, hipStream_t stream) {
+  hipLaunchKernelGGL(wave_selftest_kernel, dim3(1), dim3(64), 0, stream, out);
+  return hipGetLastError();
+}
+
+// Element-wise device arithmetic probe: which == 0 -> expf_ref, else the
+// single-logit repetition penalty.
 __global__ __launch_bounds__(kBlock) void probe_kernel(int which, const uint32_t* in,
                                                       uint32_t* out, size_t n) {
   const size_t i = (size_t)blockIdx.x * kBlock + threadIdx.x;

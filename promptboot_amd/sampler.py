@@ -101,6 +101,7 @@ EXPORTS = {
     "pb_context_set_segments": (None, [vp, u32]),
     "pb_device_expf_bits": (u32, [vp, vp, size_t, vp]),
     "pb_device_penalize_bits": (u32, [vp, vp, size_t, vp]),
+    "pb_device_wave_selftest": (u32, [vp, vp]),
     "pb_version": (ctypes.c_char_p, []),
 }
 
@@ -257,6 +258,7 @@ class BatchSampler:
         st = lib().pb_context_create(device, ctypes.byref(self._ctx))
         if st != OK:
             raise InferenceError(_Error(status=st))
+        self.segments = segments
         if segments:
             lib().pb_context_set_segments(self._ctx, segments)
 
@@ -272,6 +274,7 @@ class BatchSampler:
             pass
 
     def set_segments(self, segments: int) -> None:
+        self.segments = segments
         lib().pb_context_set_segments(self._ctx, segments)
 
     def sample(self, logits, random_24, history=None, history_len=None, *, token=None,

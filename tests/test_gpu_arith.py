@@ -27,6 +27,33 @@ def run_probe(fn, words: np.ndarray) -> np.ndarray:
     return out.cpu().numpy().view(np.uint32)
 
 
+def test_wave_lane_exchange_and_reductions():
+    """The selection's lane exchanges (DPP quad_perm / row_ror, gfx950
+    permlane16/32 swaps) must read exactly lane ^ j, and the wave max, sort
+    and min built on them must agree with numpy."""
+    import ctypes
+
+    import torch
+
+    from promptboot_amd import sampler as s
+
+    out = torch.zeros(11 * 64, dtype=torch.int32, device="cuda:0")
+    st = s.lib().pb_device_wave_selftest(ctypes.c_void_p(out.data_ptr()),
+                                         ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    assert st == 0
+    torch.cuda.synchronize()
+    o_ = out.cpu().numpy().view(np.uint32).reshape(11, 64).astype(np.uint64)
+    lane = np.arange(64, dtype=np.uint64)
+    for row, j in enumerate((1, 2, 4, 8, 16, 32)):
+        assert (o_[row] == ((lane ^ j) * 7 + 3)).all(), (j, o_[row][:20])
+    keys = ((lane * 2654435761) % 2**32 << 32) | (lane ^ 0x55)
+    got_max = o_[6] | (o_[7] << 32)
+    assert (got_max == keys.max()).all()
+    got_sorted = o_[8] | (o_[9] << 32)
+    assert (got_sorted == np.sort(keys)[::-1]).all()
+    assert (o_[10] == ((lane * 13) % 64 + 5).min()).all()
+
+
 def test_device_expf_on_softmax_domain():
     # Every (v - max) / 0.7 the sampler can form is <= 0: sweep all non-positive
     # binary32 values down to the underflow threshold at a prime stride, plus
