@@ -115,6 +115,17 @@ def lib() -> ctypes.CDLL:
         if not LIB_PATH.exists():
             raise ImportError(f"{LIB_PATH} is missing: build it with "
                               "`make -C promptboot_amd/csrc` (hipcc, gfx950)")
+        # One HIP runtime per process: torch wheels bundle their own
+        # libamdhip64 (SONAME libamdhip64.so.7, but requested by torch as
+        # "libamdhip64.so").  Loaded first, it satisfies this library's
+        # libamdhip64.so.7 dependency as well; loaded after /opt/rocm's copy,
+        # torch would map a second runtime that finds no GPU.  So torch, when
+        # installed, is imported before the library is opened; torch stream
+        # handles are then valid for the sampler's launches.
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         L = ctypes.CDLL(str(LIB_PATH))
         for name, (res, args) in EXPORTS.items():
             fn = getattr(L, name)

@@ -34,6 +34,15 @@ def test_library_exports_every_declared_function():
         assert getattr(lib, n) is not None
 
 
+def test_one_hip_runtime_is_mapped():
+    """The binding opens the library after torch, so torch's bundled
+    libamdhip64 serves both and the process holds a single HIP runtime."""
+    s.lib()
+    maps = pathlib.Path("/proc/self/maps").read_text().splitlines()
+    paths = {line.split()[-1] for line in maps if "libamdhip64" in line}
+    assert len(paths) == 1, paths
+
+
 def test_struct_layouts_match_the_reference(tmp_path):
     src = tmp_path / "layout.c"
     src.write_text("""
