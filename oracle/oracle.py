@@ -105,6 +105,15 @@ def lib() -> ctypes.CDLL:
                                        vp, vp, vp, vp, ctypes.c_int]
         L.pbo_time_batch.argtypes = [vp, size_t, u32, vp, size_t, vp, vp, vp]
         L.pbo_time_batch.restype = u64
+        L.pbo_half_to_f32_bits.argtypes = [ctypes.c_uint16]
+        L.pbo_half_to_f32_bits.restype = u32
+        L.pbo_f32_to_half_bits.argtypes = [u32]
+        L.pbo_f32_to_half_bits.restype = ctypes.c_uint16
+        L.pbo_prepare_q8.argtypes = [vp, vp, size_t]
+        L.pbo_q4_block_dot.argtypes = [vp, vp]
+        L.pbo_q4_block_dot.restype = ctypes.c_int32
+        L.pbo_q4_matvec_rows.argtypes = [vp, vp, vp, size_t, size_t]
+        L.pbo_lmhead_logits.argtypes = [vp, u32, vp, size_t, size_t, vp, ctypes.c_int]
         L.pbo_expf_array.argtypes = [vp, vp, size_t]
         L.pbo_penalize_array.argtypes = [vp, vp, size_t]
         for name in ("pbo_sizeof_detail", "pbo_sizeof_error", "pbo_sizeof_state"):
@@ -168,6 +177,52 @@ def time_batch(logits, hist, hist_len, seeds) -> tuple[float, np.ndarray]:
     ns = lib().pbo_time_batch(_ptr(lg), lg.shape[1], lg.shape[0], _ptr(h), h.shape[1],
                               _ptr(hl), _ptr(sd), _ptr(tok))
     return ns * 1e-9, tok
+
+
+Q8_STAGING_BYTES = 5184
+
+
+def half_to_f32_bits(h: int) -> int:
+    return lib().pbo_half_to_f32_bits(h & 0xFFFF)
+
+
+def f32_to_half_bits(bits: int) -> int:
+    return lib().pbo_f32_to_half_bits(bits & 0xFFFFFFFF)
+
+
+def prepare_q8(words, staging: np.ndarray | None = None) -> np.ndarray:
+    """inference_prepare_q8: returns the 5,184-byte staging area."""
+    x = _u32(words)
+    if staging is None:
+        staging = np.zeros(Q8_STAGING_BYTES, np.uint8)
+    lib().pbo_prepare_q8(_ptr(x), _ptr(staging), x.size)
+    return staging
+
+
+def q4_block_dot(weights16, activation32) -> int:
+    w = np.ascontiguousarray(weights16, dtype=np.uint8)
+    a = np.ascontiguousarray(activation32, dtype=np.int8)
+    return lib().pbo_q4_block_dot(_ptr(w), _ptr(a))
+
+
+def q4_matvec(weights: np.ndarray, staging: np.ndarray, rows: int, columns: int) -> np.ndarray:
+    w = np.ascontiguousarray(weights, dtype=np.uint8)
+    out = np.zeros(rows, np.uint32)
+    lib().pbo_q4_matvec_rows(_ptr(w), _ptr(out), _ptr(staging), rows, columns)
+    return out
+
+
+def lmhead_logits(hidden, weights: np.ndarray, vocab: int, columns: int,
+                  threads: int = 1) -> np.ndarray:
+    """Logits [rows, vocab] (uint32 words) of each hidden row through a Q4_0 head
+    in the reference layout (vocab rows of columns/32 blocks of 18 bytes)."""
+    h = _u32(hidden)
+    rows = h.shape[0]
+    w = np.ascontiguousarray(weights, dtype=np.uint8)
+    assert w.size == vocab * columns // 32 * 18
+    out = np.zeros((rows, vocab), np.uint32)
+    lib().pbo_lmhead_logits(_ptr(h), rows, _ptr(w), vocab, columns, _ptr(out), threads)
+    return out
 
 
 def expf_array(words) -> np.ndarray:

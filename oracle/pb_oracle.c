@@ -574,6 +574,157 @@ int pbo_sample_batch(const uint32_t *logits, size_t ld, size_t vocab, uint32_t r
     return 0;
 }
 
+/* ---- Q4_0 LM head with Q8_0 activations (fused LM head + sampler) ---- */
+
+/* half_to_f32_bits (fp32_sse2.rs:362-376). */
+uint32_t pbo_half_to_f32_bits(uint16_t bits) {
+    const uint32_t sign = (uint32_t)(bits & 0x8000u) << 16;
+    const uint32_t exponent = (bits >> 10) & 0x1fu;
+    const uint32_t fraction = bits & 0x03ffu;
+    if (exponent == 0 && fraction == 0) return sign;
+    if (exponent == 0) {
+        const uint32_t shift = (uint32_t)__builtin_clz(fraction) - 21u;
+        const uint32_t normalized = fraction << shift;
+        return sign | ((113u - shift) << 23) | ((normalized & 0x03ffu) << 13);
+    }
+    if (exponent == 31) return sign | 0x7f800000u | (fraction << 13);
+    return sign | ((exponent + 112u) << 23) | (fraction << 13);
+}
+
+/* f32_bits_to_half (fp32_sse2.rs:924-943): round-to-nearest-even through two
+ * power-of-two scalings and one biased add. */
+static uint16_t f32_bits_to_half(uint32_t bits) {
+    const uint32_t sign = (bits >> 16) & 0x8000u;
+    const uint32_t magnitude = bits & 0x7fffffffu;
+    const uint32_t base = bf(fb(magnitude) * fb(0x77800000u) * fb(0x08800000u));
+    const uint32_t doubled = bits + bits;
+    uint32_t bias = doubled & 0xff000000u;
+    if (bias < 0x71000000u) bias = 0x71000000u;
+    const uint32_t rounded = bf(fb((bias >> 1) + 0x07800000u) + fb(base));
+    const uint32_t exponent = (rounded >> 13) & 0x7c00u;
+    const uint32_t mantissa = rounded & 0x0fffu;
+    if (doubled > 0xff000000u) return (uint16_t)(sign | 0x7e00u);
+    return (uint16_t)(sign | (exponent + mantissa));
+}
+
+uint16_t pbo_f32_to_half_bits(uint32_t bits) {
+    const unsigned int saved = enter_fp();
+    const uint16_t h = f32_bits_to_half(bits);
+    exit_fp(saved);
+    return h;
+}
+
+/* round_half_away (fp32_sse2.rs:945-954). */
+static int32_t round_half_away(float value) {
+    const float half = bf(value) >> 31 == 0 ? fb(0x3f000000u) : fb(0xbf000000u);
+    return (int32_t)(value + half);
+}
+
+#define PBO_Q8_STAGING_BYTES 5184
+
+/* inference_prepare_q8 (fp32_sse2.rs:956-983): per 32-value block, scale =
+ * max|x| / 127 stored as fp16, quants = round_half_away(x * (1 / scale))
+ * stored as wrapping i8; staging cleared first.  34 bytes per block. */
+void pbo_prepare_q8(const uint32_t *input, uint8_t *staging, size_t columns) {
+    const unsigned int saved = enter_fp();
+    memset(staging, 0, PBO_Q8_STAGING_BYTES);
+    for (size_t block_index = 0; block_index < (columns >> 5); ++block_index) {
+        const uint32_t *x = input + block_index * 32;
+        uint8_t *block = staging + block_index * 34;
+        uint32_t maximum = 0;
+        for (int e = 0; e < 32; ++e) {
+            const uint32_t magnitude = x[e] & 0x7fffffffu;
+            if (greater(magnitude, maximum)) maximum = magnitude;
+        }
+        const float scale = fb(maximum) / fb(0x42fe0000u); /* / 127 */
+        const uint16_t h = f32_bits_to_half(bf(scale));
+        block[0] = (uint8_t)(h & 0xff);
+        block[1] = (uint8_t)(h >> 8);
+        const float inverse = bf(scale) == 0 ? 0.0f : fb(0x3f800000u) / scale;
+        for (int e = 0; e < 32; ++e) {
+            const int32_t q = round_half_away(fb(x[e]) * inverse);
+            block[2 + e] = (uint8_t)(int8_t)q;
+        }
+    }
+    exit_fp(saved);
+}
+
+/* Q4_0 x Q8_0 block dot (promptboot_inference_q4_block_dot,
+ * fp32_sse2.rs:998-1062; scalar form tests.rs:3962-3970): byte i holds element
+ * i in its low nibble and element 16 + i in its high nibble, zero point 8. */
+int32_t pbo_q4_block_dot(const uint8_t *weights16, const int8_t *activation32) {
+    int32_t total = 0;
+    for (int i = 0; i < 16; ++i) {
+        const uint8_t packed = weights16[i];
+        total += ((int32_t)(packed & 0x0f) - 8) * (int32_t)activation32[i];
+        total += ((int32_t)(packed >> 4) - 8) * (int32_t)activation32[16 + i];
+    }
+    return total;
+}
+
+/* inference_q4_matvec_rows_prepared (fp32_sse2.rs:1217-1248): per output row,
+ * total = add(total, mul(mul(f32(dot), weight_scale), activation_scale)) over
+ * the blocks in order.  Weight rows are columns/32 blocks of 18 bytes (fp16
+ * scale, 16 nibble bytes); `staging` is pbo_prepare_q8's output. */
+void pbo_q4_matvec_rows(const uint8_t *weights, uint32_t *output, const uint8_t *staging,
+                        size_t rows, size_t columns) {
+    const unsigned int saved = enter_fp();
+    const size_t blocks = columns >> 5;
+    for (size_t row = 0; row < rows; ++row) {
+        float total = 0.0f;
+        const uint8_t *row_base = weights + row * blocks * 18;
+        for (size_t b = 0; b < blocks; ++b) {
+            const uint8_t *block = row_base + b * 18;
+            const uint8_t *activation = staging + b * 34;
+            const int32_t integer = pbo_q4_block_dot(block + 2, (const int8_t *)(activation + 2));
+            const float ws = fb(pbo_half_to_f32_bits((uint16_t)(block[0] | (block[1] << 8))));
+            const float as =
+                fb(pbo_half_to_f32_bits((uint16_t)(activation[0] | (activation[1] << 8))));
+            const float scaled = (float)integer * ws;
+            total = total + scaled * as;
+        }
+        output[row] = bf(total);
+    }
+    exit_fp(saved);
+}
+
+typedef struct {
+    const uint32_t *hidden;
+    const uint8_t *weights;
+    uint32_t *logits;
+    size_t vocab, columns;
+    uint32_t row_begin, row_end;
+} lmhead_job;
+
+static void *lmhead_worker(void *arg) {
+    const lmhead_job *job = (const lmhead_job *)arg;
+    uint8_t *staging = (uint8_t *)malloc(PBO_Q8_STAGING_BYTES);
+    for (uint32_t r = job->row_begin; r < job->row_end; ++r) {
+        pbo_prepare_q8(job->hidden + (size_t)r * job->columns, staging, job->columns);
+        pbo_q4_matvec_rows(job->weights, job->logits + (size_t)r * job->vocab, staging, job->vocab,
+                           job->columns);
+    }
+    free(staging);
+    return NULL;
+}
+
+/* Logits of `rows` hidden states through the Q4_0 head: logits[r][v]. */
+void pbo_lmhead_logits(const uint32_t *hidden, uint32_t rows, const uint8_t *weights,
+                       size_t vocab, size_t columns, uint32_t *logits, int threads) {
+    if (threads < 1) threads = 1;
+    if ((uint32_t)threads > rows) threads = rows ? (int)rows : 1;
+    if (threads > 256) threads = 256;
+    pthread_t tid[256];
+    lmhead_job jobs[256];
+    for (int t = 0; t < threads; ++t) {
+        jobs[t] = (lmhead_job){hidden, weights, logits, vocab, columns,
+                               (uint32_t)((uint64_t)rows * t / threads),
+                               (uint32_t)((uint64_t)rows * (t + 1) / threads)};
+        pthread_create(&tid[t], NULL, lmhead_worker, &jobs[t]);
+    }
+    for (int t = 0; t < threads; ++t) pthread_join(tid[t], NULL);
+}
+
 /* Single-threaded CPU baseline timer.  For each row: copy the logits into a
  * private buffer and clear the scratch (untimed), then time one
  * sample_token_with_repetition call on them through its return, the timer
