@@ -160,12 +160,76 @@ def time_batch(smp, w: dict, steps: int, warmup: int) -> dict:
             "_tokens": tokens, "_detail": detail}
 
 
+MFMA_INT8_PEAK_TOPS = 5000.0     # dense int8 MFMA, MI355X
+VALU_LANE_OPS_PEAK = 256 * 4 * 16 * 2.4e9  # 32-bit VALU lane-ops/s, MI355X
+
+
+def time_lmhead(smp, steps: int, warmup: int) -> dict:
+    """Fused Q4_0 LM head + sampler, B=256 hidden states of width 896."""
+    import torch
+
+    from promptboot_amd import sampler as s
+    from promptboot_amd import workloads
+
+    w = workloads.make_lmhead(rows=256)
+    dev = torch.device("cuda:0")
+
+    def t(a):
+        return torch.from_numpy(np.ascontiguousarray(a).view(np.int32)).to(dev)
+
+    packed = smp.pack_lmhead(torch.from_numpy(w["q4"]).to(dev))
+    hidden, hist, hl, r24 = t(w["hidden"]), t(w["hist"]), t(w["hist_len"]), t(w["random_24"])
+    B = hidden.shape[0]
+    token = torch.empty(B, dtype=torch.int32, device=dev)
+    stream = torch.cuda.current_stream(dev)
+
+    def step():
+        smp.lmhead_sample(packed, hidden, r24, hist, hl, token=token, stream=stream)
+
+    step()
+    torch.cuda.synchronize()
+    t_settle = time.perf_counter()
+    while time.perf_counter() - t_settle < SETTLE_S:
+        for _ in range(4):
+            step()
+        torch.cuda.synchronize()
+    for _ in range(warmup):
+        step()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        starts[i].record(stream)
+        step()
+        ends[i].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    step_ms = float(np.mean([a.elapsed_time(b) for a, b in zip(starts, ends)]))
+    ops = 2.0 * B * workloads.VOCAB * workloads.HIDDEN
+    epilogue = 4.0 * B * workloads.VOCAB * (workloads.HIDDEN // 32)
+    alg = workloads.lmhead_algorithmic_bytes(B, w["hist_len"])
+    return {"rows": B, "ms_per_step": round(wall / steps * 1e3, 4),
+            "launch_ms": round(step_ms, 4),
+            "rows_per_s": round(B / (wall / steps), 1),
+            "int8_tops": round(ops / (step_ms / 1e3) / 1e12, 1),
+            "int8_mfma_frac": round(ops / (step_ms / 1e3) / 1e12 / MFMA_INT8_PEAK_TOPS, 4),
+            "epilogue_valu_frac": round(epilogue / (step_ms / 1e3) / VALU_LANE_OPS_PEAK, 4),
+            "hbm_gbs": round(alg / (step_ms / 1e3) / 1e9, 1),
+            "hbm_frac": round(alg / (step_ms / 1e3) / 1e9 / PEAK_HBM_GBS, 4),
+            "workload": "B=256 hidden N(0,1) x 896, Q4_0 head 151936x896 (fp16 scales "
+                        "U(0.001,0.02)), histories U[16,1024] Zipf; logits bit-exact to the "
+                        "reference Q4 head"}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-lmhead", action="store_true",
+                    help="skip the fused Q4_0 LM head + sampler timing")
     ap.add_argument("--batches", default="1,64,4096")
     ap.add_argument("--segments", type=int, default=0,
                     help="force the slices per row (0 = the library's choice)")
@@ -216,6 +280,10 @@ def main() -> int:
     for B in batches:
         log(f"timing B={B}")
         results[B] = time_batch(smp, work[B], args.steps, args.warmup)
+    lmhead = None
+    if not args.no_lmhead:
+        log("timing the fused Q4_0 LM head + sampler (B=256)")
+        lmhead = time_lmhead(smp, min(args.steps, 50), args.warmup)
     smp.close()
 
     main_res = results[head]
@@ -272,6 +340,7 @@ def main() -> int:
                    "rows": head, "vocab": 151936, "hist_ld": int(w["hist"].shape[1])},
         "tokens_per_s": round(main_res["rows_per_s"], 1),
         "by_batch": by_batch,
+        "lmhead_fused": lmhead,
         "roofline": roof,
         "cpu_baseline": cpu,
         "parity": parity,

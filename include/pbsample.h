@@ -188,6 +188,41 @@ uint32_t pb_sample_batch_inplace(pb_context *ctx, uint32_t *d_logits, size_t voc
                                  pb_sample_detail *d_detail, pb_inference_error *d_err,
                                  void *stream, pb_inference_error *err);
 
+/* ---- fused Q4_0 LM head + sampler ----
+ * Replaces, for a batch of hidden states, the reference's
+ * inference_prepare_q8 + inference_q4_matvec_rows_prepared
+ * (crates/promptboot-core/src/fp32_sse2.rs:956-983, 1217-1248) followed by
+ * sample_token_with_repetition (inference.rs:919-965) on each logits row.
+ * The logits are bit-identical to the reference's Q4 head (int8 MFMA for the
+ * exact block dots, the reference's per-block binary32 epilogue in order). */
+
+/* Bytes of the device layout of a Q4_0 head (equal to the source size:
+ * rows * cols / 32 blocks of 18 bytes). */
+size_t pb_lmhead_packed_bytes(size_t vocab, size_t cols);
+
+/* Repacks a Q4_0 matrix in promptboot's layout (vocab rows of cols/32 blocks
+ * of 18 bytes: fp16 scale, 16 nibble bytes with element i in the low and
+ * 16 + i in the high nibble; the token_embd layout of model.rs:810-812) into
+ * the device layout.  Device pointers; d_packed 16-byte aligned and
+ * pb_lmhead_packed_bytes long.  Done once per model, outside the decode step. */
+uint32_t pb_lmhead_pack_q4_0(const uint8_t *d_q4, size_t vocab, size_t cols, uint8_t *d_packed,
+                             void *stream, pb_inference_error *err);
+
+/* One decode step for `rows` sequences: hidden states (rows x cols binary32
+ * words) through the packed head, then the sampler exactly as pb_sample_batch
+ * on the resulting logits (repetition penalty, top-k 20, temperature 0.7,
+ * top-p 0.8, draw).  vocab must be PB_VOCAB, cols a multiple of 32 up to 2048
+ * (896 for Qwen2.5-0.5B).  d_logits (optional, rows x vocab words) receives the raw
+ * logits; without it they live in the context's workspace.  Per-row outputs
+ * and error records as pb_sample_batch (non-finite logit, bad history id). */
+uint32_t pb_lmhead_sample_batch(pb_context *ctx, const uint8_t *d_packed, size_t vocab,
+                                size_t cols, const uint32_t *d_hidden, uint32_t rows,
+                                const uint32_t *d_hist, size_t hist_ld,
+                                const uint32_t *d_hist_len, const uint32_t *d_random_24,
+                                uint32_t *d_token, pb_sample_detail *d_detail,
+                                pb_inference_error *d_err, uint32_t *d_logits, void *stream,
+                                pb_inference_error *err);
+
 /* Segments per row the batched sampler will use for `rows` (diagnostic). */
 uint32_t pb_segments_for_rows(uint32_t rows);
 
@@ -206,6 +241,10 @@ uint32_t pb_device_penalize_bits(const uint32_t *d_in, uint32_t *d_out, size_t n
 /* One-wave self-test of the lane exchanges (DPP, permlane swaps) and wave
  * reductions the selection uses; writes 11 x 64 words to d_out. */
 uint32_t pb_device_wave_selftest(uint32_t *d_out, void *stream);
+/* One-wave self-test of the int8 MFMA fragment layout the LM head uses:
+ * writes the 32 x 32 int32 product of A[i][k] = (7i + 3k) % 17 - 8 and
+ * B[k][j] = (5k + 11j) % 15 - 7 (k < 32) to d_out[32 i + j]. */
+uint32_t pb_device_mfma_selftest(int32_t *d_out, void *stream);
 
 /* Library version string and build target ("gfx950"). */
 const char *pb_version(void);

@@ -67,6 +67,9 @@ struct pb_context {
   size_t counter_bytes = 0;
   size_t list_bytes = 0;
 
+  void* d_lm = nullptr;  // fused LM head workspace
+  size_t lm_bytes = 0;
+
   // single-row staging
   uint32_t* d_row = nullptr;
   uint32_t* d_hist = nullptr;
@@ -135,8 +138,8 @@ static void release(pb_context* ctx) {
   if (!ctx) return;
   DeviceGuard guard(ctx->device);
   if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
-  void* dev[] = {ctx->d_work, ctx->d_row, ctx->d_hist, ctx->d_gather, ctx->d_small,
-                 ctx->d_detail, ctx->d_err, ctx->d_seen};
+  void* dev[] = {ctx->d_work, ctx->d_lm,     ctx->d_row,    ctx->d_hist, ctx->d_gather,
+                 ctx->d_small, ctx->d_detail, ctx->d_err, ctx->d_seen};
   for (void* p : dev)
     if (p) (void)hipFree(p);
   void* host[] = {ctx->h_row, ctx->h_hist, ctx->h_gather, ctx->h_small, ctx->h_detail,
@@ -329,6 +332,120 @@ uint32_t pb_sample_batch_inplace(pb_context* ctx, uint32_t* d_logits, size_t voc
   hipError_t e = pb::launch_writeback(w, s);
   if (e != hipSuccess) return device_error(err, e);
   return PB_OK;
+}
+
+// ---- fused Q4_0 LM head + sampler ----
+
+size_t pb_lmhead_packed_bytes(size_t vocab, size_t cols) { return vocab * (cols / 32) * 18; }
+
+uint32_t pb_lmhead_pack_q4_0(const uint8_t* d_q4, size_t vocab, size_t cols, uint8_t* d_packed,
+                             void* stream, pb_inference_error* err) {
+  clear_error(err);
+  if (cols == 0 || cols % 32 != 0 || vocab == 0 || vocab > 0xffffffffu) {
+    set_error(err, PB_CAPACITY, PB_DOMAIN_NONE, 32, cols, PB_FIELD_BYTES, 4);
+    return PB_CAPACITY;
+  }
+  if (((uintptr_t)d_packed & 15u) != 0) {
+    set_error(err, PB_ALIGNMENT, PB_DOMAIN_NONE, 16, (uintptr_t)d_packed & 15u,
+              PB_FIELD_ALIGNMENT, 1);
+    return PB_ALIGNMENT;
+  }
+  hipError_t e = pb::launch_lm_pack(d_q4, d_packed, (uint32_t)vocab, (uint32_t)(cols / 32),
+                                    static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? PB_OK : device_error(err, e);
+}
+
+uint32_t pb_lmhead_sample_batch(pb_context* ctx, const uint8_t* d_packed, size_t vocab,
+                                size_t cols, const uint32_t* d_hidden, uint32_t rows,
+                                const uint32_t* d_hist, size_t hist_ld,
+                                const uint32_t* d_hist_len, const uint32_t* d_random_24,
+                                uint32_t* d_token, pb_sample_detail* d_detail,
+                                pb_inference_error* d_err, uint32_t* d_logits, void* stream,
+                                pb_inference_error* err) {
+  clear_error(err);
+  if (vocab != PB_VOCAB) {
+    set_error(err, PB_CAPACITY, PB_DOMAIN_LOGITS, PB_VOCAB, vocab, PB_FIELD_LOGITS, 0);
+    return PB_CAPACITY;
+  }
+  // The head keeps every block's activation scales for 256 rows in 64 KB of
+  // LDS: up to 2,048 columns (Qwen2.5-0.5B has 896).
+  if (cols == 0 || cols % 32 != 0 || cols > 2048) {
+    set_error(err, PB_CAPACITY, PB_DOMAIN_NONE, 32, cols, PB_FIELD_BYTES, 4);
+    return PB_CAPACITY;
+  }
+  if (((uintptr_t)d_packed & 15u) != 0 || ((uintptr_t)d_logits & 15u) != 0) {
+    set_error(err, PB_ALIGNMENT, PB_DOMAIN_NONE, 16, 0, PB_FIELD_ALIGNMENT, 2);
+    return PB_ALIGNMENT;
+  }
+  if (rows == 0) return PB_OK;
+  if (d_packed == nullptr || d_hidden == nullptr || d_random_24 == nullptr ||
+      d_token == nullptr || (d_hist_len != nullptr && d_hist == nullptr)) {
+    set_error(err, PB_CAPACITY, PB_DOMAIN_ARGMAX, 1, 0, PB_FIELD_BYTES, 3);
+    return PB_CAPACITY;
+  }
+  const uint32_t rows_pad = (rows + 63u) & ~63u;
+  const uint32_t blocks = (uint32_t)(cols / 32);
+  auto align = [](size_t x) { return (x + 255) & ~(size_t)255; };
+  const size_t bitmap_b = align((size_t)rows * (PB_VOCAB / 32) * 4);
+  const size_t meta_b = align((size_t)rows * 8);
+  const size_t actq_b = align((size_t)blocks * rows_pad * 32);
+  const size_t acts_b = align((size_t)blocks * rows_pad * 4);
+  const size_t tile_b = align((size_t)rows * (PB_VOCAB / 64) * 8);
+  const size_t logit_b = d_logits ? 0 : align((size_t)rows * PB_VOCAB * 4);
+  const size_t need = bitmap_b + meta_b + actq_b + acts_b + tile_b + logit_b;
+  DeviceGuard guard(ctx->device);
+  if (need > ctx->lm_bytes) {
+    if (ctx->d_lm) {
+      hipError_t e = hipFree(ctx->d_lm);  // device-synchronising
+      ctx->d_lm = nullptr;
+      ctx->lm_bytes = 0;
+      if (e != hipSuccess) return device_error(err, e);
+    }
+    hipError_t e = hipMalloc(&ctx->d_lm, need);
+    if (e != hipSuccess) return device_error(err, e);
+    ctx->lm_bytes = need;
+  }
+  char* base = static_cast<char*>(ctx->d_lm);
+  pb::LmParams p;
+  p.weights = d_packed;
+  p.hidden = d_hidden;
+  p.rows = rows;
+  p.rows_pad = rows_pad;
+  p.cols = (uint32_t)cols;
+  p.hist = d_hist_len ? d_hist : nullptr;
+  p.hist_ld = hist_ld;
+  p.hist_len = d_hist_len;
+  p.bitmap = reinterpret_cast<uint32_t*>(base);
+  p.meta = reinterpret_cast<uint32_t*>(base + bitmap_b);
+  p.act_q = reinterpret_cast<int8_t*>(base + bitmap_b + meta_b);
+  p.act_s = reinterpret_cast<float*>(base + bitmap_b + meta_b + actq_b);
+  p.tilemax = reinterpret_cast<uint64_t*>(base + bitmap_b + meta_b + actq_b + acts_b);
+  p.logits = d_logits ? d_logits
+                      : reinterpret_cast<uint32_t*>(base + bitmap_b + meta_b + actq_b + acts_b +
+                                                    tile_b);
+  p.logits_ld = PB_VOCAB;
+
+  pb::RowParams rp;
+  memset(&rp, 0, sizeof rp);
+  rp.logits = p.logits;
+  rp.ld = PB_VOCAB;
+  rp.rows = rows;
+  rp.hist = p.hist;
+  rp.hist_ld = hist_ld;
+  rp.hist_len = d_hist_len;
+  rp.random_24 = d_random_24;
+  rp.token = d_token;
+  rp.detail = d_detail;
+  rp.err = d_err;
+  rp.segs = 1;
+  hipError_t e = pb::launch_lm_sample(p, rp, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? PB_OK : device_error(err, e);
+}
+
+uint32_t pb_device_mfma_selftest(int32_t* d_out, void* stream) {
+  return pb::launch_mfma_selftest(d_out, static_cast<hipStream_t>(stream)) == hipSuccess
+             ? PB_OK
+             : PB_DEVICE;
 }
 
 }  // extern "C"

@@ -44,6 +44,30 @@ struct WritebackParams {
   uint32_t* gather;        // rows x hist_ld final values at the history ids, or null
 };
 
+// Fused Q4_0 LM head + sampler (pb_lmhead.hip).
+struct LmParams {
+  const uint8_t* weights;   // packed head: [blocks][vocab][16] nibbles, [blocks][vocab] fp16
+  const uint32_t* hidden;   // rows x cols binary32 words
+  uint32_t rows;
+  uint32_t rows_pad;        // rows rounded up to 64
+  uint32_t cols;            // hidden width, multiple of 32
+  const uint32_t* hist;
+  size_t hist_ld;
+  const uint32_t* hist_len;
+  uint32_t* bitmap;         // rows x 4,748 history bitmap words
+  uint32_t* meta;           // rows x {first non-finite logit, first bad history position}
+  int8_t* act_q;            // [blocks][rows_pad][32] Q8_0 quants
+  float* act_s;             // [blocks][rows_pad] activation scales
+  uint32_t* logits;         // rows x logits_ld raw logits (binary32 words)
+  size_t logits_ld;
+  uint64_t* tilemax;        // rows x 2,374 largest penalised key per 64-id tile
+};
+
+hipError_t launch_lm_pack(const uint8_t* in, uint8_t* out, uint32_t vocab, uint32_t blocks,
+                          hipStream_t stream);
+hipError_t launch_lm_sample(const LmParams& p, const RowParams& rp, hipStream_t stream);
+hipError_t launch_mfma_selftest(int32_t* out, hipStream_t stream);
+
 uint32_t segments_for_rows(uint32_t rows);
 // forced_segments == 0 picks segments_for_rows(rows).
 void plan_segments(uint32_t rows, uint32_t forced_segments, uint32_t* segs, uint32_t* seg_f4);

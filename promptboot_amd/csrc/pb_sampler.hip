@@ -34,6 +34,7 @@
 
 #include "pb_device.h"
 #include "pb_internal.h"
+#include "pb_rows.h"
 
 #pragma clang fp contract(off)
 
@@ -45,8 +46,6 @@ constexpr uint32_t kRowF4 = kVocab / 4;             // 37,984 float4 per row
 constexpr uint32_t kRowWords = kVocab / 32;         // 4,748 bitmap words per row
 constexpr uint32_t kBufCap = 128;                   // candidate slots per wave
 constexpr uint32_t kMaxSegments = 32;               // slices per row, at most
-constexpr uint64_t kErrDetailFinite = (uint64_t)7 << 32;
-constexpr uint64_t kErrDetailToken = (uint64_t)2 << 32;
 
 // Block index -> work item.  Consecutive work items (the segments of one row,
 // and neighbouring rows) land on the same XCD, which the hardware picks
@@ -63,105 +62,6 @@ __device__ __forceinline__ uint32_t xcd_work_item(uint32_t block, uint32_t n) {
 __device__ __forceinline__ void set_bit_once(uint32_t* word, uint32_t bit) {
   if ((__hip_atomic_load(word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) & bit) == 0u)
     atomicOr(word, bit);
-}
-
-__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
-#pragma unroll
-  for (int m = 32; m > 0; m >>= 1) {
-    const uint32_t o = lane_xor(v, (uint32_t)m, lane_id());
-    v = o < v ? o : v;
-  }
-  return v;
-}
-
-// Finishes one row on one wave: lanes 0..19 hold the row's top-20 keys in
-// rank order.  Softmax weights, top-p cutoff and the categorical draw follow
-// fp32_sse2.rs:1818-1845 operation for operation; the binary64 sums run as a
-// lane-serial chain in rank order, so every partial sum is the reference's.
-__device__ void finalize_row(const RowParams& p, uint32_t row, uint64_t key, uint32_t bad_logit,
-                             uint32_t bad_hist, uint32_t lane) {
-  if (bad_logit != kNone || bad_hist != kNone) {
-    pb_inference_error e;
-    e.layer = PB_NO_LAYER;
-    e.position = 0;
-    e.tensor_id = PB_NO_TENSOR;
-    e.reserved = 0;
-    e.domain = PB_DOMAIN_ARGMAX;
-    if (bad_logit != kNone) {
-      e.status = PB_NONFINITE_OUTPUT;
-      e.needed = 0;
-      e.available = p.logits[(size_t)row * p.ld + bad_logit];
-      e.detail = kErrDetailFinite | bad_logit;
-    } else {
-      e.status = PB_TOKEN_ID;
-      e.needed = kVocab;
-      e.available = p.hist[(size_t)row * p.hist_ld + bad_hist];
-      e.detail = kErrDetailToken;
-    }
-    if (lane == 0) {
-      p.token[row] = kNone;
-      if (p.err) p.err[row] = e;
-    }
-    if (p.detail) {
-      uint32_t* d = reinterpret_cast<uint32_t*>(p.detail + row);
-      for (uint32_t i = lane; i < sizeof(pb_sample_detail) / 4; i += 64) d[i] = 0xffffffffu;
-    }
-    return;
-  }
-
-  const uint32_t id = key_id(key);
-  const uint32_t vbits = key_value_bits(key);
-  const float maximum = f_of(bcast32(vbits, 0));
-  float w = 0.0f;
-  if (lane < (uint32_t)kTopK) {
-    const float shifted = f_of(vbits) - maximum;
-    w = expf_ref(shifted / f_of(kTemperatureBits));
-  }
-  double running = 0.0, mine = 0.0;
-#pragma unroll
-  for (int i = 0; i < kTopK; ++i) {
-    const float wi = bcast_f32(w, (uint32_t)i);
-    running = running + (double)wi;
-    if (lane == (uint32_t)i) mine = running;
-  }
-  const double total = running;
-  const float cutoff = (float)total * f_of(kTopPBits);
-  const uint64_t stop = __ballot(lane < (uint32_t)kTopK && !(cutoff > (float)mine));
-  const uint32_t kept = stop ? (uint32_t)__ffsll((unsigned long long)stop) : (uint32_t)kTopK;
-  const double kept_total = bcast_f64(mine, kept - 1);
-  const uint32_t r24 = p.random_24[row];
-  const float unit = (float)(r24 & 0x00ffffffu) / f_of(kTwoPow24Bits);
-  const float target = (float)kept_total * unit;
-  const uint64_t hit = __ballot(lane < kept && (float)mine > target);
-  const uint32_t rank = hit ? (uint32_t)__ffsll((unsigned long long)hit) - 1 : kept - 1;
-  const uint32_t token = bcast32(id, rank);
-
-  if (lane == 0) p.token[row] = token;
-  if (p.err && lane < sizeof(pb_inference_error) / 4) {
-    reinterpret_cast<uint32_t*>(p.err + row)[lane] = 0u;
-  }
-  if (p.detail) {
-    const double draw_tol = 1e-6 * (double)(float)kept_total;
-    const double cut_tol = 1e-6 * (double)(float)total;
-    const double pm = (double)(float)mine;
-    const bool near_draw = lane < kept && __builtin_fabs(pm - (double)target) <= draw_tol;
-    const bool near_cut = lane < (uint32_t)kTopK && __builtin_fabs(pm - (double)cutoff) <= cut_tol;
-    const uint32_t flags = (__ballot(near_draw) ? kFlagDrawBoundary : 0u) |
-                           (__ballot(near_cut) ? kFlagCutoffBoundary : 0u);
-    pb_sample_detail* d = p.detail + row;
-    if (lane < (uint32_t)kTopK) {
-      d->ids[lane] = id;
-      d->value_bits[lane] = vbits;
-      d->weight_bits[lane] = b_of(w);
-      d->probs[lane] = lane < kept ? (float)((double)w / kept_total) : 0.0f;
-    }
-    if (lane == 0) {
-      d->kept = kept;
-      d->rank = rank;
-      d->flags = flags;
-      d->token = token;
-    }
-  }
 }
 
 typedef float v4f __attribute__((ext_vector_type(4)));

@@ -102,6 +102,12 @@ EXPORTS = {
     "pb_device_expf_bits": (u32, [vp, vp, size_t, vp]),
     "pb_device_penalize_bits": (u32, [vp, vp, size_t, vp]),
     "pb_device_wave_selftest": (u32, [vp, vp]),
+    "pb_device_mfma_selftest": (u32, [vp, vp]),
+    "pb_lmhead_packed_bytes": (size_t, [size_t, size_t]),
+    "pb_lmhead_pack_q4_0": (u32, [vp, size_t, size_t, vp, vp, ctypes.POINTER(_Error)]),
+    "pb_lmhead_sample_batch": (
+        u32, [vp, vp, size_t, size_t, vp, u32, vp, size_t, vp, vp, vp, vp, vp, vp, vp,
+              ctypes.POINTER(_Error)]),
     "pb_version": (ctypes.c_char_p, []),
 }
 
@@ -312,6 +318,41 @@ class BatchSampler:
                 self._ctx, p(logits), VOCAB, ld, rows, p(history), hist_ld, p(history_len),
                 p(random_24), p(token), p(detail), p(err), ctypes.c_void_p(s.cuda_stream),
                 ctypes.byref(e))
+        _check(st, e)
+
+    def pack_lmhead(self, q4_weights, vocab: int = VOCAB, cols: int = 896, stream=None):
+        """Repacks a Q4_0 head (torch uint8 device tensor in promptboot's
+        layout) into the device layout; returns the packed uint8 tensor."""
+        import torch
+
+        packed = torch.empty(lib().pb_lmhead_packed_bytes(vocab, cols), dtype=torch.uint8,
+                             device=q4_weights.device)
+        s = stream if stream is not None else torch.cuda.current_stream(q4_weights.device)
+        e = _Error()
+        st = lib().pb_lmhead_pack_q4_0(ctypes.c_void_p(q4_weights.data_ptr()), vocab, cols,
+                                       ctypes.c_void_p(packed.data_ptr()),
+                                       ctypes.c_void_p(s.cuda_stream), ctypes.byref(e))
+        _check(st, e)
+        return packed
+
+    def lmhead_sample(self, packed, hidden, random_24, history=None, history_len=None, *,
+                      token, detail=None, err=None, logits=None, cols: int = 896,
+                      stream=None) -> None:
+        """Enqueues the fused Q4_0 LM head + sampler for hidden [B, cols]."""
+        import torch
+
+        rows = hidden.shape[0]
+        hist_ld = history.shape[1] if history is not None else 0
+        s = stream if stream is not None else torch.cuda.current_stream(hidden.device)
+        e = _Error()
+
+        def p(t):
+            return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+        st = lib().pb_lmhead_sample_batch(
+            self._ctx, p(packed), VOCAB, cols, p(hidden), rows, p(history), hist_ld,
+            p(history_len), p(random_24), p(token), p(detail), p(err), p(logits),
+            ctypes.c_void_p(s.cuda_stream), ctypes.byref(e))
         _check(st, e)
 
     def sample_rows(self, logits, history, history_len, states: list[SamplingState],

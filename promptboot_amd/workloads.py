@@ -128,6 +128,36 @@ def make(name: str, rows: int | None = None, seed: int = 20240601, base_seed: in
                 random_24=next_24_stream(seeds), seeds=seeds)
 
 
+HIDDEN = 896
+
+
+def make_lmhead(rows: int = 256, seed: int = 20240601, base_seed: int = 42) -> dict:
+    """Fused LM head workload: hidden states [rows, 896] ~ N(0, 1); a Q4_0 head
+    of 151,936 x 896 in promptboot's layout (vocab rows of 28 blocks of 18
+    bytes: fp16 scale ~ U(0.001, 0.02), 16 random nibble bytes); histories as
+    in `small` (length ~ U[16, 1024], Zipf ids); one uniform per row."""
+    rng = np.random.default_rng([seed, 99])
+    blocks = HIDDEN // 32
+    hidden = rng.standard_normal((rows, HIDDEN), dtype=np.float32)
+    q4 = np.empty((VOCAB, blocks, 18), np.uint8)
+    scales = rng.uniform(0.001, 0.02, (VOCAB, blocks)).astype(np.float16)
+    q4[:, :, 0:2] = scales.view(np.uint8).reshape(VOCAB, blocks, 2)
+    q4[:, :, 2:] = rng.integers(0, 256, (VOCAB, blocks, 16), dtype=np.uint8)
+    lengths = rng.integers(16, 1025, rows).astype(np.uint32)
+    hist = zipf_history(rng, lengths, 1024)
+    seeds = np.uint64(base_seed) + np.arange(rows, dtype=np.uint64)
+    return dict(name="lmhead", hidden=hidden, q4=q4.reshape(-1), hist=hist, hist_len=lengths,
+                random_24=next_24_stream(seeds), seeds=seeds)
+
+
+def lmhead_algorithmic_bytes(rows: int, hist_len: np.ndarray) -> int:
+    """HBM bytes of one fused step: the Q4_0 head once (18 B per 32 weights),
+    the hidden states, the valid history ids, and per-row length, uniform and
+    token words."""
+    return (VOCAB * HIDDEN // 32 * 18 + rows * HIDDEN * 4 + 12 * rows
+            + 4 * int(np.asarray(hist_len, np.int64).sum()))
+
+
 def algorithmic_bytes(hist_len: np.ndarray) -> int:
     """HBM bytes the path must move per batch: every logit once, every valid
     history id once, plus the per-row length, uniform and token words."""
