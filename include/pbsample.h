@@ -26,6 +26,11 @@
  *     pb_top_logits_8;
  *   - batched device entry points (pointers to device memory, asynchronous on
  *     the given HIP stream): pb_sample_batch, pb_sample_batch_inplace;
+ *   - the fused Q4_0 LM head + sampler: pb_lmhead_pack_q4_0,
+ *     pb_lmhead_sample_batch;
+ *   - one step of the REPL's decode loop for many sequences
+ *     (src/model_repl.rs:928-1150): pb_decode_step, pb_lmhead_decode_step,
+ *     with the host helpers pb_decode_draw and pb_decode_settle;
  *   - host PRNG helpers: pb_sampling_state_new, pb_next_24, pb_fill_random_24.
  */
 #ifndef PBSAMPLE_H
@@ -222,6 +227,66 @@ uint32_t pb_lmhead_sample_batch(pb_context *ctx, const uint8_t *d_packed, size_t
                                 uint32_t *d_token, pb_sample_detail *d_detail,
                                 pb_inference_error *d_err, uint32_t *d_logits, void *stream,
                                 pb_inference_error *err);
+
+/* ---- decode loop (src/model_repl.rs:928-1150) ----
+ * One generation step for `rows` sequences at once, with the REPL's caller
+ * contract kept on the device:
+ *   - the history handed to the sampler is the row's whole working context
+ *     (prompt + generated so far: working[..prompt_count + generated],
+ *     model_repl.rs:961-968);
+ *   - a sampled token is appended to that context; an end-of-sequence piece
+ *     (<|im_end|> 151645 or <|endoftext|> 151643, tokenizer.rs:38-39, 1047)
+ *     is stored as <|im_end|> and ends the row (model_repl.rs:1099-1103,
+ *     1119-1150);
+ *   - a row whose context reaches its length limit ends (the REPL's
+ *     MAX_NEW_TOKENS / CONTEXT_LIMIT stop);
+ *   - a row error ends the row with no append and no draw.
+ * Row states (d_row_state, one word per row, updated in place): */
+enum pb_row_state {
+  PB_ROW_ACTIVE = 0, /* sampled this step */
+  PB_ROW_EOS = 1,    /* ended on an end-of-sequence piece */
+  PB_ROW_LIMIT = 2,  /* context reached its length limit */
+  PB_ROW_ERROR = 3   /* the sampler returned an error (record in d_err) */
+};
+#define PB_IM_END 151645u      /* IM_END, src/repl_contract.rs:26 */
+#define PB_END_OF_TEXT 151643u /* END_OF_TEXT, tokenizer.rs:39 */
+
+/* Samples every row whose state is PB_ROW_ACTIVE, exactly as pb_sample_batch,
+ * then appends the token to d_hist[row] at d_hist_len[row] and increments
+ * d_hist_len[row].  d_max_len (optional) caps each row's context length
+ * (default hist_ld): the append that reaches it ends the row with
+ * PB_ROW_LIMIT.  Rows in any other state are skipped: their token is
+ * PB_NO_TOKEN, their detail and error records are not written, and they
+ * consume no uniform.  d_hist and d_hist_len are required. */
+uint32_t pb_decode_step(pb_context *ctx, const uint32_t *d_logits, size_t vocab, size_t ld,
+                        uint32_t rows, uint32_t *d_hist, size_t hist_ld, uint32_t *d_hist_len,
+                        const uint32_t *d_max_len, uint32_t *d_row_state,
+                        const uint32_t *d_random_24, uint32_t *d_token,
+                        pb_sample_detail *d_detail, pb_inference_error *d_err, void *stream,
+                        pb_inference_error *err);
+
+/* The same step with the fused Q4_0 LM head in front (pb_lmhead_sample_batch
+ * for the active rows, then the decode-loop bookkeeping above). */
+uint32_t pb_lmhead_decode_step(pb_context *ctx, const uint8_t *d_packed, size_t vocab,
+                               size_t cols, const uint32_t *d_hidden, uint32_t rows,
+                               uint32_t *d_hist, size_t hist_ld, uint32_t *d_hist_len,
+                               const uint32_t *d_max_len, uint32_t *d_row_state,
+                               const uint32_t *d_random_24, uint32_t *d_token,
+                               pb_sample_detail *d_detail, pb_inference_error *d_err,
+                               uint32_t *d_logits, void *stream, pb_inference_error *err);
+
+/* Host side of a step: saves every states[i] into saved[i]; for each row with
+ * row_state[i] == PB_ROW_ACTIVE writes out[i] = pb_next_24(&states[i]); other
+ * rows keep their state and get out[i] = 0.  The REPL draws once per sampled
+ * token and never for a failed sample (inference.rs:954-963). */
+void pb_decode_draw(pb_sampling_state *states, const uint32_t *row_state, uint32_t rows,
+                    uint32_t *out, pb_sampling_state *saved);
+/* After the step: rows that were PB_ROW_ACTIVE before it and are
+ * PB_ROW_ERROR after it get their saved state back (the failed sample
+ * consumed no draw).  Returns the number of rows restored. */
+uint32_t pb_decode_settle(pb_sampling_state *states, const pb_sampling_state *saved,
+                          const uint32_t *state_before, const uint32_t *state_after,
+                          uint32_t rows);
 
 /* Segments per row the batched sampler will use for `rows` (diagnostic). */
 uint32_t pb_segments_for_rows(uint32_t rows);

@@ -318,3 +318,59 @@ def sample_batch(logits: np.ndarray, hist: np.ndarray | None, hist_len: np.ndarr
     lib().pbo_sample_batch(_ptr(lg), ld, vocab, B, _ptr(h), hld, _ptr(hl), _ptr(r),
                            _ptr(tok), _ptr(det), _ptr(err), _ptr(pen), threads)
     return tok, det, err, pen
+
+
+IM_END = 151_645       # src/repl_contract.rs:26
+END_OF_TEXT = 151_643  # crates/promptboot-core/src/tokenizer.rs:39
+
+
+class DecodeRow:
+    """One sequence through the REPL's generation loop, restated from
+    src/model_repl.rs:928-1150 with the model replaced by the caller's logits:
+
+    * the sampler sees the whole working context, working[..prompt_count +
+      generated] (:961-968), with the session's `seen` scratch and the boot's
+      SamplingState;
+    * a sampler error ends the turn; nothing is appended (:989-996);
+    * the context receives the token, or IM_END when the piece is an
+      end-of-sequence one (:1099-1103; tokenizer.rs:1047 classes IM_END and
+      END_OF_TEXT as EOS), then generated += 1 (:1114);
+    * the turn ends on end-of-sequence (:1119-1150) or once generated reaches
+      the generation limit (the `while generated < generation_limit` of :928).
+    """
+
+    def __init__(self, prompt, seed: int, limit: int, state: SamplingState | None = None):
+        self.working = [int(t) for t in prompt]
+        self.prompt_count = len(self.working)
+        self.generated = 0
+        self.limit = int(limit)
+        # one SamplingState per boot, kept across turns (model_repl.rs:333-334)
+        self.state = state if state is not None else SamplingState(seed)
+        self.seen = np.zeros(SEEN_BYTES, np.uint8)
+        self.reason = None if self.limit > 0 else "LIMIT"
+        self.error: list[int] | None = None
+        self.tokens: list[int] = []
+
+    def active(self) -> bool:
+        return self.reason is None
+
+    def step(self, logits) -> int | None:
+        """Samples one token from `logits` (not modified); None once ended."""
+        if not self.active():
+            return None
+        row = _u32(logits).copy()
+        st, tok, err = sample_token_with_repetition(
+            row, self.working[:self.prompt_count + self.generated], self.seen, self.state)
+        if st != 0:
+            self.reason = "ERROR"
+            self.error = err.tuple()
+            return None
+        eos = tok in (IM_END, END_OF_TEXT)
+        self.working.append(IM_END if eos else tok)
+        self.tokens.append(tok)
+        self.generated += 1
+        if eos:
+            self.reason = "EOS"
+        elif self.generated >= self.limit:
+            self.reason = "LIMIT"
+        return tok

@@ -236,13 +236,37 @@ void pb_context_destroy(pb_context* ctx) { release(ctx); }
 
 }  // extern "C"
 
-// Validates and enqueues one batched sample (both variants).
+// Decode-loop arguments of pb_decode_step / pb_lmhead_decode_step.
+struct DecodeArgs {
+  uint32_t* hist;
+  uint32_t* hist_len;
+  const uint32_t* max_len;
+  uint32_t* row_state;
+};
+
+static void set_decode(pb::RowParams& p, const DecodeArgs* dec) {
+  p.row_state = dec ? dec->row_state : nullptr;
+  p.hist_out = dec ? dec->hist : nullptr;
+  p.hist_len_out = dec ? dec->hist_len : nullptr;
+  p.max_len = dec ? dec->max_len : nullptr;
+}
+
+static bool decode_args_ok(const DecodeArgs& dec, pb_inference_error* err) {
+  if (dec.hist == nullptr || dec.hist_len == nullptr || dec.row_state == nullptr) {
+    set_error(err, PB_CAPACITY, PB_DOMAIN_ARGMAX, 1, 0, PB_FIELD_BYTES, 5);
+    return false;
+  }
+  return true;
+}
+
+// Validates and enqueues one batched sample (every variant).
 static uint32_t enqueue_sample(pb_context* ctx, const uint32_t* d_logits, size_t vocab, size_t ld,
                                uint32_t rows, const uint32_t* d_hist, size_t hist_ld,
                                const uint32_t* d_hist_len, const uint32_t* d_random_24,
                                const uint8_t* d_excl, uint32_t* d_token,
                                pb_sample_detail* d_detail, pb_inference_error* d_err,
-                               hipStream_t stream, pb_inference_error* err) {
+                               hipStream_t stream, pb_inference_error* err,
+                               const DecodeArgs* dec = nullptr) {
   clear_error(err);
   if (vocab != PB_VOCAB) {
     // logits_error (inference.rs:737-754)
@@ -264,7 +288,7 @@ static uint32_t enqueue_sample(pb_context* ctx, const uint32_t* d_logits, size_t
     set_error(err, PB_CAPACITY, PB_DOMAIN_ARGMAX, 1, 0, PB_FIELD_BYTES, 3);
     return PB_CAPACITY;
   }
-  pb::RowParams p;
+  pb::RowParams p{};
   p.logits = d_logits;
   p.ld = ld;
   p.rows = rows;
@@ -281,6 +305,7 @@ static uint32_t enqueue_sample(pb_context* ctx, const uint32_t* d_logits, size_t
   p.part_keys = nullptr;
   p.part_meta = nullptr;
   p.row_done = nullptr;
+  set_decode(p, dec);
   DeviceGuard guard(ctx->device);
   if (p.segs > 1) {
     const size_t slots = (size_t)rows * p.segs;
@@ -355,13 +380,15 @@ uint32_t pb_lmhead_pack_q4_0(const uint8_t* d_q4, size_t vocab, size_t cols, uin
   return e == hipSuccess ? PB_OK : device_error(err, e);
 }
 
-uint32_t pb_lmhead_sample_batch(pb_context* ctx, const uint8_t* d_packed, size_t vocab,
-                                size_t cols, const uint32_t* d_hidden, uint32_t rows,
-                                const uint32_t* d_hist, size_t hist_ld,
-                                const uint32_t* d_hist_len, const uint32_t* d_random_24,
-                                uint32_t* d_token, pb_sample_detail* d_detail,
-                                pb_inference_error* d_err, uint32_t* d_logits, void* stream,
-                                pb_inference_error* err) {
+}  // extern "C"
+
+static uint32_t enqueue_lmhead(pb_context* ctx, const uint8_t* d_packed, size_t vocab,
+                               size_t cols, const uint32_t* d_hidden, uint32_t rows,
+                               const uint32_t* d_hist, size_t hist_ld,
+                               const uint32_t* d_hist_len, const uint32_t* d_random_24,
+                               uint32_t* d_token, pb_sample_detail* d_detail,
+                               pb_inference_error* d_err, uint32_t* d_logits, void* stream,
+                               pb_inference_error* err, const DecodeArgs* dec) {
   clear_error(err);
   if (vocab != PB_VOCAB) {
     set_error(err, PB_CAPACITY, PB_DOMAIN_LOGITS, PB_VOCAB, vocab, PB_FIELD_LOGITS, 0);
@@ -438,8 +465,73 @@ uint32_t pb_lmhead_sample_batch(pb_context* ctx, const uint8_t* d_packed, size_t
   rp.detail = d_detail;
   rp.err = d_err;
   rp.segs = 1;
+  set_decode(rp, dec);
   hipError_t e = pb::launch_lm_sample(p, rp, static_cast<hipStream_t>(stream));
   return e == hipSuccess ? PB_OK : device_error(err, e);
+}
+
+extern "C" {
+
+uint32_t pb_lmhead_sample_batch(pb_context* ctx, const uint8_t* d_packed, size_t vocab,
+                                size_t cols, const uint32_t* d_hidden, uint32_t rows,
+                                const uint32_t* d_hist, size_t hist_ld,
+                                const uint32_t* d_hist_len, const uint32_t* d_random_24,
+                                uint32_t* d_token, pb_sample_detail* d_detail,
+                                pb_inference_error* d_err, uint32_t* d_logits, void* stream,
+                                pb_inference_error* err) {
+  return enqueue_lmhead(ctx, d_packed, vocab, cols, d_hidden, rows, d_hist, hist_ld, d_hist_len,
+                        d_random_24, d_token, d_detail, d_err, d_logits, stream, err, nullptr);
+}
+
+// ---- decode loop (src/model_repl.rs:928-1150) ----
+
+uint32_t pb_decode_step(pb_context* ctx, const uint32_t* d_logits, size_t vocab, size_t ld,
+                        uint32_t rows, uint32_t* d_hist, size_t hist_ld, uint32_t* d_hist_len,
+                        const uint32_t* d_max_len, uint32_t* d_row_state,
+                        const uint32_t* d_random_24, uint32_t* d_token,
+                        pb_sample_detail* d_detail, pb_inference_error* d_err, void* stream,
+                        pb_inference_error* err) {
+  clear_error(err);
+  const DecodeArgs dec{d_hist, d_hist_len, d_max_len, d_row_state};
+  if (rows != 0 && !decode_args_ok(dec, err)) return PB_CAPACITY;
+  return enqueue_sample(ctx, d_logits, vocab, ld, rows, d_hist, hist_ld, d_hist_len, d_random_24,
+                        nullptr, d_token, d_detail, d_err, static_cast<hipStream_t>(stream), err,
+                        &dec);
+}
+
+uint32_t pb_lmhead_decode_step(pb_context* ctx, const uint8_t* d_packed, size_t vocab,
+                               size_t cols, const uint32_t* d_hidden, uint32_t rows,
+                               uint32_t* d_hist, size_t hist_ld, uint32_t* d_hist_len,
+                               const uint32_t* d_max_len, uint32_t* d_row_state,
+                               const uint32_t* d_random_24, uint32_t* d_token,
+                               pb_sample_detail* d_detail, pb_inference_error* d_err,
+                               uint32_t* d_logits, void* stream, pb_inference_error* err) {
+  clear_error(err);
+  const DecodeArgs dec{d_hist, d_hist_len, d_max_len, d_row_state};
+  if (rows != 0 && !decode_args_ok(dec, err)) return PB_CAPACITY;
+  return enqueue_lmhead(ctx, d_packed, vocab, cols, d_hidden, rows, d_hist, hist_ld, d_hist_len,
+                        d_random_24, d_token, d_detail, d_err, d_logits, stream, err, &dec);
+}
+
+void pb_decode_draw(pb_sampling_state* states, const uint32_t* row_state, uint32_t rows,
+                    uint32_t* out, pb_sampling_state* saved) {
+  for (uint32_t r = 0; r < rows; ++r) {
+    saved[r] = states[r];
+    out[r] = row_state[r] == PB_ROW_ACTIVE ? pb_next_24(&states[r]) : 0u;
+  }
+}
+
+uint32_t pb_decode_settle(pb_sampling_state* states, const pb_sampling_state* saved,
+                          const uint32_t* state_before, const uint32_t* state_after,
+                          uint32_t rows) {
+  uint32_t restored = 0;
+  for (uint32_t r = 0; r < rows; ++r) {
+    if (state_before[r] == PB_ROW_ACTIVE && state_after[r] == PB_ROW_ERROR) {
+      states[r] = saved[r];
+      ++restored;
+    }
+  }
+  return restored;
 }
 
 uint32_t pb_device_mfma_selftest(int32_t* d_out, void* stream) {

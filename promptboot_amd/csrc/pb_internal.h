@@ -30,6 +30,14 @@ struct RowParams {
   uint32_t segs;           // slices per row
   uint32_t seg_f4;         // float4 per slice, multiple of 8
   uint32_t hist_vec4;      // history rows are 16-byte aligned: load 4 ids at a time
+  // Decode-loop mode (null row_state: plain sampling).  Rows not in
+  // PB_ROW_ACTIVE are skipped; a sampled token is appended to the row's
+  // context (hist_out / hist_len_out alias hist / hist_len) and the row
+  // state updated.
+  uint32_t* row_state;
+  uint32_t* hist_out;
+  uint32_t* hist_len_out;
+  const uint32_t* max_len; // per-row context cap, or null (hist_ld)
 };
 
 struct WritebackParams {

@@ -343,6 +343,10 @@ __global__ __launch_bounds__(kBlockThreads) void lm_select_kernel(LmParams p, Ro
   const uint32_t wave = threadIdx.x >> 6;
   const uint32_t row = blockIdx.x * (kBlockThreads / 64) + wave;
   if (row >= p.rows) return;
+  if (row_skipped(rp, row)) {  // decode loop: the row has ended
+    if (lane == 0) rp.token[row] = kNone;
+    return;
+  }
   const uint32_t bad_logit = p.meta[row * 2 + 0];
   const uint32_t bad_hist = p.meta[row * 2 + 1];
   if (bad_logit != kNone || bad_hist != kNone) {

@@ -25,6 +25,34 @@ __device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
   return v;
 }
 
+// True when a launch in decode-loop mode must skip `row` (not active).
+__device__ __forceinline__ bool row_skipped(const RowParams& p, uint32_t row) {
+  return p.row_state != nullptr && p.row_state[row] != PB_ROW_ACTIVE;
+}
+
+// Decode-loop bookkeeping after a row's sample (one lane): the working
+// context receives the token, an end-of-sequence piece as <|im_end|>
+// (model_repl.rs:1099-1103), and the row ends on end-of-sequence
+// (:1119-1150), on its length limit, or on an error (no append).
+__device__ __forceinline__ void decode_commit(const RowParams& p, uint32_t row, uint32_t token) {
+  if (p.row_state == nullptr) return;
+  if (token == kNone) {
+    p.row_state[row] = PB_ROW_ERROR;
+    return;
+  }
+  uint32_t cap = (uint32_t)p.hist_ld;
+  if (p.max_len != nullptr && p.max_len[row] < cap) cap = p.max_len[row];
+  const uint32_t len = p.hist_len_out[row];
+  const bool eos = token == PB_IM_END || token == PB_END_OF_TEXT;
+  uint32_t state = PB_ROW_LIMIT;
+  if (len < cap) {
+    p.hist_out[(size_t)row * p.hist_ld + len] = eos ? PB_IM_END : token;
+    p.hist_len_out[row] = len + 1u;
+    state = eos ? PB_ROW_EOS : (len + 1u == cap ? PB_ROW_LIMIT : PB_ROW_ACTIVE);
+  }
+  p.row_state[row] = state;
+}
+
 // Finishes one row on one wave: lanes 0..19 hold the row's top-20 keys in
 // rank order.  Softmax weights, top-p cutoff and the categorical draw follow
 // fp32_sse2.rs:1818-1845 operation for operation; the binary64 sums run as a
@@ -52,6 +80,7 @@ __device__ __forceinline__ void finalize_row(const RowParams& p, uint32_t row, u
     if (lane == 0) {
       p.token[row] = kNone;
       if (p.err) p.err[row] = e;
+      decode_commit(p, row, kNone);
     }
     if (p.detail) {
       uint32_t* d = reinterpret_cast<uint32_t*>(p.detail + row);
@@ -87,7 +116,10 @@ __device__ __forceinline__ void finalize_row(const RowParams& p, uint32_t row, u
   const uint32_t rank = hit ? (uint32_t)__ffsll((unsigned long long)hit) - 1 : kept - 1;
   const uint32_t token = bcast32(id, rank);
 
-  if (lane == 0) p.token[row] = token;
+  if (lane == 0) {
+    p.token[row] = token;
+    decode_commit(p, row, token);
+  }
   if (p.err && lane < sizeof(pb_inference_error) / 4) {
     reinterpret_cast<uint32_t*>(p.err + row)[lane] = 0u;
   }

@@ -94,6 +94,10 @@ __global__ __launch_bounds__(kBlock) void segment_kernel(RowParams p) {
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = tid & 63u;
   const uint32_t wave = tid >> 6;
+  if (row_skipped(p, row)) {  // decode loop: the row has ended
+    if (seg == 0 && tid == 0) p.token[row] = kNone;
+    return;
+  }
 
   const uint32_t f_lo = seg * p.seg_f4;
   const uint32_t f_hi = min(f_lo + p.seg_f4, kRowF4);

@@ -45,6 +45,12 @@ DEVICE = 0x100
 FLAG_DRAW_BOUNDARY = 1
 FLAG_CUTOFF_BOUNDARY = 2
 
+# Decode-loop row states (pb_row_state) and end-of-sequence ids
+# (src/repl_contract.rs:26, crates/promptboot-core/src/tokenizer.rs:38-39).
+ROW_ACTIVE, ROW_EOS, ROW_LIMIT, ROW_ERROR = 0, 1, 2, 3
+IM_END = 151_645
+END_OF_TEXT = 151_643
+
 LIB_PATH = pathlib.Path(__file__).resolve().parent / "libpbsample.so"
 
 u32, u64, size_t, vp = ctypes.c_uint32, ctypes.c_uint64, ctypes.c_size_t, ctypes.c_void_p
@@ -108,6 +114,14 @@ EXPORTS = {
     "pb_lmhead_sample_batch": (
         u32, [vp, vp, size_t, size_t, vp, u32, vp, size_t, vp, vp, vp, vp, vp, vp, vp,
               ctypes.POINTER(_Error)]),
+    "pb_decode_step": (
+        u32, [vp, vp, size_t, size_t, u32, vp, size_t, vp, vp, vp, vp, vp, vp, vp, vp,
+              ctypes.POINTER(_Error)]),
+    "pb_lmhead_decode_step": (
+        u32, [vp, vp, size_t, size_t, vp, u32, vp, size_t, vp, vp, vp, vp, vp, vp, vp, vp,
+              vp, ctypes.POINTER(_Error)]),
+    "pb_decode_draw": (None, [vp, vp, u32, vp, vp]),
+    "pb_decode_settle": (u32, [vp, vp, vp, vp, u32]),
     "pb_version": (ctypes.c_char_p, []),
 }
 
@@ -379,6 +393,122 @@ class BatchSampler:
             states[r]._s = before[r]._s
         dets = det.cpu().numpy().view(DETAIL_DTYPE).reshape(rows) if want_detail else None
         return tok, dets, errs
+
+
+class DecodeBatch:
+    """Many sequences through the REPL's decode loop (src/model_repl.rs:928-1150),
+    one device launch per step.
+
+    Each row owns a working context (prompt, then every generated token; an
+    end-of-sequence piece is stored as IM_END), a length cap (prompt length +
+    generation limit) and its own SamplingState, advanced once per sampled
+    token and never for a failed sample.  The contexts, lengths and row states
+    stay on the device; the host keeps the generators (pb_decode_draw /
+    pb_decode_settle)."""
+
+    def __init__(self, prompts, seeds, limits, capacity: int | None = None, device: int = 0,
+                 sampler: "BatchSampler | None" = None):
+        import torch
+
+        self.rows = len(prompts)
+        self.dev = torch.device(f"cuda:{device}")
+        cap = max(len(p) + int(g) for p, g in zip(prompts, limits))
+        self.hist_ld = int(capacity) if capacity is not None else (cap + 3) // 4 * 4
+        hist = np.zeros((self.rows, self.hist_ld), np.uint32)
+        for r, p in enumerate(prompts):
+            hist[r, :len(p)] = np.asarray(p, np.uint32)
+        lens = np.array([len(p) for p in prompts], np.uint32)
+        max_len = np.minimum(lens + np.asarray(limits, np.uint32), self.hist_ld).astype(np.uint32)
+
+        def dev(a):
+            return torch.from_numpy(np.ascontiguousarray(a).view(np.int32)).to(self.dev)
+
+        self.hist, self.hist_len, self.max_len = dev(hist), dev(lens), dev(max_len)
+        self.row_state_host = np.where(lens < max_len, ROW_ACTIVE, ROW_LIMIT).astype(np.uint32)
+        self.row_state = dev(self.row_state_host)
+        self.states = (_State * self.rows)()
+        for r, seed in enumerate(seeds):
+            lib().pb_sampling_state_new(ctypes.byref(self.states[r]), int(seed) & (2**64 - 1))
+        self._saved = (_State * self.rows)()
+        self.token = torch.empty(self.rows, dtype=torch.int32, device=self.dev)
+        self.err = torch.empty((self.rows, ERROR_DTYPE.itemsize // 4), dtype=torch.int32,
+                               device=self.dev)
+        self._own = sampler is None
+        self.sampler = sampler if sampler is not None else BatchSampler(device)
+
+    def close(self):
+        if self._own and self.sampler is not None:
+            self.sampler.close()
+        self.sampler = None
+
+    def active(self) -> bool:
+        return bool((self.row_state_host == ROW_ACTIVE).any())
+
+    def _draw(self):
+        import torch
+
+        r24 = np.zeros(self.rows, np.uint32)
+        before = self.row_state_host.copy()
+        lib().pb_decode_draw(self.states, before.ctypes.data_as(vp), self.rows,
+                             r24.ctypes.data_as(vp), self._saved)
+        return before, torch.from_numpy(r24.view(np.int32)).to(self.dev)
+
+    def _settle(self, before):
+        import torch
+
+        torch.cuda.synchronize(self.dev)
+        after = self.row_state.cpu().numpy().view(np.uint32).copy()
+        lib().pb_decode_settle(self.states, self._saved, before.ctypes.data_as(vp),
+                               after.ctypes.data_as(vp), self.rows)
+        self.row_state_host = after
+        return self.token.cpu().numpy().view(np.uint32).copy()
+
+    def step(self, logits, stream=None) -> np.ndarray:
+        """One step on logits [rows, ld] (rows that have ended are ignored).
+        Returns the tokens (NO_TOKEN for rows not sampled)."""
+        import torch
+
+        before, r24 = self._draw()
+        s = stream if stream is not None else torch.cuda.current_stream(self.dev)
+        e = _Error()
+        st = lib().pb_decode_step(
+            self.sampler._ctx, ctypes.c_void_p(logits.data_ptr()), VOCAB, logits.shape[1],
+            self.rows, ctypes.c_void_p(self.hist.data_ptr()), self.hist_ld,
+            ctypes.c_void_p(self.hist_len.data_ptr()), ctypes.c_void_p(self.max_len.data_ptr()),
+            ctypes.c_void_p(self.row_state.data_ptr()), ctypes.c_void_p(r24.data_ptr()),
+            ctypes.c_void_p(self.token.data_ptr()), None, ctypes.c_void_p(self.err.data_ptr()),
+            ctypes.c_void_p(s.cuda_stream), ctypes.byref(e))
+        _check(st, e)
+        return self._settle(before)
+
+    def lmhead_step(self, packed, hidden, cols: int = 896, stream=None) -> np.ndarray:
+        """One step through the fused Q4_0 LM head on hidden [rows, cols]."""
+        import torch
+
+        before, r24 = self._draw()
+        s = stream if stream is not None else torch.cuda.current_stream(self.dev)
+        e = _Error()
+        st = lib().pb_lmhead_decode_step(
+            self.sampler._ctx, ctypes.c_void_p(packed.data_ptr()), VOCAB, cols,
+            ctypes.c_void_p(hidden.data_ptr()), self.rows,
+            ctypes.c_void_p(self.hist.data_ptr()), self.hist_ld,
+            ctypes.c_void_p(self.hist_len.data_ptr()), ctypes.c_void_p(self.max_len.data_ptr()),
+            ctypes.c_void_p(self.row_state.data_ptr()), ctypes.c_void_p(r24.data_ptr()),
+            ctypes.c_void_p(self.token.data_ptr()), None, ctypes.c_void_p(self.err.data_ptr()),
+            None, ctypes.c_void_p(s.cuda_stream), ctypes.byref(e))
+        _check(st, e)
+        return self._settle(before)
+
+    def contexts(self) -> list[np.ndarray]:
+        h = self.hist.cpu().numpy().view(np.uint32)
+        n = self.hist_len.cpu().numpy().view(np.uint32)
+        return [h[r, :n[r]].copy() for r in range(self.rows)]
+
+    def errors(self) -> np.ndarray:
+        return self.err.cpu().numpy().view(ERROR_DTYPE).reshape(self.rows)
+
+    def sampling_states(self) -> list[SamplingState]:
+        return [SamplingState.from_parts(s.state, s.draws) for s in self.states]
 
 
 def device_expf_bits(inp, out, stream=None) -> None:

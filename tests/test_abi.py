@@ -117,3 +117,46 @@ def test_version_and_segment_plan():
     assert s.lib().pb_segments_for_rows(4096) == 1
     assert 1 < s.lib().pb_segments_for_rows(64) <= 64
     assert s.lib().pb_segments_for_rows(1) <= 64
+
+
+def test_decode_draw_and_settle_keep_one_draw_per_sampled_token():
+    """Host side of the decode step: one next_24 per active row; a row that
+    failed gets its state back (inference.rs:954-963: no draw on error)."""
+    import ctypes
+
+    rows = 5
+    states = (s._State * rows)()
+    for r in range(rows):
+        s.lib().pb_sampling_state_new(ctypes.byref(states[r]), 42 + r)
+    saved = (s._State * rows)()
+    before = np.array([s.ROW_ACTIVE, s.ROW_EOS, s.ROW_ACTIVE, s.ROW_LIMIT, s.ROW_ACTIVE],
+                      np.uint32)
+    r24 = np.full(rows, 7, np.uint32)
+    s.lib().pb_decode_draw(states, before.ctypes.data_as(ctypes.c_void_p), rows,
+                           r24.ctypes.data_as(ctypes.c_void_p), saved)
+    for r in range(rows):
+        ref = s.SamplingState(42 + r)
+        if before[r] == s.ROW_ACTIVE:
+            assert r24[r] == ref.next_24()
+        else:
+            assert r24[r] == 0
+        assert (states[r].state, states[r].draws) == (ref.state(), ref.draws())
+        assert (saved[r].state, saved[r].draws) == (s.SamplingState(42 + r).state(), 0)
+    after = np.array([s.ROW_ERROR, s.ROW_EOS, s.ROW_ACTIVE, s.ROW_ERROR, s.ROW_EOS], np.uint32)
+    n = s.lib().pb_decode_settle(states, saved, before.ctypes.data_as(ctypes.c_void_p),
+                                 after.ctypes.data_as(ctypes.c_void_p), rows)
+    assert n == 1  # row 3 was not active, so it drew nothing and has nothing to restore
+    assert [states[r].draws for r in range(rows)] == [0, 0, 1, 0, 1]
+
+
+def test_decode_step_argument_errors_need_no_device():
+    """Missing context pointers are rejected before any device work."""
+    import ctypes
+
+    e = s._Error()
+    st = s.lib().pb_decode_step(None, None, s.VOCAB, s.VOCAB, 4, None, 0, None, None, None,
+                                None, None, None, None, None, ctypes.byref(e))
+    assert st == s.CAPACITY and e.status == s.CAPACITY and e.detail == (4 << 32) | 5
+    st = s.lib().pb_decode_step(None, None, s.VOCAB + 1, s.VOCAB, 0, None, 0, None, None, None,
+                                None, None, None, None, None, ctypes.byref(e))
+    assert st == s.CAPACITY and e.needed == s.VOCAB and e.available == s.VOCAB + 1
