@@ -41,7 +41,8 @@ sys.path.insert(0, str(ROOT))
 
 METRIC = "sampled rows/s at vocab 151936 (B=1/64/4096); % of MI355X HBM roofline"
 PEAK_HBM_GBS = 8000.0
-CPU_SAMPLE_ROWS = 1024
+# The whole B=4096 batch: about 5 s per repetition on one core, 3 repetitions.
+CPU_SAMPLE_ROWS = 4096
 SETTLE_S = 0.5
 PMC_SUMMARY = ROOT / "profiles" / "segment_kernel_B4096_traffic.json"
 
