@@ -292,7 +292,7 @@ uint32_t pb_decode_settle(pb_sampling_state *states, const pb_sampling_state *sa
 uint32_t pb_segments_for_rows(uint32_t rows);
 
 /* Forces the number of row slices of this context's batched calls (0 = auto,
- * otherwise clamped to 1..64).  For tuning and for testing both the
+ * otherwise clamped to 1..32).  For tuning and for testing both the
  * single-workgroup and the multi-slice paths on the same rows. */
 void pb_context_set_segments(pb_context *ctx, uint32_t segments);
 

@@ -182,7 +182,7 @@ uint32_t pb_segments_for_rows(uint32_t rows) {
 }
 
 void pb_context_set_segments(pb_context* ctx, uint32_t segments) {
-  ctx->forced_segments = segments > 64 ? 64 : segments;
+  ctx->forced_segments = segments > 32 ? 32 : segments;
 }
 
 uint32_t pb_device_expf_bits(const uint32_t* d_in, uint32_t* d_out, size_t n, void* stream) {

@@ -200,7 +200,7 @@ __global__ __launch_bounds__(kGemmThreads) void lm_gemm_kernel(LmParams p) {
   // Activation scales of every block for this group's rows (the epilogue's
   // per-row multiplier; dynamic LDS of blocks x 256 floats), and this tile's
   // two history bitmap words per row.
-  extern __shared__ float act_scale[];
+  extern __shared__ __align__(16) float act_scale[];
   __shared__ uint32_t hist_words[kRowsPerGroup][2];
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = tid & 63u;
@@ -239,59 +239,78 @@ __global__ __launch_bounds__(kGemmThreads) void lm_gemm_kernel(LmParams p) {
   const int8_t* a_base = p.act_q + ((size_t)rw0 + col) * 32 + 16u * half;
   const uint8_t* w_base = p.weights + ((size_t)v0 + col) * 16;
 
-  // the next block's activation fragment and packed nibbles are requested
-  // before the current block's MFMAs and epilogue run
-  v4i a_cur = *reinterpret_cast<const v4i*>(a_base);
-  v4u raw_cur[2];
-  uint16_t wsh_cur[2];
-#pragma unroll
-  for (int c = 0; c < 2; ++c) {
-    raw_cur[c] = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(w_base + 32u * c * 16));
-    wsh_cur[c] = wscale[v0 + 32u * c + col];
-  }
-#pragma unroll 1
-  for (uint32_t b = 0; b < blocks; ++b) {
-    v4i a_nxt = a_cur;
-    v4u raw_nxt[2] = {raw_cur[0], raw_cur[1]};
-    uint16_t wsh_nxt[2] = {wsh_cur[0], wsh_cur[1]};
-    if (b + 1 < blocks) {
-      a_nxt = *reinterpret_cast<const v4i*>(a_base + (size_t)(b + 1) * p.rows_pad * 32);
-#pragma unroll
-      for (int c = 0; c < 2; ++c) {
-        const size_t vid = (size_t)(b + 1) * kVocab + 32u * c;
-        raw_nxt[c] =
-            __builtin_nontemporal_load(reinterpret_cast<const v4u*>(w_base + vid * 16));
-        wsh_nxt[c] = wscale[vid + v0 + col];
-      }
-    }
+  // Operands of one block: the activation fragment, both column tiles'
+  // packed nibbles and weight scales.  Two sets alternate (the loop is
+  // unrolled by two), so the next block's loads are in flight while the
+  // current block runs and no registers are copied between iterations.
+  struct Operands {
+    v4i a;
+    v4u raw[2];
+    uint16_t wsh[2];
+  };
+  auto load = [&](uint32_t b, Operands& o) {
+    o.a = *reinterpret_cast<const v4i*>(a_base + (size_t)b * p.rows_pad * 32);
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
-      const v4u raw = raw_cur[c];
+      const size_t vid = (size_t)b * kVocab + 32u * c;
+      o.raw[c] = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(w_base + vid * 16));
+      o.wsh[c] = wscale[vid + v0 + col];
+    }
+  };
+  auto run = [&](uint32_t b, const Operands& o) {
+    // this block's 16 activation scales per lane (rows 8g + 4 * half + 0..3)
+    v4f as[4];
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+      as[g] = *reinterpret_cast<const v4f*>(
+          &act_scale[b * kRowsPerGroup + lrow0 + 8u * g + 4u * half]);
+    v16i d[2];
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const v4u raw = o.raw[c];
       const v4i w = {(int)((((raw.x << nib_shift) & 0xf0f0f0f0u) ^ 0x80808080u)),
                      (int)((((raw.y << nib_shift) & 0xf0f0f0f0u) ^ 0x80808080u)),
                      (int)((((raw.z << nib_shift) & 0xf0f0f0f0u) ^ 0x80808080u)),
                      (int)((((raw.w << nib_shift) & 0xf0f0f0f0u) ^ 0x80808080u))};
-      const float ws = __half2float(__ushort_as_half(wsh_cur[c])) * 0.0625f;
-      const v16i d = __builtin_amdgcn_mfma_i32_32x32x32_i8(a_cur, w, zero, 0, 0, 0);
+      d[c] = __builtin_amdgcn_mfma_i32_32x32x32_i8(o.a, w, zero, 0, 0, 0);
+    }
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const float ws = __half2float(__ushort_as_half(o.wsh[c])) * 0.0625f;
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const v4f as = *reinterpret_cast<const v4f*>(
-            &act_scale[b * kRowsPerGroup + lrow0 + 8u * g + 4u * half]);
-        const float asv[4] = {as.x, as.y, as.z, as.w};
+        const float asv[4] = {as[g].x, as[g].y, as[g].z, as[g].w};
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const int r = 4 * g + j;
-          const float scaled = (float)d[r] * ws;
+          const float scaled = (float)d[c][r] * ws;
           total[c][r] = total[c][r] + scaled * asv[j];
         }
       }
     }
-    a_cur = a_nxt;
-    raw_cur[0] = raw_nxt[0];
-    raw_cur[1] = raw_nxt[1];
-    wsh_cur[0] = wsh_nxt[0];
-    wsh_cur[1] = wsh_nxt[1];
+  };
+
+  // Loads are unconditional (the index is clamped to the last block): a load
+  // under a branch makes the compiler wait for every outstanding load at the
+  // join, which would serialise each block behind its own prefetch.
+  // Both halves of the loop body run unconditionally (an odd last block is a
+  // tail), and scheduling barriers keep each prefetch ahead of the compute it
+  // overlaps: otherwise the loads are sunk next to their first use.
+  const uint32_t last = blocks - 1u;
+  Operands even, odd;
+  load(0, even);
+#pragma unroll 1
+  for (uint32_t b = 0; b + 1u < blocks; b += 2) {
+    load(b + 1u, odd);
+    __builtin_amdgcn_sched_barrier(0);
+    run(b, even);
+    __builtin_amdgcn_sched_barrier(0);
+    load(min(b + 2u, last), even);
+    __builtin_amdgcn_sched_barrier(0);
+    run(b + 1u, odd);
+    __builtin_amdgcn_sched_barrier(0);
   }
+  if (blocks & 1u) run(last, even);
 
   // logits, non-finite check, per-row tile maximum of the penalised keys
 #pragma unroll

@@ -349,21 +349,34 @@ __global__ __launch_bounds__(kBlock) void segment_kernel(RowParams p) {
   __syncthreads();
   if (last_slice == 0u) return;
   if (wave == 0) {
+    // Every load of the S lists and slice records is issued before the first
+    // wait: the data comes from other XCDs, and one round trip each would
+    // dominate a small batch.
+    constexpr uint32_t kStage = (kMaxSegments * kTopK + 63) / 64;
     uint64_t* staged = reinterpret_cast<uint64_t*>(bm);  // the bitmap is no longer needed
     const uint64_t* keys = p.part_keys + (size_t)row * p.segs * kTopK;
-    for (uint32_t i = lane; i < p.segs * (uint32_t)kTopK; i += 64)
-      staged[i] = __hip_atomic_load(&keys[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t nkeys = p.segs * (uint32_t)kTopK;
+    uint64_t v[kStage];
+#pragma unroll
+    for (uint32_t u = 0; u < kStage; ++u) {
+      const uint32_t i = u * 64u + lane;
+      v[u] = i < nkeys ? __hip_atomic_load(&keys[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                       : 0;
+    }
+    const uint32_t* meta = p.part_meta + (size_t)row * p.segs * 2;
+    const uint32_t b = lane < p.segs ? __hip_atomic_load(&meta[lane * 2], __ATOMIC_RELAXED,
+                                                         __HIP_MEMORY_SCOPE_AGENT)
+                                     : kNone;
+    const uint32_t hist_bad = __hip_atomic_load(&meta[1], __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+    for (uint32_t u = 0; u < kStage; ++u) {
+      const uint32_t i = u * 64u + lane;
+      if (i < nkeys) staged[i] = v[u];
+    }
     __builtin_amdgcn_wave_barrier();
     const uint64_t merged = merge_sorted_lists(staged, p.segs, lane);
-    uint32_t first_bad = kNone;
-    for (uint32_t s = lane; s < p.segs; s += 64) {
-      const uint32_t b = __hip_atomic_load(&p.part_meta[((size_t)row * p.segs + s) * 2],
-                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      first_bad = b < first_bad ? b : first_bad;
-    }
-    first_bad = wave_min_u32(first_bad);
-    const uint32_t hist_bad = __hip_atomic_load(&p.part_meta[(size_t)row * p.segs * 2 + 1],
-                                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t first_bad = wave_min_u32(b);
     finalize_row(p, row, lane < (uint32_t)kTopK ? merged : 0, first_bad, hist_bad, lane);
     if (lane == 0)  // ready for the next launch
       __hip_atomic_store(&p.row_done[row], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
