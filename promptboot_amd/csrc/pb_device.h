@@ -315,4 +315,46 @@ __device__ __forceinline__ uint64_t merge_sorted_lists(const uint64_t* lists, ui
   return mine;
 }
 
+// Top-20 of `nlists` (1..64) sorted lists as merge_sorted_lists, with two
+// 64-lane sorts instead of 20 dependent wave maxima.  With m = ceil(20 / n)
+// and r = ceil(20 / m), the r-th best of the lists' m-th keys is a threshold
+// T that at least r * m >= 20 keys reach, so the top-20 lies among the keys
+// >= T; those are a prefix of each list, gathered into `scratch` (64 keys of
+// LDS) and sorted once.  Above 64 such keys it falls back to
+// merge_sorted_lists.  Lane i < 20 returns the i-th best key.
+__device__ __forceinline__ uint64_t merge_lists_by_threshold(const uint64_t* lists,
+                                                             uint32_t nlists, uint64_t* scratch,
+                                                             uint32_t lane) {
+  const uint32_t m = ((uint32_t)kTopK + nlists - 1u) / nlists;
+  const uint32_t r = ((uint32_t)kTopK + m - 1u) / m;
+  const bool own = lane < nlists;
+  const uint64_t* mine = lists + lane * kTopK;
+  uint64_t c = own ? mine[m - 1u] : 0;
+  c = wave_sort_desc(c, lane);
+  const uint64_t t = shfl64(c, r - 1u);
+  uint32_t n = 0;
+  if (own) {
+#pragma unroll
+    for (int q = 0; q < kTopK; ++q) {
+      const uint64_t k = mine[q];
+      n += (k != 0 && k >= t) ? 1u : 0u;
+    }
+  }
+  // exclusive prefix of n (< 32) over the lanes, one ballot per bit
+  const uint64_t below = (1ull << lane) - 1ull;
+  uint32_t before = 0, total = 0;
+#pragma unroll
+  for (int b = 0; b < 5; ++b) {
+    const uint64_t bits = __ballot((n >> b) & 1u);
+    before += (uint32_t)__popcll((unsigned long long)(bits & below)) << b;
+    total += (uint32_t)__popcll((unsigned long long)bits) << b;
+  }
+  if (total > 64u) return merge_sorted_lists(lists, nlists, lane);
+  for (uint32_t q = 0; q < n; ++q) scratch[before + q] = mine[q];
+  __builtin_amdgcn_wave_barrier();
+  uint64_t key = lane < total ? scratch[lane] : 0;
+  __builtin_amdgcn_wave_barrier();
+  return wave_sort_desc(key, lane);
+}
+
 }  // namespace pb

@@ -46,6 +46,9 @@ constexpr uint32_t kRowF4 = kVocab / 4;             // 37,984 float4 per row
 constexpr uint32_t kRowWords = kVocab / 32;         // 4,748 bitmap words per row
 constexpr uint32_t kBufCap = 128;                   // candidate slots per wave
 constexpr uint32_t kMaxSegments = 32;               // slices per row, at most
+// The last slice of a row stages the S lists plus 64 keys of merge scratch
+// in the (then unused) bitmap.
+static_assert((kMaxSegments * kTopK + 64) * 8 <= kRowWords * 4, "bitmap too small for staging");
 
 // Block index -> work item.  Consecutive work items (the segments of one row,
 // and neighbouring rows) land on the same XCD, which the hardware picks
@@ -375,7 +378,8 @@ __global__ __launch_bounds__(kBlock) void segment_kernel(RowParams p) {
       if (i < nkeys) staged[i] = v[u];
     }
     __builtin_amdgcn_wave_barrier();
-    const uint64_t merged = merge_sorted_lists(staged, p.segs, lane);
+    const uint64_t merged =
+        merge_lists_by_threshold(staged, p.segs, staged + kMaxSegments * kTopK, lane);
     const uint32_t first_bad = wave_min_u32(b);
     finalize_row(p, row, lane < (uint32_t)kTopK ? merged : 0, first_bad, hist_bad, lane);
     if (lane == 0)  // ready for the next launch
