@@ -227,6 +227,24 @@ __device__ __forceinline__ uint64_t wave_sort_desc(uint64_t key, uint32_t lane) 
   return key;
 }
 
+// Bitonic sort of one 32-bit value per lane, descending, over groups of
+// kLanes lanes (32 or 64; with 32 each half of the wave is sorted on its own).
+template <uint32_t kLanes = 64>
+__device__ __forceinline__ uint32_t wave_sort_desc_u32(uint32_t v, uint32_t lane) {
+#pragma unroll
+  for (uint32_t k = 2; k <= kLanes; k <<= 1) {
+#pragma unroll
+    for (uint32_t j = k >> 1; j > 0; j >>= 1) {
+      const uint32_t other = lane_xor(v, j, lane);
+      const bool take_max = ((lane & j) == 0) == ((lane & k) == 0);
+      const uint32_t hi = v > other ? v : other;
+      const uint32_t lo = v > other ? other : v;
+      v = take_max ? hi : lo;
+    }
+  }
+  return v;
+}
+
 // One merge round: the wave's current top-20 (LDS, sorted, 0 = empty) plus up
 // to 44 new keys from `src` are sorted; the best 20 become the new top.
 // Returns the new 20th key (0 while fewer than 20 real keys are held).
@@ -315,13 +333,14 @@ __device__ __forceinline__ uint64_t merge_sorted_lists(const uint64_t* lists, ui
   return mine;
 }
 
-// Top-20 of `nlists` (1..64) sorted lists as merge_sorted_lists, with two
-// 64-lane sorts instead of 20 dependent wave maxima.  With m = ceil(20 / n)
-// and r = ceil(20 / m), the r-th best of the lists' m-th keys is a threshold
-// T that at least r * m >= 20 keys reach, so the top-20 lies among the keys
-// >= T; those are a prefix of each list, gathered into `scratch` (64 keys of
-// LDS) and sorted once.  Above 64 such keys it falls back to
-// merge_sorted_lists.  Lane i < 20 returns the i-th best key.
+// Top-20 of `nlists` (1..32) sorted lists as merge_sorted_lists, with two
+// wave sorts instead of 20 dependent wave maxima.  With m = ceil(20 / n) and
+// r = ceil(20 / m), take the r-th best value among the lists' m-th keys: the
+// smallest key of that value, T, is reached by at least r * m >= 20 keys, so
+// the top-20 lies among the keys >= T.  Those are a prefix of each list,
+// gathered into `scratch` (64 keys of LDS) and sorted once.  Above 64 such
+// keys it falls back to merge_sorted_lists.  Lane i < 20 returns the i-th
+// best key.
 __device__ __forceinline__ uint64_t merge_lists_by_threshold(const uint64_t* lists,
                                                              uint32_t nlists, uint64_t* scratch,
                                                              uint32_t lane) {
@@ -329,9 +348,8 @@ __device__ __forceinline__ uint64_t merge_lists_by_threshold(const uint64_t* lis
   const uint32_t r = ((uint32_t)kTopK + m - 1u) / m;
   const bool own = lane < nlists;
   const uint64_t* mine = lists + lane * kTopK;
-  uint64_t c = own ? mine[m - 1u] : 0;
-  c = wave_sort_desc(c, lane);
-  const uint64_t t = shfl64(c, r - 1u);
+  const uint32_t c = own ? (uint32_t)(mine[m - 1u] >> 32) : 0u;
+  const uint64_t t = (uint64_t)bcast32(wave_sort_desc_u32<32>(c, lane), r - 1u) << 32;
   uint32_t n = 0;
   if (own) {
 #pragma unroll

@@ -115,6 +115,13 @@ __global__ __launch_bounds__(kBlock) void segment_kernel(RowParams p) {
   const uint32_t nchunks = (f_hi - f_lo + chunk_f4 - 1u) / chunk_f4;
   v4f cur[F];
   load_chunk<F>(cur, rowp, f_lo, f_hi, tid);
+  // The first 256 uint4 of the history row are requested now as well, before
+  // its length is known (ids past the length are padding of the same row and
+  // are ignored): the history scan then costs one memory round trip, not two.
+  v4u h_first = {0u, 0u, 0u, 0u};
+  const v4u* h4 = p.hist_vec4 ? reinterpret_cast<const v4u*>(p.hist + (size_t)row * p.hist_ld)
+                              : nullptr;
+  if (p.hist_vec4 && tid < p.hist_ld / 4u) h_first = __builtin_nontemporal_load(h4 + tid);
 
   // ---- phase 0: clear LDS state ----
   for (uint32_t i = tid; i < nwords; i += kBlock) bm[i] = 0u;
@@ -137,13 +144,28 @@ __global__ __launch_bounds__(kBlock) void segment_kernel(RowParams p) {
     hrow = p.hist + (size_t)row * p.hist_ld;
   }
   uint32_t my_bad = kNone;
+  auto add_ids = [&](const v4u& v, uint32_t q4) {
+    const uint32_t ids[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const uint32_t q = q4 * 4u + (uint32_t)c;
+      const uint32_t id = ids[c];
+      if (q < hist_len) {
+        if (id >= kVocab) {
+          my_bad = min(my_bad, q);
+        } else if (id - e_lo < e_span) {
+          set_bit_once(&bm[(id - e_lo) >> 5], 1u << (id & 31u));
+        }
+      }
+    }
+  };
   if (p.hist_vec4) {
-    // kHistBatch uint4 loads per thread in flight at once: the scan is bound
-    // by HBM latency otherwise.
+    // kHistBatch uint4 loads per thread in flight at once after the first
+    // 256: the scan is bound by HBM latency otherwise.
     constexpr uint32_t kHistBatch = 8;
-    const v4u* h4 = reinterpret_cast<const v4u*>(hrow);
     const uint32_t n4 = (hist_len + 3u) / 4u;
-    for (uint32_t b4 = 0; b4 < n4; b4 += kHistBatch * kBlock) {
+    add_ids(h_first, tid);
+    for (uint32_t b4 = kBlock; b4 < n4; b4 += kHistBatch * kBlock) {
       v4u v[kHistBatch];
 #pragma unroll
       for (uint32_t u = 0; u < kHistBatch; ++u) {
@@ -151,22 +173,7 @@ __global__ __launch_bounds__(kBlock) void segment_kernel(RowParams p) {
         v[u] = q4 < n4 ? __builtin_nontemporal_load(h4 + q4) : v4u{0u, 0u, 0u, 0u};
       }
 #pragma unroll
-      for (uint32_t u = 0; u < kHistBatch; ++u) {
-        const uint32_t q4 = b4 + u * kBlock + tid;
-        const uint32_t ids[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const uint32_t q = q4 * 4u + (uint32_t)c;
-          const uint32_t id = ids[c];
-          if (q < hist_len) {
-            if (id >= kVocab) {
-              my_bad = min(my_bad, q);
-            } else if (id - e_lo < e_span) {
-              set_bit_once(&bm[(id - e_lo) >> 5], 1u << (id & 31u));
-            }
-          }
-        }
-      }
+      for (uint32_t u = 0; u < kHistBatch; ++u) add_ids(v[u], b4 + u * kBlock + tid);
     }
   } else {
     for (uint32_t q = tid; q < hist_len; q += kBlock) {
@@ -217,15 +224,16 @@ __global__ __launch_bounds__(kBlock) void segment_kernel(RowParams p) {
           }
         }
       }
-      uint64_t lane_key = 0;
+      // Only the value part is sorted: the smallest key of the 20th best
+      // value is reached by 20 distinct elements as well.
+      uint32_t lane_ord = 0;
       if (be != kNone) {
         const uint32_t e = be - e_lo;
         const uint32_t xb = b_of(bx);
         const uint32_t yb = ((bm[e >> 5] >> (e & 31u)) & 1u) ? penalize_bits(xb) : xb;
-        lane_key = make_key(yb, be);
+        lane_ord = ord_of(yb);
       }
-      lane_key = wave_sort_desc(lane_key, lane);
-      thr = shfl64(lane_key, kTopK - 1);
+      thr = (uint64_t)bcast32(wave_sort_desc_u32(lane_ord, lane), kTopK - 1) << 32;
       if (lane == 0 && thr != 0) atomicMax(&wg_thr, thr);
     }
 
@@ -255,8 +263,8 @@ __global__ __launch_bounds__(kBlock) void segment_kernel(RowParams p) {
         for (int k = 0; k < 4; ++k) {
           uint64_t key = 0;
           if (pass && xs[k] >= thr_f) {
-            const uint32_t xb = b_of(xs[k]);
-            const uint32_t yb = ((nib >> k) & 1u) ? penalize_bits(xb) : xb;
+            uint32_t yb = b_of(xs[k]);
+            if ((nib >> k) & 1u) yb = penalize_bits(yb);  // rare: most waves skip it
             key = make_key(yb, f * 4u + (uint32_t)k);
             if (key < thr_eff) key = 0;
           }
