@@ -63,8 +63,6 @@ struct pb_context {
 
   uint32_t forced_segments = 0;  // 0 = automatic slices per row
   void* d_work = nullptr;  // multi-slice workspace: row counters, slice top-20 lists
-  uint32_t counter_rows = 0;
-  size_t counter_bytes = 0;
   size_t list_bytes = 0;
 
   void* d_lm = nullptr;  // fused LM head workspace
@@ -88,30 +86,20 @@ struct pb_context {
   uint8_t* h_seen = nullptr;
 };
 
-// Workspace of the multi-slice path: [per-row counters | slice keys + meta].
-// The counters live at a fixed offset so that they stay zero between launches
-// (each row's last slice resets its counter); they are zeroed with a kernel,
-// on the caller's stream, whenever the buffer is (re)allocated.
-static hipError_t ensure_workspace(pb_context* ctx, uint32_t rows, size_t list_bytes,
-                                   hipStream_t stream) {
-  if (rows <= ctx->counter_rows && list_bytes <= ctx->list_bytes) return hipSuccess;
-  const uint32_t counter_rows = rows > ctx->counter_rows ? rows : ctx->counter_rows;
-  const size_t lists = list_bytes > ctx->list_bytes ? list_bytes : ctx->list_bytes;
+// Workspace of the multi-slice path: the slice keys and slice records,
+// grown as needed (hipFree synchronises the device, so no launch still
+// reads the old buffer).
+static hipError_t ensure_workspace(pb_context* ctx, size_t list_bytes) {
+  if (list_bytes <= ctx->list_bytes) return hipSuccess;
   if (ctx->d_work) {
-    hipError_t e = hipFree(ctx->d_work);  // device-synchronising: no launch still reads it
+    hipError_t e = hipFree(ctx->d_work);
     ctx->d_work = nullptr;
-    ctx->counter_rows = 0;
     ctx->list_bytes = 0;
     if (e != hipSuccess) return e;
   }
-  const size_t counter_bytes = ((size_t)counter_rows * 4 + 255) & ~(size_t)255;
-  hipError_t e = hipMalloc(&ctx->d_work, counter_bytes + lists);
+  hipError_t e = hipMalloc(&ctx->d_work, list_bytes);
   if (e != hipSuccess) return e;
-  e = pb::launch_zero(static_cast<uint32_t*>(ctx->d_work), counter_bytes / 4, stream);
-  if (e != hipSuccess) return e;
-  ctx->counter_rows = counter_rows;
-  ctx->counter_bytes = counter_bytes;
-  ctx->list_bytes = lists;
+  ctx->list_bytes = list_bytes;
   return hipSuccess;
 }
 
@@ -304,18 +292,16 @@ static uint32_t enqueue_sample(pb_context* ctx, const uint32_t* d_logits, size_t
   pb::plan_segments(rows, ctx->forced_segments, &p.segs, &p.seg_f4);
   p.part_keys = nullptr;
   p.part_meta = nullptr;
-  p.row_done = nullptr;
   set_decode(p, dec);
   DeviceGuard guard(ctx->device);
   if (p.segs > 1) {
     const size_t slots = (size_t)rows * p.segs;
     const size_t key_bytes = slots * PB_TOP_K * 8;
-    hipError_t e = ensure_workspace(ctx, rows, key_bytes + slots * 8, stream);
+    hipError_t e = ensure_workspace(ctx, key_bytes + slots * 8);
     if (e != hipSuccess) return device_error(err, e);
     char* base = static_cast<char*>(ctx->d_work);
-    p.row_done = reinterpret_cast<uint32_t*>(base);
-    p.part_keys = reinterpret_cast<uint64_t*>(base + ctx->counter_bytes);
-    p.part_meta = reinterpret_cast<uint32_t*>(base + ctx->counter_bytes + key_bytes);
+    p.part_keys = reinterpret_cast<uint64_t*>(base);
+    p.part_meta = reinterpret_cast<uint32_t*>(base + key_bytes);
   }
   hipError_t e = pb::launch_sample(p, stream);
   if (e != hipSuccess) return device_error(err, e);

@@ -26,7 +26,6 @@ struct RowParams {
   pb_inference_error* err;
   uint64_t* part_keys;     // rows x segs x 20 (segs > 1)
   uint32_t* part_meta;     // rows x segs x {first non-finite index, first bad history position}
-  uint32_t* row_done;      // rows slice counters (segs > 1), zero between launches
   uint32_t segs;           // slices per row
   uint32_t seg_f4;         // float4 per slice, multiple of 8
   uint32_t hist_vec4;      // history rows are 16-byte aligned: load 4 ids at a time
@@ -84,6 +83,5 @@ hipError_t launch_writeback(const WritebackParams& p, hipStream_t stream);
 hipError_t launch_probe(int which, const uint32_t* in, uint32_t* out, size_t n,
                         hipStream_t stream);
 hipError_t launch_wave_selftest(uint32_t* out, hipStream_t stream);
-hipError_t launch_zero(uint32_t* words, size_t n, hipStream_t stream);
 
 }  // namespace pb

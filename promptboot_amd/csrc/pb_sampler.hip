@@ -18,9 +18,9 @@
 //                    running threshold: the penalty never raises a value, so
 //                    the unpenalised value is a valid upper bound.  With S == 1
 //                    the same workgroup finishes the row (softmax, top-p,
-//                    draw); otherwise it publishes its 20 keys and the last
-//                    slice of the row to finish (a per-row counter) merges
-//                    the S lists and finishes the row.
+//                    draw); otherwise it publishes its 20 keys.
+//   finish_kernel    (S > 1 only) one wave per row merges the S published
+//                    lists and finishes the row.
 //   writeback_kernel (in-place variant only) applies the penalty to the
 //                    caller's logits once per unique history id.
 //
@@ -46,9 +46,6 @@ constexpr uint32_t kRowF4 = kVocab / 4;             // 37,984 float4 per row
 constexpr uint32_t kRowWords = kVocab / 32;         // 4,748 bitmap words per row
 constexpr uint32_t kBufCap = 128;                   // candidate slots per wave
 constexpr uint32_t kMaxSegments = 32;               // slices per row, at most
-// The last slice of a row stages the S lists plus 64 keys of merge scratch
-// in the (then unused) bitmap.
-static_assert((kMaxSegments * kTopK + 64) * 8 <= kRowWords * 4, "bitmap too small for staging");
 
 // Block index -> work item.  Consecutive work items (the segments of one row,
 // and neighbouring rows) land on the same XCD, which the hardware picks
@@ -88,7 +85,7 @@ __global__ __launch_bounds__(kBlock) void segment_kernel(RowParams p) {
   __shared__ uint64_t top[kWaves][kTopK];
   __shared__ uint64_t buf[kWaves][kBufCap];
   __shared__ unsigned long long wg_thr;
-  __shared__ uint32_t bad_logit, bad_hist, nonfinite_seen, last_slice;
+  __shared__ uint32_t bad_logit, bad_hist, nonfinite_seen;
 
   const uint32_t n = p.rows * p.segs;
   const uint32_t item = xcd_work_item(blockIdx.x, n);
@@ -131,7 +128,6 @@ __global__ __launch_bounds__(kBlock) void segment_kernel(RowParams p) {
     bad_logit = kNone;
     bad_hist = kNone;
     nonfinite_seen = 0u;
-    last_slice = 0u;
   }
   __syncthreads();
 
@@ -330,74 +326,54 @@ __global__ __launch_bounds__(kBlock) void segment_kernel(RowParams p) {
     return;
   }
 
-  // S > 1: publish this slice's top-20; the last slice of the row to finish
-  // merges all of them and finishes the row.  No workgroup ever waits for
-  // another: the per-row counter only elects which one does the merge.
-  // The slice lists cross XCDs (each XCD has its own L2), so they are written
-  // and read with agent-scope atomics, which go to the coherent level; the
-  // writer's release fence orders them before its counter increment, and the
-  // elected reader only loads them after seeing the final count.  No L2
-  // invalidation is needed, so the other slices keep their cached history.
+  // S > 1: publish this slice's top-20 and first bad positions; the next
+  // launch on the stream (finish_kernel) merges the S lists of each row.  A
+  // kernel boundary makes them visible to every XCD; finishing the row in
+  // this launch instead needs an agent-scope release per slice, a writeback
+  // of the XCD's L2 that serialises across the workgroups.
   if (wave == 0) {
     const uint64_t key = merge_two_lists(top[0], top[1], lane);
     const size_t slot = (size_t)row * p.segs + seg;
-    if (lane < (uint32_t)kTopK)
-      __hip_atomic_store(&p.part_keys[slot * kTopK + lane], key, __ATOMIC_RELAXED,
-                         __HIP_MEMORY_SCOPE_AGENT);
+    if (lane < (uint32_t)kTopK) p.part_keys[slot * kTopK + lane] = key;
     if (lane == 0) {
-      __hip_atomic_store(&p.part_meta[slot * 2 + 0], bad_logit, __ATOMIC_RELAXED,
-                         __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(&p.part_meta[slot * 2 + 1], bad_hist, __ATOMIC_RELAXED,
-                         __HIP_MEMORY_SCOPE_AGENT);
+      p.part_meta[slot * 2 + 0] = bad_logit;
+      p.part_meta[slot * 2 + 1] = bad_hist;
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-    if (lane == 0) {
-      const uint32_t done = __hip_atomic_fetch_add(&p.row_done[row], 1u, __ATOMIC_RELAXED,
-                                                   __HIP_MEMORY_SCOPE_AGENT);
-      last_slice = done == p.segs - 1u ? 1u : 0u;
-    }
-  }
-  __syncthreads();
-  if (last_slice == 0u) return;
-  if (wave == 0) {
-    // Every load of the S lists and slice records is issued before the first
-    // wait: the data comes from other XCDs, and one round trip each would
-    // dominate a small batch.
-    constexpr uint32_t kStage = (kMaxSegments * kTopK + 63) / 64;
-    uint64_t* staged = reinterpret_cast<uint64_t*>(bm);  // the bitmap is no longer needed
-    const uint64_t* keys = p.part_keys + (size_t)row * p.segs * kTopK;
-    const uint32_t nkeys = p.segs * (uint32_t)kTopK;
-    uint64_t v[kStage];
-#pragma unroll
-    for (uint32_t u = 0; u < kStage; ++u) {
-      const uint32_t i = u * 64u + lane;
-      v[u] = i < nkeys ? __hip_atomic_load(&keys[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                       : 0;
-    }
-    const uint32_t* meta = p.part_meta + (size_t)row * p.segs * 2;
-    const uint32_t b = lane < p.segs ? __hip_atomic_load(&meta[lane * 2], __ATOMIC_RELAXED,
-                                                         __HIP_MEMORY_SCOPE_AGENT)
-                                     : kNone;
-    const uint32_t hist_bad = __hip_atomic_load(&meta[1], __ATOMIC_RELAXED,
-                                                __HIP_MEMORY_SCOPE_AGENT);
-#pragma unroll
-    for (uint32_t u = 0; u < kStage; ++u) {
-      const uint32_t i = u * 64u + lane;
-      if (i < nkeys) staged[i] = v[u];
-    }
-    __builtin_amdgcn_wave_barrier();
-    const uint64_t merged =
-        merge_lists_by_threshold(staged, p.segs, staged + kMaxSegments * kTopK, lane);
-    const uint32_t first_bad = wave_min_u32(b);
-    finalize_row(p, row, lane < (uint32_t)kTopK ? merged : 0, first_bad, hist_bad, lane);
-    if (lane == 0)  // ready for the next launch
-      __hip_atomic_store(&p.row_done[row], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
-__global__ __launch_bounds__(kBlock) void zero_kernel(uint32_t* words, size_t n) {
-  const size_t i = (size_t)blockIdx.x * kBlock + threadIdx.x;
-  if (i < n) words[i] = 0u;
+// Finishes the rows of a multi-slice launch, one wave per row: the S slice
+// lists are merged (merge_lists_by_threshold) and the row finished.
+__global__ __launch_bounds__(kBlock) void finish_kernel(RowParams p) {
+  __shared__ __align__(16) uint64_t staged[kWaves][kMaxSegments * kTopK + 64];
+  const uint32_t lane = threadIdx.x & 63u;
+  const uint32_t wave = threadIdx.x >> 6;
+  const uint32_t row = blockIdx.x * kWaves + wave;
+  if (row >= p.rows) return;
+  if (row_skipped(p, row)) return;  // decode loop: the token is already PB_NO_TOKEN
+  // every load of the S lists and slice records is issued before the first wait
+  constexpr uint32_t kStage = (kMaxSegments * kTopK + 63) / 64;
+  uint64_t* st = staged[wave];
+  const uint64_t* keys = p.part_keys + (size_t)row * p.segs * kTopK;
+  const uint32_t nkeys = p.segs * (uint32_t)kTopK;
+  uint64_t v[kStage];
+#pragma unroll
+  for (uint32_t u = 0; u < kStage; ++u) {
+    const uint32_t i = u * 64u + lane;
+    v[u] = i < nkeys ? keys[i] : 0;
+  }
+  const uint32_t* meta = p.part_meta + (size_t)row * p.segs * 2;
+  const uint32_t b = lane < p.segs ? meta[lane * 2] : kNone;
+  const uint32_t hist_bad = meta[1];
+#pragma unroll
+  for (uint32_t u = 0; u < kStage; ++u) {
+    const uint32_t i = u * 64u + lane;
+    if (i < nkeys) st[i] = v[u];
+  }
+  __builtin_amdgcn_wave_barrier();
+  const uint64_t merged = merge_lists_by_threshold(st, p.segs, st + kMaxSegments * kTopK, lane);
+  const uint32_t first_bad = wave_min_u32(b);
+  finalize_row(p, row, lane < (uint32_t)kTopK ? merged : 0, first_bad, hist_bad, lane);
 }
 
 // In-place penalty for successful rows (fp32_sse2.rs:1848-1876): the first
@@ -468,14 +444,9 @@ hipError_t launch_sample(const RowParams& p, hipStream_t stream) {
     hipLaunchKernelGGL((segment_kernel<kChunkF4, true>), dim3(blocks), dim3(kBlock), 0, stream, p);
   } else {
     hipLaunchKernelGGL((segment_kernel<kChunkF4, false>), dim3(blocks), dim3(kBlock), 0, stream, p);
+    hipLaunchKernelGGL(finish_kernel, dim3((p.rows + kWaves - 1) / kWaves), dim3(kBlock), 0, stream,
+                       p);
   }
-  return hipGetLastError();
-}
-
-hipError_t launch_zero(uint32_t* words, size_t n, hipStream_t stream) {
-  if (n == 0) return hipSuccess;
-  hipLaunchKernelGGL(zero_kernel, dim3((uint32_t)((n + kBlock - 1) / kBlock)), dim3(kBlock), 0,
-                     stream, words, n);
   return hipGetLastError();
 }
 
