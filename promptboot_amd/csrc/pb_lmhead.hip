@@ -317,7 +317,11 @@ __global__ __launch_bounds__(kGemmThreads) void lm_gemm_kernel(LmParams p) {
   for (int r = 0; r < 16; ++r) {
     const uint32_t row = rw0 + 8u * (r / 4) + 4u * half + (r % 4);
     const bool live = row < p.rows;
-    uint64_t best = 0;
+    // The lane's better element of its two columns (the lower id on equal
+    // values), kept as (value order, id, sign of zero): the largest key of
+    // the row's 64 ids is then a 32-lane maximum of the value order followed
+    // by a minimum of the id among the lanes holding it.
+    uint32_t best_ord = 0, best_tag = 0;
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
       const uint32_t v = v0 + 32u * c + col;
@@ -326,17 +330,28 @@ __global__ __launch_bounds__(kGemmThreads) void lm_gemm_kernel(LmParams p) {
         p.logits[(size_t)row * p.logits_ld + v] = xb;
         if ((xb & 0x7f800000u) == 0x7f800000u) atomicMin(&p.meta[row * 2], v);
       }
-      const uint32_t member = live ? (hist_words[row - group0][c] >> col) & 1u : 0u;
+      const bool member = live && ((hist_words[row - group0][c] >> col) & 1u) != 0u;
       const uint32_t yb = member ? penalize_bits(xb) : xb;
-      const uint64_t key = make_key(yb, v);
-      best = key > best ? key : best;
+      const uint32_t ord = ord_of(yb);
+      if (c == 0 || ord > best_ord) {
+        best_ord = ord;
+        best_tag = (v << 1) | (yb == 0x80000000u ? 1u : 0u);
+      }
     }
+    uint32_t top_ord = best_ord;
 #pragma unroll
     for (uint32_t m = 1; m < 32; m <<= 1) {
-      const uint64_t o = shfl_xor64(best, (int)m);
-      best = o > best ? o : best;
+      const uint32_t o = lane_xor(top_ord, m, lane);
+      top_ord = o > top_ord ? o : top_ord;
     }
-    if (live && col == 0) p.tilemax[(size_t)row * kTilesPerRow + tile] = best;
+    uint32_t tag = best_ord == top_ord ? best_tag : 0xffffffffu;
+#pragma unroll
+    for (uint32_t m = 1; m < 32; m <<= 1) {
+      const uint32_t o = lane_xor(tag, m, lane);
+      tag = o < tag ? o : tag;
+    }
+    const uint32_t low = ((0x3ffffu - (tag >> 1)) << 1) | (tag & 1u);  // make_key's low word
+    if (live && col == 0) p.tilemax[(size_t)row * kTilesPerRow + tile] = ((uint64_t)top_ord << 32) | low;
   }
 }
 
