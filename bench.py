@@ -9,14 +9,19 @@ row.  The headline workload is B=4096 rows with full-context histories
 reported under "by_batch".
 
 The printed JSON line also carries:
-  roofline      the segment kernel's algorithmic HBM bytes per launch over
-                its average launch time (HIP events on the launch stream)
-                against the 8 TB/s MI355X peak, and the measured HBM traffic
-                from the committed rocprofv3 counter summary when present;
-  cpu_baseline  the CPU oracle (a restatement of the reference sampler),
-                single-threaded and pinned to one CPU, on a bounded sample of
-                the same rows (first 1024 rows, 3 repetitions, median);
-  parity        token agreement with the oracle over every row of the batch.
+  roofline           the segment kernel's algorithmic HBM bytes per launch
+                     over its average launch time (HIP events on the launch
+                     stream) against the 8 TB/s MI355X peak, and the measured
+                     HBM traffic from the committed rocprofv3 counter summary
+                     when present;
+  cpu_baseline       the CPU oracle (a restatement of the reference sampler),
+                     single-threaded and pinned to one CPU, on the same 4096
+                     rows (3 repetitions, median);
+  parity             token agreement with the oracle over every row of the
+                     batch;
+  adversarial_B1024  the flat / ties / dominant / half-vocabulary-history
+                     sub-cases, each timed and checked against the oracle;
+  lmhead_fused       the fused Q4_0 LM head + sampler step (B=256).
 
 Before the W warmup steps every batch size runs an untimed settle phase
 (the step repeated for 0.5 s) so the GPU is at its working clocks.
@@ -223,12 +228,46 @@ def time_lmhead(smp, steps: int, warmup: int) -> dict:
                         "reference Q4 head"}
 
 
+ADVERSARIAL = ("flat", "ties", "dominant", "half")
+
+
+def time_adversarial(smp, steps: int, warmup: int, threads: int) -> dict:
+    """The adversarial B=1024 sub-cases (flat logits, ties at the rank-20
+    boundary, one dominant token, a history over half the vocabulary), each
+    timed and checked row by row against the oracle."""
+    from oracle import oracle as o
+    from promptboot_amd import workloads
+
+    out = {}
+    for name in ADVERSARIAL:
+        log(f"adversarial {name}: generating, timing, checking")
+        w = workloads.make(name)
+        r = time_batch(smp, w, steps, warmup)
+        rtok, rdet, _, _ = o.sample_batch(w["logits"], w["hist"], w["hist_len"],
+                                          w["random_24"], threads=threads)
+        boundary = r["_detail"]["flags"] != 0
+        agree = r["_tokens"] == rtok
+        out[name] = {"rows": int(len(rtok)), "rows_per_s": round(r["rows_per_s"], 1),
+                     "launch_ms": round(r["launch_ms"], 4),
+                     "hbm_frac": round(r["achieved_gbs"] / PEAK_HBM_GBS, 4),
+                     "segments_per_row": r["segments"],
+                     "token_agreement": float(agree.mean()),
+                     "token_agreement_non_boundary": float(agree[~boundary].mean())
+                     if (~boundary).any() else None,
+                     "boundary_rows": int(boundary.sum()),
+                     "top20_set_agreement": float((r["_detail"]["ids"] == rdet["ids"]).all(axis=1).mean())}
+        del w
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-adversarial", action="store_true",
+                    help="skip the adversarial B=1024 sub-cases")
     ap.add_argument("--no-lmhead", action="store_true",
                     help="skip the fused Q4_0 LM head + sampler timing")
     ap.add_argument("--batches", default="1,64,4096")
@@ -281,6 +320,10 @@ def main() -> int:
     for B in batches:
         log(f"timing B={B}")
         results[B] = time_batch(smp, work[B], args.steps, args.warmup)
+    threads = min(16, len(os.sched_getaffinity(0)))
+    adversarial = None
+    if not args.no_adversarial:
+        adversarial = time_adversarial(smp, min(args.steps, 50), args.warmup, threads)
     lmhead = None
     if not args.no_lmhead:
         log("timing the fused Q4_0 LM head + sampler (B=256)")
@@ -291,7 +334,7 @@ def main() -> int:
     w = work[head]
     log("checking tokens against the oracle")
     rtok, rdet, _, _ = o.sample_batch(w["logits"], w["hist"], w["hist_len"], w["random_24"],
-                                      threads=min(16, len(os.sched_getaffinity(0))))
+                                      threads=threads)
     boundary = (main_res["_detail"]["flags"] != 0)
     agree = main_res["_tokens"] == rtok
     topk_agree = (main_res["_detail"]["ids"] == rdet["ids"]).all(axis=1)
@@ -341,6 +384,7 @@ def main() -> int:
                    "rows": head, "vocab": 151936, "hist_ld": int(w["hist"].shape[1])},
         "tokens_per_s": round(main_res["rows_per_s"], 1),
         "by_batch": by_batch,
+        "adversarial_B1024": adversarial,
         "lmhead_fused": lmhead,
         "roofline": roof,
         "cpu_baseline": cpu,
