@@ -49,6 +49,7 @@ PEAK_HBM_GBS = 8000.0
 # The whole B=4096 batch: about 5 s per repetition on one core, 3 repetitions.
 CPU_SAMPLE_ROWS = 4096
 SETTLE_S = 0.5
+PARITY_LMHEAD_ROWS = 64  # rows of the LM head step re-computed by the oracle (~9 G MACs)
 PMC_SUMMARY = ROOT / "profiles" / "segment_kernel_B4096_traffic.json"
 
 
@@ -192,8 +193,17 @@ def time_lmhead(smp, steps: int, warmup: int) -> dict:
     def step():
         smp.lmhead_sample(packed, hidden, r24, hist, hl, token=token, stream=stream)
 
-    step()
+    # one step with the logits and detail kept, for the parity check below
+    logits = torch.empty((B, s.VOCAB), dtype=torch.int32, device=dev)
+    det = torch.empty((B, s.DETAIL_DTYPE.itemsize // 4), dtype=torch.int32, device=dev)
+    smp.lmhead_sample(packed, hidden, r24, hist, hl, token=token, detail=det, logits=logits,
+                      stream=stream)
     torch.cuda.synchronize()
+    n_check = PARITY_LMHEAD_ROWS
+    g_logits = logits[:n_check].cpu().numpy().view(np.uint32)
+    g_tokens = token.cpu().numpy().view(np.uint32)[:n_check].copy()
+    g_flags = det.cpu().numpy().view(s.DETAIL_DTYPE).reshape(B)["flags"][:n_check].copy()
+    del logits, det
     t_settle = time.perf_counter()
     while time.perf_counter() - t_settle < SETTLE_S:
         for _ in range(4):
@@ -212,6 +222,25 @@ def time_lmhead(smp, steps: int, warmup: int) -> dict:
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     step_ms = float(np.mean([a.elapsed_time(b) for a, b in zip(starts, ends)]))
+    # parity on a bounded sample: the oracle's Q4_0 head and sampler on the
+    # first rows (bit-exact logits; token agreement on non-boundary rows)
+    from oracle import oracle as o
+
+    threads = min(16, len(os.sched_getaffinity(0)))
+    r_logits = o.lmhead_logits(w["hidden"][:n_check], w["q4"], workloads.VOCAB,
+                               workloads.HIDDEN, threads=threads)
+    r_tok, _, _, _ = o.sample_batch(r_logits, w["hist"][:n_check], w["hist_len"][:n_check],
+                                    w["random_24"][:n_check], threads=threads)
+    rl = r_logits.view(np.float32).astype(np.float64)
+    gl = g_logits.view(np.float32).astype(np.float64)
+    boundary = g_flags != 0
+    parity = {"rows": n_check,
+              "logits_bit_exact": float((g_logits == r_logits).mean()),
+              "logits_max_rel_err": float(np.max(np.abs(gl - rl) / np.maximum(np.abs(rl), 1e-30))),
+              "token_agreement": float((g_tokens == r_tok).mean()),
+              "token_agreement_non_boundary": float((g_tokens == r_tok)[~boundary].mean())
+              if (~boundary).any() else None,
+              "boundary_rows": int(boundary.sum())}
     ops = 2.0 * B * workloads.VOCAB * workloads.HIDDEN
     epilogue = 4.0 * B * workloads.VOCAB * (workloads.HIDDEN // 32)
     alg = workloads.lmhead_algorithmic_bytes(B, w["hist_len"])
@@ -223,6 +252,7 @@ def time_lmhead(smp, steps: int, warmup: int) -> dict:
             "epilogue_valu_frac": round(epilogue / (step_ms / 1e3) / VALU_LANE_OPS_PEAK, 4),
             "hbm_gbs": round(alg / (step_ms / 1e3) / 1e9, 1),
             "hbm_frac": round(alg / (step_ms / 1e3) / 1e9 / PEAK_HBM_GBS, 4),
+            "parity": parity,
             "workload": "B=256 hidden N(0,1) x 896, Q4_0 head 151936x896 (fp16 scales "
                         "U(0.001,0.02)), histories U[16,1024] Zipf; logits bit-exact to the "
                         "reference Q4 head"}
