@@ -288,7 +288,8 @@ static uint32_t enqueue_sample(pb_context* ctx, const uint32_t* d_logits, size_t
   p.token = d_token;
   p.detail = d_detail;
   p.err = d_err;
-  p.hist_vec4 = (p.hist != nullptr && (hist_ld & 3u) == 0 && ((uintptr_t)d_hist & 15u) == 0);
+  p.hist_vec4 = (p.hist != nullptr && hist_ld >= 4u && (hist_ld & 3u) == 0 &&
+                 ((uintptr_t)d_hist & 15u) == 0);
   pb::plan_segments(rows, ctx->forced_segments, &p.segs, &p.seg_f4);
   p.part_keys = nullptr;
   p.part_meta = nullptr;

@@ -245,17 +245,22 @@ __device__ __forceinline__ uint32_t wave_sort_desc_u32(uint32_t v, uint32_t lane
   return v;
 }
 
+struct KeepKey {
+  __device__ uint64_t operator()(uint64_t key) const { return key; }
+};
+
 // One merge round: the wave's current top-20 (LDS, sorted, 0 = empty) plus up
-// to 44 new keys from `src` are sorted; the best 20 become the new top.
-// Returns the new 20th key (0 while fewer than 20 real keys are held).
-template <typename SrcPtr>
+// to 44 new keys from `src` are sorted; the best 20 become the new top.  Each
+// new key passes through `fix` first (the sampler applies the history penalty
+// there).  Returns the new 20th key (0 while fewer than 20 real keys are held).
+template <typename SrcPtr, typename Fix = KeepKey>
 __device__ __forceinline__ uint64_t merge_round(uint64_t* top, SrcPtr src, uint32_t n,
-                                                uint32_t lane) {
+                                                uint32_t lane, Fix fix = Fix()) {
   uint64_t key = 0;
   if (lane < (uint32_t)kTopK) {
     key = top[lane];
   } else if (lane - kTopK < n) {
-    key = src[lane - kTopK];
+    key = fix(src[lane - kTopK]);
   }
   key = wave_sort_desc(key, lane);
   __builtin_amdgcn_wave_barrier();

@@ -25,9 +25,17 @@ __device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
   return v;
 }
 
+// A per-row word read through the scalar cache (s_load, counted apart from
+// vector loads, so that waiting for it does not wait for a row's streams).
+// Only for words that no wave of the launch writes before this read: the
+// row's own state and length, which its own workgroup updates at the end.
+__device__ __forceinline__ uint32_t row_word(const uint32_t* ptr) {
+  return *(const __attribute__((address_space(4))) uint32_t*)ptr;
+}
+
 // True when a launch in decode-loop mode must skip `row` (not active).
 __device__ __forceinline__ bool row_skipped(const RowParams& p, uint32_t row) {
-  return p.row_state != nullptr && p.row_state[row] != PB_ROW_ACTIVE;
+  return p.row_state != nullptr && row_word(p.row_state + row) != PB_ROW_ACTIVE;
 }
 
 // Decode-loop bookkeeping after a row's sample (one lane): the working

@@ -11,24 +11,28 @@
 //   segment_kernel   grid = rows x S workgroups of 256 threads.  A workgroup
 //                    owns one contiguous slice (segment) of one row.  It
 //                    builds the row's history bitmap for its slice in LDS,
-//                    streams the slice once from HBM in register chunks of
-//                    256 x F float4, and keeps the exact top-20 of the
-//                    penalised values with 64-bit keys (value, -id).  The
-//                    penalty is evaluated only for elements that pass the
-//                    running threshold: the penalty never raises a value, so
-//                    the unpenalised value is a valid upper bound.  With S == 1
-//                    the same workgroup finishes the row (softmax, top-p,
-//                    draw); otherwise it publishes its 20 keys.
+//                    streams the slice once from HBM (two register chunks of
+//                    256 x F float4 in flight per thread, each float4
+//                    reloaded as soon as it has been examined), and keeps the
+//                    exact top-20 of the penalised values with 64-bit keys
+//                    (value, -id).  Candidates are keyed by their raw value
+//                    and penalised when merged: the penalty never raises a
+//                    value, so a raw key below the threshold is below it
+//                    penalised as well.  With S == 1 the same workgroup
+//                    finishes the row (softmax, top-p, draw); otherwise it
+//                    publishes its 20 keys.
 //   finish_kernel    (S > 1 only) one wave per row merges the S published
 //                    lists and finishes the row.
 //   writeback_kernel (in-place variant only) applies the penalty to the
 //                    caller's logits once per unique history id.
 //
-// Threshold logic per wave: the first chunk seeds a threshold from the 20th
-// best lane maximum (20 distinct real elements are at least that good, so
-// nothing below it can be in the top-20); later candidates must reach the
-// wave's current 20th-best key (or the workgroup-wide best of those), and are
-// merged 44 at a time with a 64-lane bitonic sort.
+// Threshold logic: a key below the threshold is dropped, so the threshold
+// must never exceed the slice's final 20th-best key; it is a lower bound
+// backed by at least 20 distinct elements.  The first chunk seeds it from the
+// lane maxima (the 20th best of a wave's 64, and the smallest of the waves'
+// 5th best: 4 x 5 distinct elements).  Later the same two bounds come from the
+// waves' top lists, which absorb pending candidates 24 at a time with a
+// 64-lane bitonic sort.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -42,9 +46,15 @@ namespace pb {
 
 constexpr uint32_t kBlock = 256;
 constexpr uint32_t kWaves = kBlock / 64;
+// Keys each wave contributes to the workgroup threshold: kWaves * kQuota >= 20.
+constexpr uint32_t kQuota = (kTopK + kWaves - 1) / kWaves;
 constexpr uint32_t kRowF4 = kVocab / 4;             // 37,984 float4 per row
 constexpr uint32_t kRowWords = kVocab / 32;         // 4,748 bitmap words per row
 constexpr uint32_t kBufCap = 128;                   // candidate slots per wave
+// Pending keys that trigger a merge: an earlier merge raises the wave's
+// threshold sooner, and fewer later elements reach the slow path.
+constexpr uint32_t kMergeAt = 24;
+static_assert(kMergeAt >= 1 && kMergeAt - 1 + 64 <= kBufCap, "one ballot of keys must fit");
 constexpr uint32_t kMaxSegments = 32;               // slices per row, at most
 
 // Block index -> work item.  Consecutive work items (the segments of one row,
@@ -67,6 +77,11 @@ __device__ __forceinline__ void set_bit_once(uint32_t* word, uint32_t bit) {
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 
+// Loads float4 base + j*256 + tid, j < F, of a slice ending at f_hi.  Past the
+// end the address is clamped to the slice's last float4 (users mask those
+// lanes by index): every load is unconditional, so the number of loads in
+// flight is the same on every path and a wait for an older load (the
+// history's) does not have to wait for all of them.
 template <int F>
 __device__ __forceinline__ void load_chunk(v4f (&dst)[F], const v4f* __restrict__ rowp,
                                            uint32_t base, uint32_t f_hi, uint32_t tid) {
@@ -75,7 +90,7 @@ __device__ __forceinline__ void load_chunk(v4f (&dst)[F], const v4f* __restrict_
     const uint32_t f = base + (uint32_t)j * kBlock + tid;
     // Each logit is read exactly once: a non-temporal load keeps the stream
     // from evicting the history and the workspace from the caches.
-    dst[j] = f < f_hi ? __builtin_nontemporal_load(rowp + f) : v4f{0.f, 0.f, 0.f, 0.f};
+    dst[j] = __builtin_nontemporal_load(rowp + min(f, f_hi - 1u));
   }
 }
 
@@ -85,6 +100,7 @@ __global__ __launch_bounds__(kBlock) void segment_kernel(RowParams p) {
   __shared__ uint64_t top[kWaves][kTopK];
   __shared__ uint64_t buf[kWaves][kBufCap];
   __shared__ unsigned long long wg_thr;
+  __shared__ uint64_t wave_q[kWaves];  // each wave's kQuota-th best key
   __shared__ uint32_t bad_logit, bad_hist, nonfinite_seen;
 
   const uint32_t n = p.rows * p.segs;
@@ -105,26 +121,36 @@ __global__ __launch_bounds__(kBlock) void segment_kernel(RowParams p) {
   const uint32_t e_span = (f_hi - f_lo) * 4u;
   const uint32_t nwords = e_span / 32u;
 
-  // The first chunk of logits is requested before the history is scanned, so
-  // the two streams overlap.
   const v4f* __restrict__ rowp = reinterpret_cast<const v4f*>(p.logits + (size_t)row * p.ld);
   const uint32_t chunk_f4 = kBlock * (uint32_t)F;
   const uint32_t nchunks = (f_hi - f_lo + chunk_f4 - 1u) / chunk_f4;
+  // The first 256 uint4 of the history row and the first chunk of logits are
+  // requested before anything else, the history first (the scan needs it
+  // first), before the history length is known (ids past the length are
+  // padding of the same row and are ignored): the two streams overlap and the
+  // scan costs one memory round trip, not two.  The history load is
+  // unconditional, from a clamped address (the logits row when the history is
+  // not 16-byte aligned; the value is then unused): a load under a branch
+  // makes the compiler wait for every outstanding load where the branch joins.
+  const v4u* h4 = p.hist_vec4 ? reinterpret_cast<const v4u*>(p.hist + (size_t)row * p.hist_ld)
+                              : reinterpret_cast<const v4u*>(rowp);
+  const uint32_t h4_last = p.hist_vec4 ? (uint32_t)(p.hist_ld / 4u) - 1u : kBlock - 1u;
+  const v4u h_first = __builtin_nontemporal_load(h4 + min(tid, h4_last));
   v4f cur[F];
   load_chunk<F>(cur, rowp, f_lo, f_hi, tid);
-  // The first 256 uint4 of the history row are requested now as well, before
-  // its length is known (ids past the length are padding of the same row and
-  // are ignored): the history scan then costs one memory round trip, not two.
-  v4u h_first = {0u, 0u, 0u, 0u};
-  const v4u* h4 = p.hist_vec4 ? reinterpret_cast<const v4u*>(p.hist + (size_t)row * p.hist_ld)
-                              : nullptr;
-  if (p.hist_vec4 && tid < p.hist_ld / 4u) h_first = __builtin_nontemporal_load(h4 + tid);
+  uint32_t hist_len = 0;
+  if (p.hist != nullptr && p.hist_len != nullptr) {
+    hist_len = row_word(p.hist_len + row);
+    if ((size_t)hist_len > p.hist_ld) hist_len = (uint32_t)p.hist_ld;
+  }
 
   // ---- phase 0: clear LDS state ----
   for (uint32_t i = tid; i < nwords; i += kBlock) bm[i] = 0u;
   if (tid < kWaves * kTopK) (&top[0][0])[tid] = 0u;
   if (tid == 0) {
     wg_thr = 0u;
+#pragma unroll
+    for (uint32_t w = 0; w < kWaves; ++w) wave_q[w] = 0u;
     bad_logit = kNone;
     bad_hist = kNone;
     nonfinite_seen = 0u;
@@ -132,41 +158,62 @@ __global__ __launch_bounds__(kBlock) void segment_kernel(RowParams p) {
   __syncthreads();
 
   // ---- phase 1: history ids -> bitmap of this slice, first bad position ----
-  uint32_t hist_len = 0;
-  const uint32_t* __restrict__ hrow = nullptr;
-  if (p.hist != nullptr && p.hist_len != nullptr) {
-    hist_len = p.hist_len[row];
-    if ((size_t)hist_len > p.hist_ld) hist_len = (uint32_t)p.hist_ld;
-    hrow = p.hist + (size_t)row * p.hist_ld;
-  }
+  const uint32_t* __restrict__ hrow = hist_len != 0 ? p.hist + (size_t)row * p.hist_ld : nullptr;
   uint32_t my_bad = kNone;
+  // Marks the ids at history positions 4*q4 .. 4*q4+3 in the slice bitmap.
+  // The four bitmap words are read first and only bits not yet set are OR-ed
+  // in: a wave waits for LDS once per four ids, and repeated ids (most of a
+  // long history) cost no atomic.  Lanes with nothing to mark read word 0.
   auto add_ids = [&](const v4u& v, uint32_t q4) {
     const uint32_t ids[4] = {v.x, v.y, v.z, v.w};
+    uint32_t word[4], cur_bits[4];
+    bool mark[4];
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       const uint32_t q = q4 * 4u + (uint32_t)c;
-      const uint32_t id = ids[c];
-      if (q < hist_len) {
-        if (id >= kVocab) {
-          my_bad = min(my_bad, q);
-        } else if (id - e_lo < e_span) {
-          set_bit_once(&bm[(id - e_lo) >> 5], 1u << (id & 31u));
-        }
-      }
+      const bool valid = q < hist_len;
+      my_bad = min(my_bad, valid && ids[c] >= kVocab ? q : kNone);
+      const uint32_t rel = ids[c] - e_lo;  // ids >= kVocab fall outside every slice
+      mark[c] = valid && rel < e_span;
+      word[c] = mark[c] ? rel >> 5 : 0u;
+      cur_bits[c] = __hip_atomic_load(&bm[word[c]], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const uint32_t bit = 1u << (ids[c] & 31u);
+      if (mark[c] && (cur_bits[c] & bit) == 0u) atomicOr(&bm[word[c]], bit);
     }
   };
   if (p.hist_vec4) {
-    // kHistBatch uint4 loads per thread in flight at once after the first
-    // 256: the scan is bound by HBM latency otherwise.
-    constexpr uint32_t kHistBatch = 8;
+    // After the first 256 uint4, kHistBatch uint4 per thread stay in flight:
+    // each one consumed is replaced by the load kHistBatch*256 uint4 further
+    // on, while there is a further batch.  Loads past the length are clamped
+    // to the row's last uint4 (a repeat of it marks nothing new: its
+    // positions are past the length).  The scan is bound by HBM latency
+    // otherwise.
+    constexpr uint32_t kHistBatch = 4;
+    constexpr uint32_t kStep = kHistBatch * kBlock;
     const uint32_t n4 = (hist_len + 3u) / 4u;
     add_ids(h_first, tid);
-    for (uint32_t b4 = kBlock; b4 < n4; b4 += kHistBatch * kBlock) {
+    if (n4 > kBlock) {
+      const uint32_t last = n4 - 1u;
       v4u v[kHistBatch];
 #pragma unroll
-      for (uint32_t u = 0; u < kHistBatch; ++u) {
-        const uint32_t q4 = b4 + u * kBlock + tid;
-        v[u] = q4 < n4 ? __builtin_nontemporal_load(h4 + q4) : v4u{0u, 0u, 0u, 0u};
+      for (uint32_t u = 0; u < kHistBatch; ++u)
+        v[u] = __builtin_nontemporal_load(h4 + min(kBlock + u * kBlock + tid, last));
+      uint32_t b4 = kBlock;
+      for (; b4 + kStep < n4; b4 += kStep) {
+#pragma unroll
+        for (uint32_t u = 0; u < kHistBatch; ++u) {
+          add_ids(v[u], b4 + u * kBlock + tid);
+          // Keeps the ids of v[u] from living past its reload (the empty asm
+          // makes my_bad final here, not at the end of the iteration): the
+          // reload then lands in v[u]'s own registers, and the loop does not
+          // wait for it to copy it back before the next iteration.
+          __asm__ volatile("" : "+v"(my_bad));
+          __builtin_amdgcn_sched_barrier(0);
+          v[u] = __builtin_nontemporal_load(h4 + min(b4 + kStep + u * kBlock + tid, last));
+        }
       }
 #pragma unroll
       for (uint32_t u = 0; u < kHistBatch; ++u) add_ids(v[u], b4 + u * kBlock + tid);
@@ -198,49 +245,90 @@ __global__ __launch_bounds__(kBlock) void segment_kernel(RowParams p) {
   uint32_t cnt = 0;      // pending candidates in my_buf
   float nan_probe = 0.0f;
 
-  for (uint32_t c = 0; c < nchunks; ++c) {
-    const uint32_t base = f_lo + c * chunk_f4;
-    v4f nxt[F];
-    if (c + 1 < nchunks) load_chunk<F>(nxt, rowp, base + chunk_f4, f_hi, tid);
+  // Two chunks are in flight per thread at all times: chunk c sits in
+  // cur (c even) or nxt (c odd), and as soon as float4 j of chunk c has been
+  // examined its registers are reloaded with float4 j of chunk c + 2.  The
+  // reloads are unconditional (clamped past the end of the slice; those lanes
+  // are masked by index), so every wait is for the oldest load only.
+  v4f nxt[F];
+  load_chunk<F>(nxt, rowp, f_lo + chunk_f4, f_hi, tid);
 
-    if (c == 0) {
-      // Seed: the best element of each lane (largest value, lowest id), its
-      // penalised key, and the 20th best of those 64 keys.
-      float bx = 0.0f;
-      uint32_t be = kNone;
+  // Workgroup threshold: the largest of the waves' 20th best keys, and the
+  // smallest of their kQuota-th best keys -- the waves' lists then hold at
+  // least kWaves * kQuota >= 20 distinct keys at or above it, so the row's
+  // 20th best key is never below it.  With the row split over the waves, the
+  // second bound is close to the row's own 20th best seen so far; the first
+  // is the 20th best of a quarter of it.
+  auto publish_quota = [&](uint64_t q) {
+    __hip_atomic_store(&wave_q[wave], q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  };
+  auto wg_threshold = [&]() -> uint64_t {
+    uint64_t t = __hip_atomic_load(&wg_thr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    uint64_t m = __hip_atomic_load(&wave_q[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 #pragma unroll
-      for (int j = 0; j < F; ++j) {
-        const uint32_t f = base + (uint32_t)j * kBlock + tid;
-        const float xs[4] = {cur[j].x, cur[j].y, cur[j].z, cur[j].w};
+    for (uint32_t w = 1; w < kWaves; ++w) {
+      const uint64_t o = __hip_atomic_load(&wave_q[w], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      m = o < m ? o : m;
+    }
+    return t > m ? t : m;
+  };
+
+  {
+    // Seed: the best element of each lane in chunk 0 (largest value, lowest
+    // id), its penalised key, and the 20th best of those 64 keys.
+    float bx = 0.0f;
+    uint32_t be = kNone;
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          if (f < f_hi && (be == kNone || xs[k] > bx)) {
-            bx = xs[k];
-            be = f * 4u + (uint32_t)k;
-          }
+    for (int j = 0; j < F; ++j) {
+      const uint32_t f = f_lo + (uint32_t)j * kBlock + tid;
+      const float xs[4] = {cur[j].x, cur[j].y, cur[j].z, cur[j].w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        if (f < f_hi && (be == kNone || xs[k] > bx)) {
+          bx = xs[k];
+          be = f * 4u + (uint32_t)k;
         }
       }
-      // Only the value part is sorted: the smallest key of the 20th best
-      // value is reached by 20 distinct elements as well.
-      uint32_t lane_ord = 0;
-      if (be != kNone) {
-        const uint32_t e = be - e_lo;
-        const uint32_t xb = b_of(bx);
-        const uint32_t yb = ((bm[e >> 5] >> (e & 31u)) & 1u) ? penalize_bits(xb) : xb;
-        lane_ord = ord_of(yb);
-      }
-      thr = (uint64_t)bcast32(wave_sort_desc_u32(lane_ord, lane), kTopK - 1) << 32;
-      if (lane == 0 && thr != 0) atomicMax(&wg_thr, thr);
     }
+    // Only the value part is sorted: the smallest key of the 20th best
+    // value is reached by 20 distinct elements as well.
+    uint32_t lane_ord = 0;
+    if (be != kNone) {
+      const uint32_t e = be - e_lo;
+      const uint32_t xb = b_of(bx);
+      const uint32_t yb = ((bm[e >> 5] >> (e & 31u)) & 1u) ? penalize_bits(xb) : xb;
+      lane_ord = ord_of(yb);
+    }
+    const uint32_t sorted = wave_sort_desc_u32(lane_ord, lane);
+    thr = (uint64_t)bcast32(sorted, kTopK - 1) << 32;
+    if (lane == 0) {
+      if (thr != 0) atomicMax(&wg_thr, thr);
+      publish_quota((uint64_t)bcast32(sorted, kQuota - 1) << 32);
+    }
+  }
+  // Every wave's seed is in place before any wave filters chunk 0, where the
+  // threshold matters most.
+  __syncthreads();
 
-    uint64_t shared_thr = __hip_atomic_load(&wg_thr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  // The exact (penalised) key of a buffered raw key.
+  auto exact_key = [&](uint64_t key) -> uint64_t {
+    const uint32_t id = key_id(key);
+    const uint32_t e = id - e_lo;
+    if ((bm[e >> 5] >> (e & 31u)) & 1u) return make_key(penalize_bits(key_value_bits(key)), id);
+    return key;
+  };
+
+  // Examines chunk c held in `x4` and reloads each of its float4 with chunk
+  // c + 2.
+  auto stream_chunk = [&](v4f (&x4)[F], uint32_t c) {
+    const uint32_t base = f_lo + c * chunk_f4;
+    uint64_t shared_thr = wg_threshold();
     uint64_t thr_eff = thr > shared_thr ? thr : shared_thr;
     float thr_f = key_floor_value(thr_eff);
-
 #pragma unroll
     for (int j = 0; j < F; ++j) {
       const uint32_t f = base + (uint32_t)j * kBlock + tid;
-      const v4f x = cur[j];
+      const v4f x = x4[j];
       nan_probe = __builtin_fmaf(x.x, 0.0f, nan_probe);
       nan_probe = __builtin_fmaf(x.y, 0.0f, nan_probe);
       nan_probe = __builtin_fmaf(x.z, 0.0f, nan_probe);
@@ -248,50 +336,56 @@ __global__ __launch_bounds__(kBlock) void segment_kernel(RowParams p) {
       const float m = fmaxf(fmaxf(x.x, x.y), fmaxf(x.z, x.w));
       const bool pass = f < f_hi && m >= thr_f;
       if (__ballot(pass)) {
-        // Slow path (rare once the threshold has settled): exact keys.
-        uint32_t nib = 0;
-        if (pass) {
-          const uint32_t e = f * 4u - e_lo;
-          nib = bm[e >> 5] >> (e & 31u);
-        }
+        // Slow path (rare once the threshold has settled): keys of the raw
+        // values.  The penalty only lowers a key, so a raw key below the
+        // threshold is below it penalised as well; the penalty is applied
+        // when the key is merged.
         const float xs[4] = {x.x, x.y, x.z, x.w};
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
           uint64_t key = 0;
           if (pass && xs[k] >= thr_f) {
-            uint32_t yb = b_of(xs[k]);
-            if ((nib >> k) & 1u) yb = penalize_bits(yb);  // rare: most waves skip it
-            key = make_key(yb, f * 4u + (uint32_t)k);
+            key = make_key(b_of(xs[k]), f * 4u + (uint32_t)k);
             if (key < thr_eff) key = 0;
           }
           const uint64_t mask = __ballot(key != 0);
           if (key != 0) my_buf[cnt + lanes_below(mask)] = key;
           cnt += (uint32_t)__popcll((unsigned long long)mask);
-          if (cnt >= kMergeTake) {
+          if (cnt >= kMergeAt) {
             __builtin_amdgcn_wave_barrier();
-            while (cnt >= kMergeTake) {
-              const uint64_t t = merge_round(my_top, my_buf + (cnt - kMergeTake), kMergeTake, lane);
-              cnt -= kMergeTake;
+            while (cnt > 0) {
+              const uint32_t take = cnt < kMergeTake ? cnt : kMergeTake;
+              const uint64_t t = merge_round(my_top, my_buf + (cnt - take), take, lane, exact_key);
+              cnt -= take;
               if (t > thr) thr = t;
             }
-            if (lane == 0 && thr != 0) atomicMax(&wg_thr, thr);
-            shared_thr = __hip_atomic_load(&wg_thr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            if (lane == 0) {
+              if (thr != 0) atomicMax(&wg_thr, thr);
+              publish_quota(my_top[kQuota - 1]);
+            }
+            shared_thr = wg_threshold();
             thr_eff = thr > shared_thr ? thr : shared_thr;
             thr_f = key_floor_value(thr_eff);
           }
         }
       }
+      // The empty asm makes nan_probe final here, so nothing reads x4[j]
+      // past its reload: the reload lands in x4[j]'s own registers and no
+      // copy (and no wait for it) follows.
+      __asm__ volatile("" : "+v"(nan_probe));
+      __builtin_amdgcn_sched_barrier(0);
+      x4[j] = __builtin_nontemporal_load(rowp + min(f + 2u * chunk_f4, f_hi - 1u));
     }
-    if (c + 1 < nchunks) {
-#pragma unroll
-      for (int j = 0; j < F; ++j) cur[j] = nxt[j];
-    }
+  };
+  for (uint32_t c = 0; c < nchunks; c += 2) {
+    stream_chunk(cur, c);
+    stream_chunk(nxt, c + 1);  // past the last chunk: every lane masked
   }
   // drain pending candidates
   __builtin_amdgcn_wave_barrier();
   while (cnt > 0) {
     const uint32_t take = cnt < kMergeTake ? cnt : kMergeTake;
-    merge_round(my_top, my_buf + (cnt - take), take, lane);
+    merge_round(my_top, my_buf + (cnt - take), take, lane, exact_key);
     cnt -= take;
   }
   if (__ballot(nan_probe != nan_probe) && lane == 0) nonfinite_seen = 1u;
