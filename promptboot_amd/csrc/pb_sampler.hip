@@ -55,6 +55,12 @@ constexpr uint32_t kBufCap = 128;                   // candidate slots per wave
 // threshold sooner, and fewer later elements reach the slow path.
 constexpr uint32_t kMergeAt = 24;
 static_assert(kMergeAt >= 1 && kMergeAt - 1 + 64 <= kBufCap, "one ballot of keys must fit");
+// Staged float4 per wave: a float4 whose maximum reaches the threshold is
+// parked in LDS with its index, and the staged float4 are keyed and merged
+// together once per chunk (or when the stage is half full), by one copy of
+// the keying and merging code instead of one per float4 of the unrolled loop.
+constexpr uint32_t kStageCap = 128;
+static_assert(kStageCap >= 2 * 64, "a flush at half capacity leaves room for one ballot");
 constexpr uint32_t kMaxSegments = 32;               // slices per row, at most
 
 // Block index -> work item.  Consecutive work items (the segments of one row,
@@ -99,6 +105,8 @@ __global__ __launch_bounds__(kBlock) void segment_kernel(RowParams p) {
   __shared__ __align__(16) uint32_t bm[kRowWords];
   __shared__ uint64_t top[kWaves][kTopK];
   __shared__ uint64_t buf[kWaves][kBufCap];
+  __shared__ __align__(16) float stage_x[kWaves][kStageCap][4];
+  __shared__ uint32_t stage_f[kWaves][kStageCap];
   __shared__ unsigned long long wg_thr;
   __shared__ uint64_t wave_q[kWaves];  // each wave's kQuota-th best key
   __shared__ uint32_t bad_logit, bad_hist, nonfinite_seen;
@@ -318,13 +326,68 @@ __global__ __launch_bounds__(kBlock) void segment_kernel(RowParams p) {
     return key;
   };
 
+  // Keys the staged float4 (raw values: the penalty only lowers a key, so a
+  // raw key below the threshold is below it penalised as well; the penalty is
+  // applied when the key is merged), appends those reaching the threshold to
+  // the wave's buffer and merges the buffer into the wave's top-20 whenever
+  // kMergeAt keys are pending.  Returns the refreshed threshold floor.
+  float (*my_stage_x)[4] = stage_x[wave];
+  uint32_t* my_stage_f = stage_f[wave];
+  uint32_t nst = 0;  // staged float4 (wave-uniform)
+  uint64_t thr_eff = 0;
+  auto refresh = [&]() -> float {
+    const uint64_t shared_thr = wg_threshold();
+    thr_eff = thr > shared_thr ? thr : shared_thr;
+    return key_floor_value(thr_eff);
+  };
+  auto flush_stage = [&]() -> float {
+    __builtin_amdgcn_wave_barrier();
+    float thr_f = refresh();
+#pragma unroll 1
+    for (uint32_t s0 = 0; s0 < nst; s0 += 64u) {
+      const uint32_t i = s0 + lane;
+      const bool have = i < nst;
+      const v4f x = have ? *reinterpret_cast<const v4f*>(my_stage_x[i]) : v4f{0.f, 0.f, 0.f, 0.f};
+      const uint32_t f = have ? my_stage_f[i] : 0u;
+      // a runtime loop over the four elements: one copy of the merge code
+#pragma unroll 1
+      for (uint32_t k = 0; k < 4u; ++k) {
+        const float xk = k == 0u ? x.x : k == 1u ? x.y : k == 2u ? x.z : x.w;
+        uint64_t key = 0;
+        if (have && xk >= thr_f) {
+          key = make_key(b_of(xk), f * 4u + k);
+          if (key < thr_eff) key = 0;
+        }
+        const uint64_t mask = __ballot(key != 0);
+        if (key != 0) my_buf[cnt + lanes_below(mask)] = key;
+        cnt += (uint32_t)__popcll((unsigned long long)mask);
+        if (cnt >= kMergeAt) {
+          __builtin_amdgcn_wave_barrier();
+          while (cnt > 0) {
+            const uint32_t take = cnt < kMergeTake ? cnt : kMergeTake;
+            const uint64_t t = merge_round(my_top, my_buf + (cnt - take), take, lane, exact_key);
+            cnt -= take;
+            if (t > thr) thr = t;
+          }
+          if (lane == 0) {
+            if (thr != 0) atomicMax(&wg_thr, thr);
+            publish_quota(my_top[kQuota - 1]);
+          }
+          thr_f = refresh();
+        }
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+    nst = 0;
+    return thr_f;
+  };
+
   // Examines chunk c held in `x4` and reloads each of its float4 with chunk
-  // c + 2.
+  // c + 2.  A float4 whose maximum reaches the threshold is staged; the stage
+  // is flushed at the end of the chunk, or as soon as it is half full.
   auto stream_chunk = [&](v4f (&x4)[F], uint32_t c) {
     const uint32_t base = f_lo + c * chunk_f4;
-    uint64_t shared_thr = wg_threshold();
-    uint64_t thr_eff = thr > shared_thr ? thr : shared_thr;
-    float thr_f = key_floor_value(thr_eff);
+    float thr_f = refresh();
 #pragma unroll
     for (int j = 0; j < F; ++j) {
       const uint32_t f = base + (uint32_t)j * kBlock + tid;
@@ -335,39 +398,15 @@ __global__ __launch_bounds__(kBlock) void segment_kernel(RowParams p) {
       nan_probe = __builtin_fmaf(x.w, 0.0f, nan_probe);
       const float m = fmaxf(fmaxf(x.x, x.y), fmaxf(x.z, x.w));
       const bool pass = f < f_hi && m >= thr_f;
-      if (__ballot(pass)) {
-        // Slow path (rare once the threshold has settled): keys of the raw
-        // values.  The penalty only lowers a key, so a raw key below the
-        // threshold is below it penalised as well; the penalty is applied
-        // when the key is merged.
-        const float xs[4] = {x.x, x.y, x.z, x.w};
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          uint64_t key = 0;
-          if (pass && xs[k] >= thr_f) {
-            key = make_key(b_of(xs[k]), f * 4u + (uint32_t)k);
-            if (key < thr_eff) key = 0;
-          }
-          const uint64_t mask = __ballot(key != 0);
-          if (key != 0) my_buf[cnt + lanes_below(mask)] = key;
-          cnt += (uint32_t)__popcll((unsigned long long)mask);
-          if (cnt >= kMergeAt) {
-            __builtin_amdgcn_wave_barrier();
-            while (cnt > 0) {
-              const uint32_t take = cnt < kMergeTake ? cnt : kMergeTake;
-              const uint64_t t = merge_round(my_top, my_buf + (cnt - take), take, lane, exact_key);
-              cnt -= take;
-              if (t > thr) thr = t;
-            }
-            if (lane == 0) {
-              if (thr != 0) atomicMax(&wg_thr, thr);
-              publish_quota(my_top[kQuota - 1]);
-            }
-            shared_thr = wg_threshold();
-            thr_eff = thr > shared_thr ? thr : shared_thr;
-            thr_f = key_floor_value(thr_eff);
-          }
+      const uint64_t pmask = __ballot(pass);
+      if (pmask) {
+        if (pass) {
+          const uint32_t slot = nst + lanes_below(pmask);
+          *reinterpret_cast<v4f*>(my_stage_x[slot]) = x;
+          my_stage_f[slot] = f;
         }
+        nst += (uint32_t)__popcll((unsigned long long)pmask);
+        if (nst > kStageCap - 64u) thr_f = flush_stage();
       }
       // The empty asm makes nan_probe final here, so nothing reads x4[j]
       // past its reload: the reload lands in x4[j]'s own registers and no
@@ -376,6 +415,7 @@ __global__ __launch_bounds__(kBlock) void segment_kernel(RowParams p) {
       __builtin_amdgcn_sched_barrier(0);
       x4[j] = __builtin_nontemporal_load(rowp + min(f + 2u * chunk_f4, f_hi - 1u));
     }
+    if (nst != 0) flush_stage();
   };
   for (uint32_t c = 0; c < nchunks; c += 2) {
     stream_chunk(cur, c);
