@@ -208,7 +208,8 @@ size_t pb_lmhead_packed_bytes(size_t vocab, size_t cols);
 /* Repacks a Q4_0 matrix in promptboot's layout (vocab rows of cols/32 blocks
  * of 18 bytes: fp16 scale, 16 nibble bytes with element i in the low and
  * 16 + i in the high nibble; the token_embd layout of model.rs:810-812) into
- * the device layout.  Device pointers; d_packed 16-byte aligned and
+ * the device layout (tiles of 64 ids: vocab must be a multiple of 64, as
+ * PB_VOCAB is).  Device pointers; d_packed 16-byte aligned and
  * pb_lmhead_packed_bytes long.  Done once per model, outside the decode step. */
 uint32_t pb_lmhead_pack_q4_0(const uint8_t *d_q4, size_t vocab, size_t cols, uint8_t *d_packed,
                              void *stream, pb_inference_error *err);

@@ -353,8 +353,13 @@ size_t pb_lmhead_packed_bytes(size_t vocab, size_t cols) { return vocab * (cols 
 uint32_t pb_lmhead_pack_q4_0(const uint8_t* d_q4, size_t vocab, size_t cols, uint8_t* d_packed,
                              void* stream, pb_inference_error* err) {
   clear_error(err);
-  if (cols == 0 || cols % 32 != 0 || vocab == 0 || vocab > 0xffffffffu) {
+  if (cols == 0 || cols % 32 != 0) {
     set_error(err, PB_CAPACITY, PB_DOMAIN_NONE, 32, cols, PB_FIELD_BYTES, 4);
+    return PB_CAPACITY;
+  }
+  // the device layout groups the vocabulary in tiles of 64 ids
+  if (vocab == 0 || vocab % 64 != 0 || vocab > 0xffffffffu) {
+    set_error(err, PB_CAPACITY, PB_DOMAIN_LOGITS, 64, vocab, PB_FIELD_LOGITS, 1);
     return PB_CAPACITY;
   }
   if (((uintptr_t)d_packed & 15u) != 0) {

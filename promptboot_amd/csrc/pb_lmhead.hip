@@ -10,10 +10,11 @@
 // Kernels, in launch order:
 //   lm_bitmap_kernel   one workgroup per row: the row's history as a 151,936-bit
 //                      bitmap (global), the first bad history position.
-//   lm_q8_kernel       one thread per (row, block): the Q8_0 activations and
-//                      the fp32 activation scale, rows padded to 64 with zeros.
+//   lm_q8_kernel       one thread per (row, block): the Q8_0 activations (in the
+//                      head's contraction order) and the fp32 activation scale
+//                      divided by 16, rows padded to 64 with zeros.
 //   lm_gemm_kernel     one workgroup per (64-id vocabulary tile, 256 rows):
-//                      v_mfma_i32_32x32x32_i8 gives each block's exact int32
+//                      v_mfma_i32_16x16x32_i8 gives each block's exact int32
 //                      dot; the reference's per-block binary32 epilogue runs on
 //                      the VALU.  Writes the raw logits and, per (row, tile),
 //                      the largest penalised 64-bit selection key.
@@ -25,12 +26,14 @@
 //                      selects exactly, and finishes the row (softmax, top-p,
 //                      draw) with the sampler's finalize_row.
 //
-// Weight nibbles are expanded to int8 as (n ^ 8) << 4 = 16 * (n - 8); the
-// factor 16 is removed exactly by pre-scaling the fp16 weight scale by 2^-4,
-// so f32(16 * dot) * (w_scale / 16) rounds exactly like f32(dot) * w_scale.
+// Weight nibbles are stored XOR 8 and expanded to int8 by masking them into
+// the high half of a byte: (n ^ 8) << 4 = 16 * (n - 8) as a signed byte.  The
+// factor 16 is removed exactly in the epilogue (below).
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include <type_traits>
 
 #include "pb_device.h"
 #include "pb_internal.h"
@@ -43,7 +46,6 @@ namespace pb {
 namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
-typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 
@@ -55,6 +57,32 @@ constexpr uint32_t kRowsPerGroup = 256;
 constexpr uint32_t kWordsPerRow = kVocab / 32;
 constexpr uint32_t kTilesPerRow = kVocab / kTileIds;  // 2,374
 constexpr uint32_t kCandCap = 800;       // >= 20 lanes x 38 tile keys
+constexpr uint32_t kTileBytes = kTileIds * 16;  // packed nibbles of one (block, tile)
+// M = 1.5 * 2^23: its binade has unit spacing, so M + i is exact for |i| < 2^22.
+constexpr uint32_t kMagicBits = 0x4b400000u;
+constexpr float kMagic = 12582912.0f;
+
+// Maximum / minimum over the 16 lanes of a DPP row (lanes 16r .. 16r+15), in
+// every lane of the row: quad_perm [1,0,3,2] and [2,3,0,1] combine a quad, row
+// rotations by 4 and 8 combine the four quads.
+__device__ __forceinline__ uint32_t row_dpp(uint32_t v, int ctrl) {
+  switch (ctrl) {
+    case 0: return (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0xB1, 0xF, 0xF, false);
+    case 1: return (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x4E, 0xF, 0xF, false);
+    case 2: return (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x124, 0xF, 0xF, false);
+    default: return (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x128, 0xF, 0xF, false);
+  }
+}
+__device__ __forceinline__ float row16_max(float v) {
+#pragma unroll
+  for (int s = 0; s < 4; ++s) v = fmaxf(v, f_of(row_dpp(b_of(v), s)));
+  return v;
+}
+__device__ __forceinline__ uint32_t row16_min(uint32_t v) {
+#pragma unroll
+  for (int s = 0; s < 4; ++s) v = min(v, row_dpp(v, s));
+  return v;
+}
 
 // cvttss2si semantics (x86 truncation): NaN and out-of-range give INT_MIN.
 __device__ __forceinline__ int32_t trunc_i32_x86(float v) {
@@ -94,9 +122,13 @@ __device__ __forceinline__ uint32_t f32_bits_to_half(uint32_t bits) {
 
 }  // namespace
 
-// ---- repack: promptboot's Q4_0 rows -> block-major nibbles and fp16 scales ----
-// in:  vocab rows of `blocks` x 18 bytes (fp16 scale, 16 nibble bytes)
-// out: [blocks][vocab][16] nibble bytes, then [blocks][vocab] fp16 scales.
+// ---- repack: promptboot's Q4_0 rows -> the head's tile layout ----
+// in:  vocab rows of `blocks` x 18 bytes (fp16 scale, 16 nibble bytes: byte j
+//      holds element j in the low and element 16 + j in the high nibble).
+// out: [blocks][vocab / 64 tiles][1 KB] nibbles, then [blocks][vocab] fp16
+//      scales.  In the kilobyte of (block b, tile t), lane l = 16 q + n of a
+//      head wave reads the 16 bytes at 16 l: word c of them is bytes
+//      4q .. 4q+3 of id 64 t + 4 n + c, every nibble XOR 8.  vocab % 64 == 0.
 __global__ __launch_bounds__(kBlockThreads) void lm_pack_kernel(const uint8_t* __restrict__ in,
                                                                 uint8_t* __restrict__ out,
                                                                 uint32_t vocab, uint32_t blocks) {
@@ -105,14 +137,16 @@ __global__ __launch_bounds__(kBlockThreads) void lm_pack_kernel(const uint8_t* _
   const uint32_t v = (uint32_t)(gid / blocks);
   const uint32_t b = (uint32_t)(gid % blocks);
   const uint8_t* src = in + gid * 18;
-  uint32_t w[4];
+  const uint32_t t = v / kTileIds;
+  const uint32_t n = (v % kTileIds) / 4u;
+  const uint32_t c = v % 4u;
+  uint32_t* tile = reinterpret_cast<uint32_t*>(out + ((size_t)b * (vocab / kTileIds) + t) * kTileBytes);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    w[i] = (uint32_t)src[2 + 4 * i] | ((uint32_t)src[3 + 4 * i] << 8) |
-           ((uint32_t)src[4 + 4 * i] << 16) | ((uint32_t)src[5 + 4 * i] << 24);
+  for (uint32_t q = 0; q < 4; ++q) {
+    const uint32_t w = (uint32_t)src[2 + 4 * q] | ((uint32_t)src[3 + 4 * q] << 8) |
+                       ((uint32_t)src[4 + 4 * q] << 16) | ((uint32_t)src[5 + 4 * q] << 24);
+    tile[(q * 16u + n) * 4u + c] = w ^ 0x88888888u;
   }
-  v4u* dst = reinterpret_cast<v4u*>(out + ((size_t)b * vocab + v) * 16);
-  *dst = v4u{w[0], w[1], w[2], w[3]};
   uint16_t* scales = reinterpret_cast<uint16_t*>(out + (size_t)blocks * vocab * 16);
   scales[(size_t)b * vocab + v] = (uint16_t)(src[0] | (src[1] << 8));
 }
@@ -155,8 +189,10 @@ __global__ __launch_bounds__(kBlockThreads) void lm_bitmap_kernel(LmParams p) {
 }
 
 // ---- Q8_0 activations (inference_prepare_q8) ----
-// act_q: [blocks][rows_pad][32] int8; act_s: [blocks][rows_pad] fp32 scale as
-// the dot uses it (half_to_f32 of the stored fp16).  Pad rows are zero.
+// act_q: [blocks][rows_pad][32] int8 in the head's contraction order: bytes
+// 8q .. 8q+7 hold elements 4q .. 4q+3 and 16+4q .. 16+4q+3 (q = 0..3).
+// act_s: [blocks][rows_pad] the fp32 scale the dot uses (half_to_f32 of the
+// stored fp16) times 2^-4, which is exact.  Pad rows are zero.
 __global__ __launch_bounds__(kBlockThreads) void lm_q8_kernel(LmParams p) {
   const uint32_t gid = blockIdx.x * kBlockThreads + threadIdx.x;
   const uint32_t blocks = p.cols / 32u;
@@ -182,36 +218,66 @@ __global__ __launch_bounds__(kBlockThreads) void lm_q8_kernel(LmParams p) {
       const float v = f_of(x[e]) * inverse;
       const float half = (b_of(v) >> 31) == 0u ? f_of(0x3f000000u) : f_of(0xbf000000u);
       const uint32_t q = (uint32_t)trunc_i32_x86(v + half) & 0xffu;
-      packed[e >> 2] |= q << (8 * (e & 3));
+      packed[2 * ((e & 15) >> 2) + (e >> 4)] |= q << (8 * (e & 3));
     }
   }
   v4u* dst = reinterpret_cast<v4u*>(p.act_q + ((size_t)b * p.rows_pad + row) * 32);
   dst[0] = v4u{packed[0], packed[1], packed[2], packed[3]};
   dst[1] = v4u{packed[4], packed[5], packed[6], packed[7]};
-  p.act_s[(size_t)b * p.rows_pad + row] = act_scale;
+  p.act_s[(size_t)b * p.rows_pad + row] = act_scale * 0.0625f;
 }
 
 // ---- the head: int8 MFMA per block + the reference's binary32 epilogue ----
-// Fragment layout of v_mfma_i32_32x32x32_i8 used here (A and B share it, so
-// the contraction index only has to agree between them): lane l holds row
-// (A) / column (B) l % 32 and contraction elements 16 * (l / 32) + 0..15; the
-// result register r of lane l is D[8 * (r / 4) + 4 * (l / 32) + r % 4][l % 32].
+// Fragment layout of v_mfma_i32_16x16x32_i8 (A and B alike, so only the
+// contraction index has to agree between them): lane l holds row (A) /
+// column (B) l % 16 and eight contraction slots 8 (l / 16) + 0..7 as one
+// 64-bit operand; result register i of lane l is D[4 (l / 16) + i][l % 16].
+// Slots 8q .. 8q+3 carry block elements 4q .. 4q+3 and slots 8q+4 .. 8q+7 the
+// elements 16+4q .. 16+4q+3, so one packed weight word gives both halves of a
+// lane's B operand: its low nibbles and its high nibbles.  MFMA column n of
+// column tile c is vocabulary id v0 + 4n + c: a lane's four columns are four
+// consecutive ids.
+//
+// Epilogue without an int -> float conversion: the accumulator starts at the
+// bit pattern of M = 1.5 * 2^23, so each result word read as binary32 is
+// exactly M + 16 dot (|16 dot| < 2^19).  fma(M + 16 dot, ws, -M ws) is then
+// 16 dot ws rounded once (M ws is exact: ws has at most 11 significant bits),
+// which is 16 times the reference's mul(f32(dot), ws); its product with
+// a_scale / 16 (from lm_q8_kernel) is the reference's
+// mul(mul(f32(dot), ws), a_scale) bit for bit.  Scaling by powers of two is
+// exact here: |16 dot ws| is 0 or lies in [2^-20, 2^36), far from the
+// subnormal and overflow ranges.  A tile with an infinite or NaN fp16 weight
+// scale uses (x - M) * ws instead, which gives inf * 0 = NaN as the
+// reference does.
 __global__ __launch_bounds__(kGemmThreads) void lm_gemm_kernel(LmParams p) {
-  // Activation scales of every block for this group's rows (the epilogue's
-  // per-row multiplier; dynamic LDS of blocks x 256 floats), and this tile's
-  // two history bitmap words per row.
-  extern __shared__ __align__(16) float act_scale[];
+  // Dynamic LDS: the activation scales / 16 of every block for the group's
+  // 256 rows, then this tile's weight scales and -M * weight scales by block.
+  extern __shared__ __align__(16) float lds[];
   __shared__ uint32_t hist_words[kRowsPerGroup][2];
+  const uint32_t blocks = p.cols / 32u;
+  float* act_scale = lds;
+  float* w_scale = lds + blocks * kRowsPerGroup;
+  float* w_neg = w_scale + blocks * kTileIds;
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = tid & 63u;
   const uint32_t wave = tid >> 6;
-  const uint32_t half = lane >> 5;
-  const uint32_t col = lane & 31u;
+  const uint32_t n = lane & 15u;  // MFMA row (A) / column (B)
+  const uint32_t q = lane >> 4;   // contraction quarter; result rows 4q .. 4q+3
   const uint32_t tile = blockIdx.x;
   const uint32_t v0 = tile * kTileIds;
   const uint32_t group0 = blockIdx.y * kRowsPerGroup;
-  const uint32_t blocks = p.cols / 32u;
+  const uint16_t* wscale16 =
+      reinterpret_cast<const uint16_t*>(p.weights + (size_t)blocks * kVocab * 16);
 
+  uint32_t odd = 0;  // this tile has an infinite or NaN weight scale
+  for (uint32_t i = tid; i < blocks * kTileIds; i += kGemmThreads) {
+    const uint32_t b = i / kTileIds;
+    const float ws =
+        __half2float(__ushort_as_half(wscale16[(size_t)b * kVocab + v0 + (i - b * kTileIds)]));
+    w_scale[i] = ws;
+    w_neg[i] = ws * -kMagic;
+    odd |= (b_of(ws) & 0x7f800000u) == 0x7f800000u ? 1u : 0u;
+  }
   for (uint32_t i = tid; i < kRowsPerGroup * 2; i += kGemmThreads) {
     const uint32_t r = group0 + i / 2;
     (&hist_words[0][0])[i] = r < p.rows ? p.bitmap[(size_t)r * kWordsPerRow + v0 / 32 + i % 2] : 0u;
@@ -221,70 +287,71 @@ __global__ __launch_bounds__(kGemmThreads) void lm_gemm_kernel(LmParams p) {
     const uint32_t r = group0 + (i - b * kRowsPerGroup);
     act_scale[i] = r < p.rows_pad ? p.act_s[(size_t)b * p.rows_pad + r] : 0.0f;
   }
-  __syncthreads();
+  const bool odd_tile = __syncthreads_or((int)odd) != 0;
 
   const uint32_t rw0 = group0 + wave * kRowsPerWave;  // this wave's 32 rows
   if (rw0 >= p.rows_pad) return;  // whole wave idle (no barrier follows)
   const uint32_t lrow0 = wave * kRowsPerWave;       // first row inside the group
 
-  float total[2][16];
+  float total[2][4][4];  // [row tile][column tile][result register]
 #pragma unroll
-  for (int c = 0; c < 2; ++c)
+  for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) total[c][r] = 0.0f;
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) total[rt][c][i] = 0.0f;
 
-  const uint32_t nib_shift = half ? 0u : 4u;  // low nibbles for elements 0..15
-  const v16i zero = {};
-  const uint16_t* wscale = reinterpret_cast<const uint16_t*>(p.weights + (size_t)blocks * kVocab * 16);
-  const int8_t* a_base = p.act_q + ((size_t)rw0 + col) * 32 + 16u * half;
-  const uint8_t* w_base = p.weights + ((size_t)v0 + col) * 16;
+  const v4i magic = {(int)kMagicBits, (int)kMagicBits, (int)kMagicBits, (int)kMagicBits};
+  const uint8_t* a_base = reinterpret_cast<const uint8_t*>(p.act_q) + ((size_t)rw0 + n) * 32 + 8u * q;
+  const size_t a_stride = (size_t)p.rows_pad * 32;  // bytes per block
+  const v4u* w_base = reinterpret_cast<const v4u*>(p.weights + (size_t)tile * kTileBytes) + lane;
+  const size_t w_stride = (size_t)kTilesPerRow * (kTileBytes / 16);  // uint4 per block
 
-  // Operands of one block: the activation fragment, both column tiles'
-  // packed nibbles and weight scales.  Two sets alternate (the loop is
-  // unrolled by two), so the next block's loads are in flight while the
-  // current block runs and no registers are copied between iterations.
+  // Operands of one block: both row tiles' activation fragments and the
+  // lane's packed weight words (one per column tile).  Two sets alternate
+  // (the loop is unrolled by two), so the next block's loads are in flight
+  // while the current block runs and no registers are copied.
   struct Operands {
-    v4i a;
-    v4u raw[2];
-    uint16_t wsh[2];
+    uint64_t a[2];
+    v4u raw;
   };
   auto load = [&](uint32_t b, Operands& o) {
-    o.a = *reinterpret_cast<const v4i*>(a_base + (size_t)b * p.rows_pad * 32);
-#pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      const size_t vid = (size_t)b * kVocab + 32u * c;
-      o.raw[c] = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(w_base + vid * 16));
-      o.wsh[c] = wscale[vid + v0 + col];
-    }
+    const uint8_t* ab = a_base + (size_t)b * a_stride;
+    o.a[0] = *reinterpret_cast<const uint64_t*>(ab);
+    o.a[1] = *reinterpret_cast<const uint64_t*>(ab + 16u * 32u);
+    o.raw = w_base[(size_t)b * w_stride];
   };
-  auto run = [&](uint32_t b, const Operands& o) {
-    // this block's 16 activation scales per lane (rows 8g + 4 * half + 0..3)
-    v4f as[4];
+  auto run = [&](uint32_t b, const Operands& o, auto odd_tag) {
+    constexpr bool kOdd = decltype(odd_tag)::value;
+    const v4f ws = *reinterpret_cast<const v4f*>(&w_scale[b * kTileIds + 4u * n]);
+    const v4f wn = *reinterpret_cast<const v4f*>(&w_neg[b * kTileIds + 4u * n]);
+    v4f as[2];
 #pragma unroll
-    for (int g = 0; g < 4; ++g)
-      as[g] = *reinterpret_cast<const v4f*>(
-          &act_scale[b * kRowsPerGroup + lrow0 + 8u * g + 4u * half]);
-    v16i d[2];
+    for (int rt = 0; rt < 2; ++rt)
+      as[rt] = *reinterpret_cast<const v4f*>(
+          &act_scale[b * kRowsPerGroup + lrow0 + 16u * rt + 4u * q]);
+    const uint32_t raw[4] = {o.raw.x, o.raw.y, o.raw.z, o.raw.w};
+    v4i d[2][4];
 #pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      const v4u raw = o.raw[c];
-      const v4i w = {(int)((((raw.x << nib_shift) & 0xf0f0f0f0u) ^ 0x80808080u)),
-                     (int)((((raw.y << nib_shift) & 0xf0f0f0f0u) ^ 0x80808080u)),
-                     (int)((((raw.z << nib_shift) & 0xf0f0f0f0u) ^ 0x80808080u)),
-                     (int)((((raw.w << nib_shift) & 0xf0f0f0f0u) ^ 0x80808080u))};
-      d[c] = __builtin_amdgcn_mfma_i32_32x32x32_i8(o.a, w, zero, 0, 0, 0);
+    for (int c = 0; c < 4; ++c) {
+      const uint64_t w = (uint64_t)((raw[c] << 4) & 0xf0f0f0f0u) |
+                         ((uint64_t)(raw[c] & 0xf0f0f0f0u) << 32);
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt)
+        d[rt][c] = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)o.a[rt], (long)w, magic, 0, 0, 0);
     }
+    const float wsv[4] = {ws.x, ws.y, ws.z, ws.w};
+    const float wnv[4] = {wn.x, wn.y, wn.z, wn.w};
 #pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      const float ws = __half2float(__ushort_as_half(o.wsh[c])) * 0.0625f;
+    for (int rt = 0; rt < 2; ++rt) {
+      const float asv[4] = {as[rt].x, as[rt].y, as[rt].z, as[rt].w};
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const float asv[4] = {as[g].x, as[g].y, as[g].z, as[g].w};
+      for (int c = 0; c < 4; ++c) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int r = 4 * g + j;
-          const float scaled = (float)d[c][r] * ws;
-          total[c][r] = total[c][r] + scaled * asv[j];
+        for (int i = 0; i < 4; ++i) {
+          const float x = __int_as_float(d[rt][c][i]);
+          const float y = kOdd ? (x - kMagic) * wsv[c] : __builtin_fmaf(x, wsv[c], wnv[c]);
+          total[rt][c][i] = total[rt][c][i] + y * asv[i];
         }
       }
     }
@@ -296,62 +363,83 @@ __global__ __launch_bounds__(kGemmThreads) void lm_gemm_kernel(LmParams p) {
   // Both halves of the loop body run unconditionally (an odd last block is a
   // tail), and scheduling barriers keep each prefetch ahead of the compute it
   // overlaps: otherwise the loads are sunk next to their first use.
-  const uint32_t last = blocks - 1u;
-  Operands even, odd;
-  load(0, even);
+  auto gemm = [&](auto odd_tag) {
+    const uint32_t last = blocks - 1u;
+    Operands even, odd_ops;
+    load(0, even);
 #pragma unroll 1
-  for (uint32_t b = 0; b + 1u < blocks; b += 2) {
-    load(b + 1u, odd);
-    __builtin_amdgcn_sched_barrier(0);
-    run(b, even);
-    __builtin_amdgcn_sched_barrier(0);
-    load(min(b + 2u, last), even);
-    __builtin_amdgcn_sched_barrier(0);
-    run(b + 1u, odd);
-    __builtin_amdgcn_sched_barrier(0);
+    for (uint32_t b = 0; b + 1u < blocks; b += 2) {
+      load(b + 1u, odd_ops);
+      __builtin_amdgcn_sched_barrier(0);
+      run(b, even, odd_tag);
+      __builtin_amdgcn_sched_barrier(0);
+      load(min(b + 2u, last), even);
+      __builtin_amdgcn_sched_barrier(0);
+      run(b + 1u, odd_ops, odd_tag);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (blocks & 1u) run(last, even, odd_tag);
+  };
+  if (odd_tile) {
+    gemm(std::true_type{});
+  } else {
+    gemm(std::false_type{});
   }
-  if (blocks & 1u) run(last, even);
 
-  // logits, non-finite check, per-row tile maximum of the penalised keys
+  // Logits, non-finite probe, history penalty and, per row, the tile's
+  // largest penalised key.  Lanes 16q .. 16q+15 hold the 64 ids of rows
+  // 4q + i of each row tile, four consecutive ids per lane.
+  float probe = 0.0f;
 #pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const uint32_t row = rw0 + 8u * (r / 4) + 4u * half + (r % 4);
-    const bool live = row < p.rows;
-    // The lane's better element of its two columns (the lower id on equal
-    // values), kept as (value order, id, sign of zero): the largest key of
-    // the row's 64 ids is then a 32-lane maximum of the value order followed
-    // by a minimum of the id among the lanes holding it.
-    uint32_t best_ord = 0, best_tag = 0;
+  for (int rt = 0; rt < 2; ++rt) {
 #pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      const uint32_t v = v0 + 32u * c + col;
-      const uint32_t xb = b_of(total[c][r]);
-      if (live) {
-        p.logits[(size_t)row * p.logits_ld + v] = xb;
-        if ((xb & 0x7f800000u) == 0x7f800000u) atomicMin(&p.meta[row * 2], v);
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t lr = lrow0 + 16u * rt + 4u * q + (uint32_t)i;
+      const uint32_t row = group0 + lr;
+      const bool live = row < p.rows;
+      float y[4] = {total[rt][0][i], total[rt][1][i], total[rt][2][i], total[rt][3][i]};
+      if (live)
+        *reinterpret_cast<v4f*>(p.logits + (size_t)row * p.logits_ld + v0 + 4u * n) =
+            v4f{y[0], y[1], y[2], y[3]};
+#pragma unroll
+      for (int c = 0; c < 4; ++c) probe = __builtin_fmaf(y[c], 0.0f, probe);
+      const uint32_t hb = live ? (hist_words[lr][n >> 3] >> (4u * (n & 7u))) & 0xfu : 0u;
+      if (hb != 0u) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          if ((hb >> c) & 1u) y[c] = f_of(penalize_bits(b_of(y[c])));
       }
-      const bool member = live && ((hist_words[row - group0][c] >> col) & 1u) != 0u;
-      const uint32_t yb = member ? penalize_bits(xb) : xb;
-      const uint32_t ord = ord_of(yb);
-      if (c == 0 || ord > best_ord) {
-        best_ord = ord;
-        best_tag = (v << 1) | (yb == 0x80000000u ? 1u : 0u);
+      // The row's best element of the tile: the largest value (-0 == +0),
+      // then the lowest id holding it, with that element's sign of zero.
+      const float m = row16_max(fmaxf(fmaxf(y[0], y[1]), fmaxf(y[2], y[3])));
+      uint32_t pick = 0xffffffffu;
+#pragma unroll
+      for (int c = 3; c >= 0; --c) {
+        if (y[c] == m)
+          pick = ((4u * n + (uint32_t)c) << 1) | (b_of(y[c]) == 0x80000000u ? 1u : 0u);
+      }
+      pick = row16_min(pick);
+      if (live && n == 0u) {
+        const uint32_t id = v0 + (pick >> 1);
+        const uint32_t low = ((0x3ffffu - id) << 1) | (pick & 1u);  // make_key's low word
+        p.tilemax[(size_t)row * kTilesPerRow + tile] = ((uint64_t)ord_of(b_of(m)) << 32) | low;
       }
     }
-    uint32_t top_ord = best_ord;
+  }
+  if (__ballot(probe != probe)) {
+    // a non-finite raw logit in this wave's rows: lower each row's first index
 #pragma unroll
-    for (uint32_t m = 1; m < 32; m <<= 1) {
-      const uint32_t o = lane_xor(top_ord, m, lane);
-      top_ord = o > top_ord ? o : top_ord;
-    }
-    uint32_t tag = best_ord == top_ord ? best_tag : 0xffffffffu;
+    for (int rt = 0; rt < 2; ++rt) {
 #pragma unroll
-    for (uint32_t m = 1; m < 32; m <<= 1) {
-      const uint32_t o = lane_xor(tag, m, lane);
-      tag = o < tag ? o : tag;
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t row = group0 + lrow0 + 16u * rt + 4u * q + (uint32_t)i;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          if (row < p.rows && (b_of(total[rt][c][i]) & 0x7f800000u) == 0x7f800000u)
+            atomicMin(&p.meta[row * 2], v0 + 4u * n + (uint32_t)c);
+        }
+      }
     }
-    const uint32_t low = ((0x3ffffu - (tag >> 1)) << 1) | (tag & 1u);  // make_key's low word
-    if (live && col == 0) p.tilemax[(size_t)row * kTilesPerRow + tile] = ((uint64_t)top_ord << 32) | low;
   }
 }
 
@@ -433,28 +521,34 @@ __global__ __launch_bounds__(kBlockThreads) void lm_select_kernel(LmParams p, Ro
   finalize_row(rp, row, key, kNone, kNone, lane);
 }
 
-// MFMA layout self-test (one wave): A[i][k] = (7i + 3k) % 17 - 8,
-// B[k][j] = (5k + 11j) % 15 - 7, D written as out[32 * i + j] through the
-// fragment mapping the head uses.
+// MFMA layout self-test (one wave): A[i][k] = (7i + 3k) % 17 - 8 and
+// B[k][j] = (5k + 11j) % 15 - 7 for i, j, k < 32, multiplied as four 16 x 16
+// tiles through the head's fragment mapping, contraction order and
+// accumulator start M: out[32 * i + j] = (D[i][j] read as binary32) - M.
 __global__ __launch_bounds__(64) void mfma_selftest_kernel(int32_t* out) {
   const uint32_t lane = lane_id();
-  const uint32_t half = lane >> 5;
-  const uint32_t idx = lane & 31u;
-  uint32_t a[4] = {0u, 0u, 0u, 0u}, b[4] = {0u, 0u, 0u, 0u};
-  for (uint32_t pos = 0; pos < 16; ++pos) {
-    const uint32_t k = 16u * half + pos;
-    const int av = (int)((7u * idx + 3u * k) % 17u) - 8;
-    const int bv = (int)((5u * k + 11u * idx) % 15u) - 7;
-    a[pos >> 2] |= ((uint32_t)av & 0xffu) << (8 * (pos & 3));
-    b[pos >> 2] |= ((uint32_t)bv & 0xffu) << (8 * (pos & 3));
-  }
-  const v4i av = {(int)a[0], (int)a[1], (int)a[2], (int)a[3]};
-  const v4i bv = {(int)b[0], (int)b[1], (int)b[2], (int)b[3]};
-  const v16i zero = {};
-  const v16i d = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv, zero, 0, 0, 0);
-  for (int r = 0; r < 16; ++r) {
-    const uint32_t i = 8u * (r / 4) + 4u * half + (r % 4);
-    out[32 * i + idx] = d[r];
+  const uint32_t n = lane & 15u;
+  const uint32_t q = lane >> 4;
+  const v4i magic = {(int)kMagicBits, (int)kMagicBits, (int)kMagicBits, (int)kMagicBits};
+  for (uint32_t ti = 0; ti < 2; ++ti) {
+    for (uint32_t tj = 0; tj < 2; ++tj) {
+      uint64_t a = 0, b = 0;
+      for (uint32_t slot = 0; slot < 8; ++slot) {
+        const uint32_t k = slot < 4 ? 4u * q + slot : 16u + 4u * q + (slot - 4u);
+        const uint32_t i = 16u * ti + n;
+        const uint32_t j = 16u * tj + n;
+        const int av = (int)((7u * i + 3u * k) % 17u) - 8;
+        const int bv = (int)((5u * k + 11u * j) % 15u) - 7;
+        a |= (uint64_t)((uint32_t)av & 0xffu) << (8 * slot);
+        b |= (uint64_t)((uint32_t)bv & 0xffu) << (8 * slot);
+      }
+      const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)a, (long)b, magic, 0, 0, 0);
+      for (int r = 0; r < 4; ++r) {
+        const uint32_t i = 16u * ti + 4u * q + (uint32_t)r;
+        const uint32_t j = 16u * tj + n;
+        out[32 * i + j] = (int32_t)(__int_as_float(d[r]) - kMagic);
+      }
+    }
   }
 }
 
@@ -466,6 +560,10 @@ hipError_t launch_lm_pack(const uint8_t* in, uint8_t* out, uint32_t vocab, uint3
   return hipGetLastError();
 }
 
+size_t gemm_lds_bytes(uint32_t cols) {
+  return (size_t)(cols / 32u) * (kRowsPerGroup + 2u * kTileIds) * sizeof(float);
+}
+
 hipError_t launch_lm_sample(const LmParams& p, const RowParams& rp, hipStream_t stream) {
   hipLaunchKernelGGL(lm_bitmap_kernel, dim3(p.rows), dim3(kBlockThreads), 0, stream, p);
   const uint32_t q8_threads = p.rows_pad * (p.cols / 32u);
@@ -473,8 +571,7 @@ hipError_t launch_lm_sample(const LmParams& p, const RowParams& rp, hipStream_t 
                      dim3(kBlockThreads), 0, stream, p);
   hipLaunchKernelGGL(lm_gemm_kernel,
                      dim3(kTilesPerRow, (p.rows_pad + kRowsPerGroup - 1) / kRowsPerGroup),
-                     dim3(kGemmThreads), (p.cols / 32u) * kRowsPerGroup * sizeof(float), stream,
-                     p);
+                     dim3(kGemmThreads), gemm_lds_bytes(p.cols), stream, p);
   hipLaunchKernelGGL(lm_select_kernel, dim3((p.rows + 3) / 4), dim3(kBlockThreads), 0, stream,
                      p, rp);
   return hipGetLastError();

@@ -160,3 +160,16 @@ def test_decode_step_argument_errors_need_no_device():
     st = s.lib().pb_decode_step(None, None, s.VOCAB + 1, s.VOCAB, 0, None, 0, None, None, None,
                                 None, None, None, None, None, ctypes.byref(e))
     assert st == s.CAPACITY and e.needed == s.VOCAB and e.available == s.VOCAB + 1
+
+
+def test_lmhead_pack_argument_errors_need_no_device():
+    """The packed head groups the vocabulary in 64-id tiles; other sizes and
+    hidden widths that are not whole Q4_0 blocks are rejected before any
+    device work."""
+    import ctypes
+
+    e = s._Error()
+    st = s.lib().pb_lmhead_pack_q4_0(None, s.VOCAB + 32, 896, None, None, ctypes.byref(e))
+    assert st == s.CAPACITY and e.needed == 64 and e.available == s.VOCAB + 32
+    st = s.lib().pb_lmhead_pack_q4_0(None, s.VOCAB, 900, None, None, ctypes.byref(e))
+    assert st == s.CAPACITY and e.needed == 32 and e.available == 900

@@ -123,3 +123,79 @@ def test_error_rows(smp, head):
     assert gerr["available"][2] == V + 7 and gerr["available"][3] == V
     assert (gtok == rtok).all()
     assert (gdet[0]["ids"] == rdet[0]["ids"]).all()
+
+
+def _set_scales(q4, edits):
+    """q4: [V, blocks, 18] uint8; edits: {(id, block): fp16 bits}."""
+    for (v, b), bits in edits.items():
+        q4[v, b, 0] = bits & 0xFF
+        q4[v, b, 1] = bits >> 8
+
+
+def test_special_weight_and_activation_scales(smp, head):
+    """Edge scales through both epilogue forms of the head.  Finite scales
+    (signed zeros, +-1, fp16 subnormals, +-65504) sit in tiles that take the
+    fused multiply-add form; +-inf and NaN sit in tiles of their own, which
+    take the subtract-then-multiply form (inf * 0 = NaN as in the reference).
+    The hidden rows give activation scales that are normal, fp16-subnormal,
+    zero for one block, and infinite (amax / 127 above fp16's range).
+    Logits are compared bit for bit with the oracle, NaN positions as a set."""
+    import torch
+
+    w, _ = head
+    blocks = workloads.HIDDEN // 32
+    q4 = w["q4"].reshape(V, blocks, 18).copy()
+    finite = [0x0000, 0x8000, 0x3C00, 0xBC00, 0x0001, 0x03FF, 0x7BFF, 0xFBFF]
+    edits = {}
+    for j, bits in enumerate(finite):   # tiles 10 .. 17, assorted ids and blocks
+        edits[(64 * (10 + j) + 5 * j + 1, (3 * j) % blocks)] = bits
+        edits[(64 * (10 + j) + 63, blocks - 1)] = bits
+    for j, bits in enumerate([0x7C00, 0xFC00, 0x7E00]):  # tiles 100 .. 102
+        edits[(64 * (100 + j) + 7 * j, j)] = bits
+    edits[(64 * 103 + 40, blocks - 1)] = 0x7C00          # inf in the last block only
+    _set_scales(q4, edits)
+    packed = smp.pack_lmhead(torch.from_numpy(q4.reshape(-1)).to("cuda:0"))
+    rng = np.random.default_rng(5)
+    hidden = np.empty((4, workloads.HIDDEN), np.float32)
+    hidden[0] = rng.standard_normal(workloads.HIDDEN)
+    hidden[1] = rng.standard_normal(workloads.HIDDEN) * np.float32(1e-4)   # subnormal fp16 scales
+    hidden[2] = rng.standard_normal(workloads.HIDDEN)
+    hidden[2, 64:96] = 0.0                                                # one all-zero block
+    hidden[3] = rng.standard_normal(workloads.HIDDEN) * np.float32(1e7)    # amax / 127 -> inf
+    glog, _, _, _ = run_head(smp, packed, hidden, w["hist"][:4], w["hist_len"][:4],
+                             w["random_24"][:4])
+    rlog = o.lmhead_logits(hidden, q4.reshape(-1), V, workloads.HIDDEN, threads=16)
+    gnan = np.isnan(glog.view(np.float32))
+    rnan = np.isnan(rlog.view(np.float32))
+    assert (gnan == rnan).all()
+    bad = np.argwhere((glog != rlog) & ~rnan)
+    assert bad.size == 0, (bad[:5], glog[tuple(bad[0])], rlog[tuple(bad[0])])
+    # the edits really reach special values: inf and NaN columns exist
+    assert rnan[0].any() and np.isinf(rlog.view(np.float32)[0]).any()
+
+
+def test_widest_hidden_state(smp):
+    """cols = 2048, the widest the head accepts (its per-block scales then take
+    96 KB of the workgroup's LDS): logits bit-exact for three rows."""
+    import torch
+
+    cols, rows = 2048, 3
+    rng = np.random.default_rng(11)
+    blocks = cols // 32
+    q4 = rng.integers(0, 256, (V, blocks, 18), dtype=np.uint8)
+    sc = rng.uniform(0.001, 0.02, (V, blocks)).astype(np.float16).view(np.uint16)
+    q4[:, :, 0] = sc & 0xFF
+    q4[:, :, 1] = sc >> 8
+    packed = smp.pack_lmhead(torch.from_numpy(q4.reshape(-1)).to("cuda:0"), cols=cols)
+    hidden = rng.standard_normal((rows, cols)).astype(np.float32)
+    r24 = np.arange(rows, dtype=np.uint32) * 977
+    token = torch.empty(rows, dtype=torch.int32, device="cuda:0")
+    logits = torch.empty((rows, V), dtype=torch.int32, device="cuda:0")
+    smp.lmhead_sample(packed, to_dev(hidden), to_dev(r24), token=token, logits=logits, cols=cols)
+    torch.cuda.synchronize()
+    glog = logits.cpu().numpy().view(np.uint32)
+    rlog = o.lmhead_logits(hidden, q4.reshape(-1), V, cols, threads=16)
+    assert (glog == rlog).all()
+    rtok, _, _, _ = o.sample_batch(rlog, np.zeros((rows, 1), np.uint32),
+                                   np.zeros(rows, np.uint32), r24, threads=4)
+    assert (token.cpu().numpy().view(np.uint32) == rtok).all()
