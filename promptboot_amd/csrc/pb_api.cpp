@@ -409,7 +409,7 @@ static uint32_t enqueue_lmhead(pb_context* ctx, const uint8_t* d_packed, size_t 
   const size_t meta_b = align((size_t)rows * 8);
   const size_t actq_b = align((size_t)blocks * rows_pad * 32);
   const size_t acts_b = align((size_t)blocks * rows_pad * 4);
-  const size_t tile_b = align((size_t)rows * (PB_VOCAB / 64) * 8);
+  const size_t tile_b = align((size_t)rows * (PB_VOCAB / 64) * 4);
   const size_t logit_b = d_logits ? 0 : align((size_t)rows * PB_VOCAB * 4);
   const size_t need = bitmap_b + meta_b + actq_b + acts_b + tile_b + logit_b;
   DeviceGuard guard(ctx->device);
@@ -438,7 +438,7 @@ static uint32_t enqueue_lmhead(pb_context* ctx, const uint8_t* d_packed, size_t 
   p.meta = reinterpret_cast<uint32_t*>(base + bitmap_b);
   p.act_q = reinterpret_cast<int8_t*>(base + bitmap_b + meta_b);
   p.act_s = reinterpret_cast<float*>(base + bitmap_b + meta_b + actq_b);
-  p.tilemax = reinterpret_cast<uint64_t*>(base + bitmap_b + meta_b + actq_b + acts_b);
+  p.tilemax = reinterpret_cast<uint32_t*>(base + bitmap_b + meta_b + actq_b + acts_b);
   p.logits = d_logits ? d_logits
                       : reinterpret_cast<uint32_t*>(base + bitmap_b + meta_b + actq_b + acts_b +
                                                     tile_b);

@@ -67,7 +67,7 @@ struct LmParams {
   float* act_s;             // [blocks][rows_pad] activation scales
   uint32_t* logits;         // rows x logits_ld raw logits (binary32 words)
   size_t logits_ld;
-  uint64_t* tilemax;        // rows x 2,374 largest penalised key per 64-id tile
+  uint32_t* tilemax;        // rows x 2,374 order word of the largest penalised value per 64-id tile
 };
 
 hipError_t launch_lm_pack(const uint8_t* in, uint8_t* out, uint32_t vocab, uint32_t blocks,

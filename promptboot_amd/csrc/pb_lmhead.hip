@@ -8,21 +8,21 @@
 // followed by the sampler of pb_sampler.hip on the resulting logits rows.
 //
 // Kernels, in launch order:
-//   lm_bitmap_kernel   one workgroup per row: the row's history as a 151,936-bit
-//                      bitmap (global), the first bad history position.
-//   lm_q8_kernel       one thread per (row, block): the Q8_0 activations (in the
-//                      head's contraction order) and the fp32 activation scale
-//                      divided by 16, rows padded to 64 with zeros.
+//   lm_prep_kernel     one workgroup per row (rows padded to 64): the Q8_0
+//                      activations (in the head's contraction order) and the
+//                      fp32 activation scales divided by 16, zeros for pad
+//                      rows; the row's history as a 151,936-bit bitmap
+//                      (global) and its first bad history position.
 //   lm_gemm_kernel     one workgroup per (64-id vocabulary tile, 256 rows):
 //                      v_mfma_i32_16x16x32_i8 gives each block's exact int32
 //                      dot; the reference's per-block binary32 epilogue runs on
 //                      the VALU.  Writes the raw logits and, per (row, tile),
-//                      the largest penalised 64-bit selection key.
+//                      the order word of the largest penalised value.
 //   lm_select_kernel   one wave per row: the row's top-20 lies inside the 20
-//                      tiles with the largest tile keys (each of the 20 best
-//                      tile maxima is a distinct element at least as good as
-//                      the 20th best of them, so every top-20 element sits in
-//                      one of those tiles); it re-reads those 1,280 logits,
+//                      tiles with the largest maxima (each of the 20 best tile
+//                      maxima is a distinct element at least as good as the
+//                      20th best of them, so every top-20 element sits in one
+//                      of those tiles); it re-reads those 1,280 logits,
 //                      selects exactly, and finishes the row (softmax, top-p,
 //                      draw) with the sampler's finalize_row.
 //
@@ -62,7 +62,7 @@ constexpr uint32_t kTileBytes = kTileIds * 16;  // packed nibbles of one (block,
 constexpr uint32_t kMagicBits = 0x4b400000u;
 constexpr float kMagic = 12582912.0f;
 
-// Maximum / minimum over the 16 lanes of a DPP row (lanes 16r .. 16r+15), in
+// Maximum over the 16 lanes of a DPP row (lanes 16r .. 16r+15), in
 // every lane of the row: quad_perm [1,0,3,2] and [2,3,0,1] combine a quad, row
 // rotations by 4 and 8 combine the four quads.
 __device__ __forceinline__ uint32_t row_dpp(uint32_t v, int ctrl) {
@@ -76,11 +76,6 @@ __device__ __forceinline__ uint32_t row_dpp(uint32_t v, int ctrl) {
 __device__ __forceinline__ float row16_max(float v) {
 #pragma unroll
   for (int s = 0; s < 4; ++s) v = fmaxf(v, f_of(row_dpp(b_of(v), s)));
-  return v;
-}
-__device__ __forceinline__ uint32_t row16_min(uint32_t v) {
-#pragma unroll
-  for (int s = 0; s < 4; ++s) v = min(v, row_dpp(v, s));
   return v;
 }
 
@@ -151,12 +146,51 @@ __global__ __launch_bounds__(kBlockThreads) void lm_pack_kernel(const uint8_t* _
   scales[(size_t)b * vocab + v] = (uint16_t)(src[0] | (src[1] << 8));
 }
 
-// ---- per-row history bitmap and first bad history position ----
-__global__ __launch_bounds__(kBlockThreads) void lm_bitmap_kernel(LmParams p) {
+// ---- Q8_0 activations of one (row, block) (inference_prepare_q8) ----
+// act_q: [blocks][rows_pad][32] int8 in the head's contraction order: bytes
+// 8q .. 8q+7 hold elements 4q .. 4q+3 and 16+4q .. 16+4q+3 (q = 0..3).
+// act_s: [blocks][rows_pad] the fp32 scale the dot uses (half_to_f32 of the
+// stored fp16) times 2^-4, which is exact.  Pad rows are zero.
+__device__ __forceinline__ void quantize_block(const LmParams& p, uint32_t row, uint32_t b) {
+  uint32_t packed[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
+  float act_scale = 0.0f;
+  if (row < p.rows) {
+    const uint32_t* x = p.hidden + (size_t)row * p.cols + b * 32u;
+    uint32_t maximum = 0u;
+#pragma unroll
+    for (int e = 0; e < 32; ++e) {
+      const uint32_t magnitude = x[e] & 0x7fffffffu;
+      if (f_of(magnitude) > f_of(maximum)) maximum = magnitude;
+    }
+    const float scale = f_of(maximum) / f_of(0x42fe0000u);  // / 127
+    const uint32_t h = f32_bits_to_half(b_of(scale));
+    act_scale = f_of(half_to_f32_bits(h));
+    const float inverse = b_of(scale) == 0u ? 0.0f : f_of(0x3f800000u) / scale;
+#pragma unroll
+    for (int e = 0; e < 32; ++e) {
+      const float v = f_of(x[e]) * inverse;
+      const float half = (b_of(v) >> 31) == 0u ? f_of(0x3f000000u) : f_of(0xbf000000u);
+      const uint32_t q = (uint32_t)trunc_i32_x86(v + half) & 0xffu;
+      packed[2 * ((e & 15) >> 2) + (e >> 4)] |= q << (8 * (e & 3));
+    }
+  }
+  v4u* dst = reinterpret_cast<v4u*>(p.act_q + ((size_t)b * p.rows_pad + row) * 32);
+  dst[0] = v4u{packed[0], packed[1], packed[2], packed[3]};
+  dst[1] = v4u{packed[4], packed[5], packed[6], packed[7]};
+  p.act_s[(size_t)b * p.rows_pad + row] = act_scale * 0.0625f;
+}
+
+// ---- per row: Q8_0 activations, history bitmap, first bad history position ----
+// One workgroup per padded row: threads 0 .. blocks-1 quantise the row's
+// blocks (pad rows get zeros) while the workgroup builds the row's 151,936-bit
+// history bitmap in LDS and writes it out.
+__global__ __launch_bounds__(kBlockThreads) void lm_prep_kernel(LmParams p) {
   __shared__ uint32_t bm[kWordsPerRow];
   __shared__ uint32_t bad;
   const uint32_t row = blockIdx.x;
   const uint32_t tid = threadIdx.x;
+  if (tid < p.cols / 32u) quantize_block(p, row, tid);
+  if (row >= p.rows) return;  // pad row: the whole workgroup leaves here
   for (uint32_t i = tid; i < kWordsPerRow; i += kBlockThreads) bm[i] = 0u;
   if (tid == 0) bad = kNone;
   __syncthreads();
@@ -188,45 +222,6 @@ __global__ __launch_bounds__(kBlockThreads) void lm_bitmap_kernel(LmParams p) {
   }
 }
 
-// ---- Q8_0 activations (inference_prepare_q8) ----
-// act_q: [blocks][rows_pad][32] int8 in the head's contraction order: bytes
-// 8q .. 8q+7 hold elements 4q .. 4q+3 and 16+4q .. 16+4q+3 (q = 0..3).
-// act_s: [blocks][rows_pad] the fp32 scale the dot uses (half_to_f32 of the
-// stored fp16) times 2^-4, which is exact.  Pad rows are zero.
-__global__ __launch_bounds__(kBlockThreads) void lm_q8_kernel(LmParams p) {
-  const uint32_t gid = blockIdx.x * kBlockThreads + threadIdx.x;
-  const uint32_t blocks = p.cols / 32u;
-  if (gid >= p.rows_pad * blocks) return;
-  const uint32_t row = gid / blocks;
-  const uint32_t b = gid - row * blocks;
-  uint32_t packed[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
-  float act_scale = 0.0f;
-  if (row < p.rows) {
-    const uint32_t* x = p.hidden + (size_t)row * p.cols + b * 32u;
-    uint32_t maximum = 0u;
-#pragma unroll
-    for (int e = 0; e < 32; ++e) {
-      const uint32_t magnitude = x[e] & 0x7fffffffu;
-      if (f_of(magnitude) > f_of(maximum)) maximum = magnitude;
-    }
-    const float scale = f_of(maximum) / f_of(0x42fe0000u);  // / 127
-    const uint32_t h = f32_bits_to_half(b_of(scale));
-    act_scale = f_of(half_to_f32_bits(h));
-    const float inverse = b_of(scale) == 0u ? 0.0f : f_of(0x3f800000u) / scale;
-#pragma unroll
-    for (int e = 0; e < 32; ++e) {
-      const float v = f_of(x[e]) * inverse;
-      const float half = (b_of(v) >> 31) == 0u ? f_of(0x3f000000u) : f_of(0xbf000000u);
-      const uint32_t q = (uint32_t)trunc_i32_x86(v + half) & 0xffu;
-      packed[2 * ((e & 15) >> 2) + (e >> 4)] |= q << (8 * (e & 3));
-    }
-  }
-  v4u* dst = reinterpret_cast<v4u*>(p.act_q + ((size_t)b * p.rows_pad + row) * 32);
-  dst[0] = v4u{packed[0], packed[1], packed[2], packed[3]};
-  dst[1] = v4u{packed[4], packed[5], packed[6], packed[7]};
-  p.act_s[(size_t)b * p.rows_pad + row] = act_scale * 0.0625f;
-}
-
 // ---- the head: int8 MFMA per block + the reference's binary32 epilogue ----
 // Fragment layout of v_mfma_i32_16x16x32_i8 (A and B alike, so only the
 // contraction index has to agree between them): lane l holds row (A) /
@@ -243,7 +238,7 @@ __global__ __launch_bounds__(kBlockThreads) void lm_q8_kernel(LmParams p) {
 // exactly M + 16 dot (|16 dot| < 2^19).  fma(M + 16 dot, ws, -M ws) is then
 // 16 dot ws rounded once (M ws is exact: ws has at most 11 significant bits),
 // which is 16 times the reference's mul(f32(dot), ws); its product with
-// a_scale / 16 (from lm_q8_kernel) is the reference's
+// a_scale / 16 (from lm_prep_kernel) is the reference's
 // mul(mul(f32(dot), ws), a_scale) bit for bit.  Scaling by powers of two is
 // exact here: |16 dot ws| is 0 or lies in [2^-20, 2^36), far from the
 // subnormal and overflow ranges.  A tile with an infinite or NaN fp16 weight
@@ -386,9 +381,9 @@ __global__ __launch_bounds__(kGemmThreads) void lm_gemm_kernel(LmParams p) {
     gemm(std::false_type{});
   }
 
-  // Logits, non-finite probe, history penalty and, per row, the tile's
-  // largest penalised key.  Lanes 16q .. 16q+15 hold the 64 ids of rows
-  // 4q + i of each row tile, four consecutive ids per lane.
+  // Logits, non-finite probe, history penalty and, per row, the order word of
+  // the tile's largest penalised value.  Lanes 16q .. 16q+15 hold the 64 ids
+  // of rows 4q + i of each row tile, four consecutive ids per lane.
   float probe = 0.0f;
 #pragma unroll
   for (int rt = 0; rt < 2; ++rt) {
@@ -409,21 +404,8 @@ __global__ __launch_bounds__(kGemmThreads) void lm_gemm_kernel(LmParams p) {
         for (int c = 0; c < 4; ++c)
           if ((hb >> c) & 1u) y[c] = f_of(penalize_bits(b_of(y[c])));
       }
-      // The row's best element of the tile: the largest value (-0 == +0),
-      // then the lowest id holding it, with that element's sign of zero.
       const float m = row16_max(fmaxf(fmaxf(y[0], y[1]), fmaxf(y[2], y[3])));
-      uint32_t pick = 0xffffffffu;
-#pragma unroll
-      for (int c = 3; c >= 0; --c) {
-        if (y[c] == m)
-          pick = ((4u * n + (uint32_t)c) << 1) | (b_of(y[c]) == 0x80000000u ? 1u : 0u);
-      }
-      pick = row16_min(pick);
-      if (live && n == 0u) {
-        const uint32_t id = v0 + (pick >> 1);
-        const uint32_t low = ((0x3ffffu - id) << 1) | (pick & 1u);  // make_key's low word
-        p.tilemax[(size_t)row * kTilesPerRow + tile] = ((uint64_t)ord_of(b_of(m)) << 32) | low;
-      }
+      if (live && n == 0u) p.tilemax[(size_t)row * kTilesPerRow + tile] = ord_of(b_of(m));
     }
   }
   if (__ballot(probe != probe)) {
@@ -479,15 +461,18 @@ __global__ __launch_bounds__(kBlockThreads) void lm_select_kernel(LmParams p, Ro
   uint64_t* my_cand = cand[wave];
   uint64_t* my_top = top[wave];
 
-  // 1. the 20 tiles with the largest maxima
+  // 1. the 20 tiles with the largest maxima.  A tile's key is its order word
+  // with 0xffff - tile below it: tiles hold consecutive ids, so among tiles
+  // with equal maxima the lower tile holds the lower id, and these keys order
+  // the tiles exactly as the 64-bit keys of their best elements would.
   constexpr int kPerLane = (kTilesPerRow + 63) / 64;  // 38
-  const uint64_t* tm = p.tilemax + (size_t)row * kTilesPerRow;
+  const uint32_t* tm = p.tilemax + (size_t)row * kTilesPerRow;
   uint64_t keys[kPerLane];
   uint64_t lane_best = 0;
 #pragma unroll
   for (int j = 0; j < kPerLane; ++j) {
     const uint32_t i = lane + 64u * j;
-    keys[j] = i < kTilesPerRow ? tm[i] : 0;
+    keys[j] = i < kTilesPerRow ? ((uint64_t)tm[i] << 32) | (0xffffu - i) : 0;
     lane_best = keys[j] > lane_best ? keys[j] : lane_best;
   }
   uint64_t thr = shfl64(wave_sort_desc(lane_best, lane), kTopK - 1);
@@ -504,7 +489,7 @@ __global__ __launch_bounds__(kBlockThreads) void lm_select_kernel(LmParams p, Ro
   lane_best = 0;
 #pragma unroll
   for (int i = 0; i < kTopK; ++i) {
-    const uint32_t tile = key_id(shfl64(tile_key, (uint32_t)i)) / kTileIds;
+    const uint32_t tile = 0xffffu - (uint32_t)shfl64(tile_key, (uint32_t)i);
     const uint32_t v = tile * kTileIds + lane;
     const uint32_t xb = lrow[v];
     const uint32_t yb = ((brow[v >> 5] >> (v & 31u)) & 1u) ? penalize_bits(xb) : xb;
@@ -565,10 +550,7 @@ size_t gemm_lds_bytes(uint32_t cols) {
 }
 
 hipError_t launch_lm_sample(const LmParams& p, const RowParams& rp, hipStream_t stream) {
-  hipLaunchKernelGGL(lm_bitmap_kernel, dim3(p.rows), dim3(kBlockThreads), 0, stream, p);
-  const uint32_t q8_threads = p.rows_pad * (p.cols / 32u);
-  hipLaunchKernelGGL(lm_q8_kernel, dim3((q8_threads + kBlockThreads - 1) / kBlockThreads),
-                     dim3(kBlockThreads), 0, stream, p);
+  hipLaunchKernelGGL(lm_prep_kernel, dim3(p.rows_pad), dim3(kBlockThreads), 0, stream, p);
   hipLaunchKernelGGL(lm_gemm_kernel,
                      dim3(kTilesPerRow, (p.rows_pad + kRowsPerGroup - 1) / kRowsPerGroup),
                      dim3(kGemmThreads), gemm_lds_bytes(p.cols), stream, p);
