@@ -467,6 +467,10 @@ __global__ __launch_bounds__(kBlockThreads) void lm_select_kernel(LmParams p, Ro
   // the tiles exactly as the 64-bit keys of their best elements would.
   constexpr int kPerLane = (kTilesPerRow + 63) / 64;  // 38
   const uint32_t* tm = p.tilemax + (size_t)row * kTilesPerRow;
+  // The threshold is the 20th best lane maximum as a full key: keys are
+  // distinct, so exactly 20 lanes reach it and at most 20 x 38 keys are
+  // collected (kCandCap).  A threshold on the order word alone would let
+  // every lane through when values tie.
   uint64_t keys[kPerLane];
   uint64_t lane_best = 0;
 #pragma unroll
@@ -485,14 +489,22 @@ __global__ __launch_bounds__(kBlockThreads) void lm_select_kernel(LmParams p, Ro
   // 2. exact top-20 over those tiles' 1,280 logits
   const uint32_t* lrow = p.logits + (size_t)row * p.logits_ld;
   const uint32_t* brow = p.bitmap + (size_t)row * kWordsPerRow;
+  // Every load is issued before the first is used: with the penalty's branch
+  // between them the compiler would otherwise wait for each tile in turn.
+  uint32_t xb[kTopK], hw[kTopK];
+#pragma unroll
+  for (int i = 0; i < kTopK; ++i) {
+    const uint32_t v = (0xffffu - (uint32_t)shfl64(tile_key, (uint32_t)i)) * kTileIds + lane;
+    xb[i] = lrow[v];
+    hw[i] = brow[v >> 5];
+  }
+  __builtin_amdgcn_sched_barrier(0);
   uint64_t ek[kTopK];
   lane_best = 0;
 #pragma unroll
   for (int i = 0; i < kTopK; ++i) {
-    const uint32_t tile = 0xffffu - (uint32_t)shfl64(tile_key, (uint32_t)i);
-    const uint32_t v = tile * kTileIds + lane;
-    const uint32_t xb = lrow[v];
-    const uint32_t yb = ((brow[v >> 5] >> (v & 31u)) & 1u) ? penalize_bits(xb) : xb;
+    const uint32_t v = (0xffffu - (uint32_t)shfl64(tile_key, (uint32_t)i)) * kTileIds + lane;
+    const uint32_t yb = ((hw[i] >> (v & 31u)) & 1u) ? penalize_bits(xb[i]) : xb[i];
     ek[i] = make_key(yb, v);
     lane_best = ek[i] > lane_best ? ek[i] : lane_best;
   }
