@@ -355,13 +355,14 @@ __device__ __forceinline__ uint64_t merge_lists_by_threshold(const uint64_t* lis
   const uint64_t* mine = lists + lane * kTopK;
   const uint32_t c = own ? (uint32_t)(mine[m - 1u] >> 32) : 0u;
   const uint64_t t = (uint64_t)bcast32(wave_sort_desc_u32<32>(c, lane), r - 1u) << 32;
+  // The lane's list stays in registers for the gather below: a loop that
+  // re-reads each key from LDS before storing it waits once per key.
+  uint64_t kk[kTopK];
   uint32_t n = 0;
-  if (own) {
 #pragma unroll
-    for (int q = 0; q < kTopK; ++q) {
-      const uint64_t k = mine[q];
-      n += (k != 0 && k >= t) ? 1u : 0u;
-    }
+  for (int q = 0; q < kTopK; ++q) {
+    kk[q] = own ? mine[q] : 0;
+    n += (kk[q] != 0 && kk[q] >= t) ? 1u : 0u;
   }
   // exclusive prefix of n (< 32) over the lanes, one ballot per bit
   const uint64_t below = (1ull << lane) - 1ull;
@@ -373,7 +374,10 @@ __device__ __forceinline__ uint64_t merge_lists_by_threshold(const uint64_t* lis
     total += (uint32_t)__popcll((unsigned long long)bits) << b;
   }
   if (total > 64u) return merge_sorted_lists(lists, nlists, lane);
-  for (uint32_t q = 0; q < n; ++q) scratch[before + q] = mine[q];
+#pragma unroll
+  for (uint32_t q = 0; q < (uint32_t)kTopK; ++q) {
+    if (q < n) scratch[before + q] = kk[q];
+  }
   __builtin_amdgcn_wave_barrier();
   uint64_t key = lane < total ? scratch[lane] : 0;
   __builtin_amdgcn_wave_barrier();

@@ -62,21 +62,20 @@ constexpr uint32_t kTileBytes = kTileIds * 16;  // packed nibbles of one (block,
 constexpr uint32_t kMagicBits = 0x4b400000u;
 constexpr float kMagic = 12582912.0f;
 
-// Maximum over the 16 lanes of a DPP row (lanes 16r .. 16r+15), in
-// every lane of the row: quad_perm [1,0,3,2] and [2,3,0,1] combine a quad, row
-// rotations by 4 and 8 combine the four quads.
-__device__ __forceinline__ uint32_t row_dpp(uint32_t v, int ctrl) {
-  switch (ctrl) {
-    case 0: return (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0xB1, 0xF, 0xF, false);
-    case 1: return (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x4E, 0xF, 0xF, false);
-    case 2: return (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x124, 0xF, 0xF, false);
-    default: return (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x128, 0xF, 0xF, false);
-  }
+// Maximum over the 16 lanes of a DPP row (lanes 16r .. 16r+15), in every
+// lane of the row: quad_perm [1,0,3,2] and [2,3,0,1] combine a quad, row
+// rotations by 4 and 8 combine the four quads.  The moved value's `old` is 0,
+// the identity of an unsigned maximum, so each step folds into one
+// v_max_u32 with a DPP operand.
+template <int kCtrl>
+__device__ __forceinline__ uint32_t dpp_or_zero(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, kCtrl, 0xF, 0xF, true);
 }
-__device__ __forceinline__ float row16_max(float v) {
-#pragma unroll
-  for (int s = 0; s < 4; ++s) v = fmaxf(v, f_of(row_dpp(b_of(v), s)));
-  return v;
+__device__ __forceinline__ uint32_t row16_max_u32(uint32_t v) {
+  v = max(v, dpp_or_zero<0xB1>(v));
+  v = max(v, dpp_or_zero<0x4E>(v));
+  v = max(v, dpp_or_zero<0x124>(v));
+  return max(v, dpp_or_zero<0x128>(v));
 }
 
 // cvttss2si semantics (x86 truncation): NaN and out-of-range give INT_MIN.
@@ -385,6 +384,7 @@ __global__ __launch_bounds__(kGemmThreads) void lm_gemm_kernel(LmParams p) {
   // the tile's largest penalised value.  Lanes 16q .. 16q+15 hold the 64 ids
   // of rows 4q + i of each row tile, four consecutive ids per lane.
   float probe = 0.0f;
+  uint32_t* lbase = p.logits + (size_t)(group0 + lrow0 + 4u * q) * p.logits_ld + v0 + 4u * n;
 #pragma unroll
   for (int rt = 0; rt < 2; ++rt) {
 #pragma unroll
@@ -394,7 +394,7 @@ __global__ __launch_bounds__(kGemmThreads) void lm_gemm_kernel(LmParams p) {
       const bool live = row < p.rows;
       float y[4] = {total[rt][0][i], total[rt][1][i], total[rt][2][i], total[rt][3][i]};
       if (live)
-        *reinterpret_cast<v4f*>(p.logits + (size_t)row * p.logits_ld + v0 + 4u * n) =
+        *reinterpret_cast<v4f*>(lbase + (size_t)(16u * rt + (uint32_t)i) * p.logits_ld) =
             v4f{y[0], y[1], y[2], y[3]};
 #pragma unroll
       for (int c = 0; c < 4; ++c) probe = __builtin_fmaf(y[c], 0.0f, probe);
@@ -404,8 +404,12 @@ __global__ __launch_bounds__(kGemmThreads) void lm_gemm_kernel(LmParams p) {
         for (int c = 0; c < 4; ++c)
           if ((hb >> c) & 1u) y[c] = f_of(penalize_bits(b_of(y[c])));
       }
-      const float m = row16_max(fmaxf(fmaxf(y[0], y[1]), fmaxf(y[2], y[3])));
-      if (live && n == 0u) p.tilemax[(size_t)row * kTilesPerRow + tile] = ord_of(b_of(m));
+      // order word of the row's largest value in the tile (ord_of: adding +0
+      // turns -0 into +0, then negative values are inverted)
+      uint32_t o = b_of(fmaxf(fmaxf(y[0], y[1]), fmaxf(y[2], y[3])) + 0.0f);
+      o ^= (uint32_t)((int32_t)o >> 31) | 0x80000000u;
+      o = row16_max_u32(o);
+      if (live && n == 0u) p.tilemax[(size_t)row * kTilesPerRow + tile] = o;
     }
   }
   if (__ballot(probe != probe)) {
