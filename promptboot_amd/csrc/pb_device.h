@@ -162,20 +162,23 @@ __device__ __forceinline__ uint32_t lanes_below(uint64_t mask) {
 // halves of lane ^ 4), and gfx950's v_permlane16_swap / v_permlane32_swap
 // for 16 and 32.  Every lane of the wave must be active.  `j` must fold to a
 // constant at each call site (unrolled loops).
+// Every source lane of these patterns is valid, so the DPP `old` operand is
+// never selected; passing 0 with bound_ctrl lets the compiler emit a single
+// v_mov_b32_dpp (or fold it into the consumer) instead of a copy and a move.
 __device__ __forceinline__ uint32_t lane_xor(uint32_t v, uint32_t j, uint32_t lane) {
   const int iv = (int)v;
   switch (j) {
     case 1:
-      return (uint32_t)__builtin_amdgcn_update_dpp(iv, iv, 0xB1, 0xF, 0xF, false);  // [1,0,3,2]
+      return (uint32_t)__builtin_amdgcn_update_dpp(0, iv, 0xB1, 0xF, 0xF, true);  // [1,0,3,2]
     case 2:
-      return (uint32_t)__builtin_amdgcn_update_dpp(iv, iv, 0x4E, 0xF, 0xF, false);  // [2,3,0,1]
+      return (uint32_t)__builtin_amdgcn_update_dpp(0, iv, 0x4E, 0xF, 0xF, true);  // [2,3,0,1]
     case 4: {
-      const uint32_t from_above = (uint32_t)__builtin_amdgcn_update_dpp(iv, iv, 0x12C, 0xF, 0xF, false);
-      const uint32_t from_below = (uint32_t)__builtin_amdgcn_update_dpp(iv, iv, 0x124, 0xF, 0xF, false);
+      const uint32_t from_above = (uint32_t)__builtin_amdgcn_update_dpp(0, iv, 0x12C, 0xF, 0xF, true);
+      const uint32_t from_below = (uint32_t)__builtin_amdgcn_update_dpp(0, iv, 0x124, 0xF, 0xF, true);
       return (lane & 4u) ? from_below : from_above;
     }
     case 8:
-      return (uint32_t)__builtin_amdgcn_update_dpp(iv, iv, 0x128, 0xF, 0xF, false);  // row_ror:8
+      return (uint32_t)__builtin_amdgcn_update_dpp(0, iv, 0x128, 0xF, 0xF, true);  // row_ror:8
     case 16: {
       const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
       return (lane & 16u) ? r[0] : r[1];
