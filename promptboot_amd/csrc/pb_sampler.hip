@@ -561,10 +561,16 @@ __global__ __launch_bounds__(kBlock) void writeback_kernel(WritebackParams p) {
 // ---- host-side launchers ----
 
 uint32_t segments_for_rows(uint32_t rows) {
-  // About 1024 workgroups for small batches (measured on MI355X: B=64 is
-  // fastest at 16 slices, B=1 at 32); one slice per row from B=1024 up.
+  // Measured on MI355X (HIP events per step, histories of up to 1024 ids):
+  //   B=1: 32 slices; B=64: 16 slices (22.4 us; 8: 23.3, 4: 25.3, 1: 30);
+  //   B=128: 4 slices (30.1 us; 8: 31.2, 2: 30.4);
+  //   B=256: 1 slice (36.2 us; 2: 38.8, 4: 42.0);
+  //   B=512: 1 slice (56.3 us; 2: 61.2).
+  // Slices stream a row over more CUs, but each slice rescans the history and
+  // a second launch merges them; from 256 rows the batch fills the GPU alone.
   if (rows == 0) return 1;
-  uint32_t s = 1024u / rows;
+  if (rows >= 256) return 1;
+  uint32_t s = rows <= 64 ? 1024u / rows : 512u / rows;
   if (s < 1) s = 1;
   if (s > kMaxSegments) s = kMaxSegments;
   return s;
