@@ -51,7 +51,7 @@ typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 
 constexpr uint32_t kBlockThreads = 256;
 constexpr uint32_t kTileIds = 64;        // vocabulary ids per tile and per workgroup
-constexpr uint32_t kRowsPerWave = 32;   // one 32-row MFMA tile per wave in the head
+constexpr uint32_t kRowsPerWave = 32;   // two 16-row MFMA row tiles per wave in the head
 constexpr uint32_t kGemmThreads = 512;  // eight waves
 constexpr uint32_t kRowsPerGroup = 256;
 constexpr uint32_t kWordsPerRow = kVocab / 32;
