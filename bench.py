@@ -242,7 +242,8 @@ def time_lmhead(smp, steps: int, warmup: int) -> dict:
               if (~boundary).any() else None,
               "boundary_rows": int(boundary.sum())}
     ops = 2.0 * B * workloads.VOCAB * workloads.HIDDEN
-    epilogue = 4.0 * B * workloads.VOCAB * (workloads.HIDDEN // 32)
+    # three IEEE roundings per (row, id, block): f32(dot) * w_scale, * a_scale, + total
+    epilogue = 3.0 * B * workloads.VOCAB * (workloads.HIDDEN // 32)
     alg = workloads.lmhead_algorithmic_bytes(B, w["hist_len"])
     return {"rows": B, "ms_per_step": round(wall / steps * 1e3, 4),
             "launch_ms": round(step_ms, 4),
