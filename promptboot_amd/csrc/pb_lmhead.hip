@@ -457,9 +457,10 @@ __global__ __launch_bounds__(kBlockThreads) void lm_select_kernel(LmParams p, Ro
   }
   const uint32_t bad_logit = p.meta[row * 2 + 0];
   const uint32_t bad_hist = p.meta[row * 2 + 1];
+  const uint32_t r24 = rp.random_24[row];  // requested before the selection
   if (bad_logit != kNone || bad_hist != kNone) {
     // error row: the GEMM lowered meta[0] to the first non-finite logit
-    finalize_row(rp, row, 0, bad_logit, bad_hist, lane);
+    finalize_row(rp, row, 0, bad_logit, bad_hist, lane, r24);
     return;
   }
   uint64_t* my_cand = cand[wave];
@@ -519,7 +520,7 @@ __global__ __launch_bounds__(kBlockThreads) void lm_select_kernel(LmParams p, Ro
   __builtin_amdgcn_wave_barrier();
   merge_all(my_top, my_cand, count, lane);
   const uint64_t key = lane < (uint32_t)kTopK ? my_top[lane] : 0;
-  finalize_row(rp, row, key, kNone, kNone, lane);
+  finalize_row(rp, row, key, kNone, kNone, lane, r24);
 }
 
 // MFMA layout self-test (one wave): A[i][k] = (7i + 3k) % 17 - 8 and

@@ -65,8 +65,9 @@ __device__ __forceinline__ void decode_commit(const RowParams& p, uint32_t row, 
 // rank order.  Softmax weights, top-p cutoff and the categorical draw follow
 // fp32_sse2.rs:1818-1845 operation for operation; the binary64 sums run as a
 // lane-serial chain in rank order, so every partial sum is the reference's.
+// `r24` is the row's uniform (random_24[row]), which callers request early.
 __device__ __forceinline__ void finalize_row(const RowParams& p, uint32_t row, uint64_t key, uint32_t bad_logit,
-                             uint32_t bad_hist, uint32_t lane) {
+                             uint32_t bad_hist, uint32_t lane, uint32_t r24) {
   if (bad_logit != kNone || bad_hist != kNone) {
     pb_inference_error e;
     e.layer = PB_NO_LAYER;
@@ -117,7 +118,6 @@ __device__ __forceinline__ void finalize_row(const RowParams& p, uint32_t row, u
   const uint64_t stop = __ballot(lane < (uint32_t)kTopK && !(cutoff > (float)mine));
   const uint32_t kept = stop ? (uint32_t)__ffsll((unsigned long long)stop) : (uint32_t)kTopK;
   const double kept_total = bcast_f64(mine, kept - 1);
-  const uint32_t r24 = p.random_24[row];
   const float unit = (float)(r24 & 0x00ffffffu) / f_of(kTwoPow24Bits);
   const float target = (float)kept_total * unit;
   const uint64_t hit = __ballot(lane < kept && (float)mine > target);

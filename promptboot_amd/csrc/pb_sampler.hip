@@ -150,6 +150,9 @@ __global__ __launch_bounds__(kBlock) void segment_kernel(RowParams p) {
                               : reinterpret_cast<const v4u*>(rowp);
   const uint32_t h4_last = p.hist_vec4 ? (uint32_t)(p.hist_ld / 4u) - 1u : kBlock - 1u;
   const v4u h_first = __builtin_nontemporal_load(h4 + min(tid, h4_last));
+  // The row's uniform, for the finish (S == 1); requested now so that its
+  // latency never lands on the row's last step.
+  const uint32_t r24 = kFinalize ? p.random_24[row] : 0u;
   v4f cur[F];
   load_chunk<F>(cur, rowp, f_lo, f_hi, tid);
   uint32_t hist_len = 0;
@@ -462,7 +465,7 @@ __global__ __launch_bounds__(kBlock) void segment_kernel(RowParams p) {
   if (kFinalize) {
     if (wave == 0) {
       const uint64_t key = merge_two_lists(top[0], top[1], lane);
-      finalize_row(p, row, lane < (uint32_t)kTopK ? key : 0, bad_logit, bad_hist, lane);
+      finalize_row(p, row, lane < (uint32_t)kTopK ? key : 0, bad_logit, bad_hist, lane, r24);
     }
     return;
   }
@@ -503,6 +506,7 @@ __global__ __launch_bounds__(kBlock) void finish_kernel(RowParams p) {
     const uint32_t i = u * 64u + lane;
     v[u] = i < nkeys ? keys[i] : 0;
   }
+  const uint32_t r24 = p.random_24[row];  // requested with the lists
   const uint32_t* meta = p.part_meta + (size_t)row * p.segs * 2;
   const uint32_t b = lane < p.segs ? meta[lane * 2] : kNone;
   const uint32_t hist_bad = meta[1];
@@ -514,7 +518,7 @@ __global__ __launch_bounds__(kBlock) void finish_kernel(RowParams p) {
   __builtin_amdgcn_wave_barrier();
   const uint64_t merged = merge_lists_by_threshold(st, p.segs, st + kMaxSegments * kTopK, lane);
   const uint32_t first_bad = wave_min_u32(b);
-  finalize_row(p, row, lane < (uint32_t)kTopK ? merged : 0, first_bad, hist_bad, lane);
+  finalize_row(p, row, lane < (uint32_t)kTopK ? merged : 0, first_bad, hist_bad, lane, r24);
 }
 
 // In-place penalty for successful rows (fp32_sse2.rs:1848-1876): the first
