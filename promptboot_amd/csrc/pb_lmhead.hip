@@ -150,11 +150,11 @@ __global__ __launch_bounds__(kBlockThreads) void lm_pack_kernel(const uint8_t* _
 // 8q .. 8q+7 hold elements 4q .. 4q+3 and 16+4q .. 16+4q+3 (q = 0..3).
 // act_s: [blocks][rows_pad] the fp32 scale the dot uses (half_to_f32 of the
 // stored fp16) times 2^-4, which is exact.  Pad rows are zero.
-__device__ __forceinline__ void quantize_block(const LmParams& p, uint32_t row, uint32_t b) {
+__device__ __forceinline__ void quantize_block(const LmParams& p, uint32_t row, uint32_t b,
+                                               const uint32_t (&x)[32]) {
   uint32_t packed[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
   float act_scale = 0.0f;
   if (row < p.rows) {
-    const uint32_t* x = p.hidden + (size_t)row * p.cols + b * 32u;
     uint32_t maximum = 0u;
 #pragma unroll
     for (int e = 0; e < 32; ++e) {
@@ -182,26 +182,41 @@ __device__ __forceinline__ void quantize_block(const LmParams& p, uint32_t row, 
 // ---- per row: Q8_0 activations, history bitmap, first bad history position ----
 // One workgroup per padded row: threads 0 .. blocks-1 quantise the row's
 // blocks (pad rows get zeros) while the workgroup builds the row's 151,936-bit
-// history bitmap in LDS and writes it out.
+// history bitmap in LDS and writes it out.  Every load is requested first --
+// the quantisers' inputs, the history length and the first 1,024 ids of the
+// padded history row (ids past the length are ignored) -- so the bitmap is
+// built while the quantisers' inputs arrive.
 __global__ __launch_bounds__(kBlockThreads) void lm_prep_kernel(LmParams p) {
+  constexpr uint32_t kEarlyIds = 4;  // history ids per thread requested up front
   __shared__ uint32_t bm[kWordsPerRow];
   __shared__ uint32_t bad;
   const uint32_t row = blockIdx.x;
   const uint32_t tid = threadIdx.x;
-  if (tid < p.cols / 32u) quantize_block(p, row, tid);
-  if (row >= p.rows) return;  // pad row: the whole workgroup leaves here
+  const bool live = row < p.rows;
+  const bool quantiser = tid < p.cols / 32u;
+  uint32_t x[32];
+#pragma unroll
+  for (int e = 0; e < 32; ++e)
+    x[e] = quantiser && live ? p.hidden[(size_t)row * p.cols + tid * 32u + (uint32_t)e] : 0u;
+  const bool has_hist = live && p.hist != nullptr && p.hist_len != nullptr;
+  const uint32_t* hrow = p.hist + (size_t)row * p.hist_ld;
+  uint32_t early[kEarlyIds];
+#pragma unroll
+  for (uint32_t u = 0; u < kEarlyIds; ++u) {
+    const uint32_t q = tid + u * kBlockThreads;
+    early[u] = has_hist && q < p.hist_ld ? hrow[q] : 0u;
+  }
+  uint32_t len = has_hist ? p.hist_len[row] : 0u;
+  if ((size_t)len > p.hist_ld) len = (uint32_t)p.hist_ld;
+  if (!live) {  // pad row: zero activations only (the whole workgroup leaves here)
+    if (quantiser) quantize_block(p, row, tid, x);
+    return;
+  }
   for (uint32_t i = tid; i < kWordsPerRow; i += kBlockThreads) bm[i] = 0u;
   if (tid == 0) bad = kNone;
   __syncthreads();
-  uint32_t len = 0;
-  if (p.hist != nullptr && p.hist_len != nullptr) {
-    len = p.hist_len[row];
-    if ((size_t)len > p.hist_ld) len = (uint32_t)p.hist_ld;
-  }
-  const uint32_t* hrow = p.hist + (size_t)row * p.hist_ld;
   uint32_t my_bad = kNone;
-  for (uint32_t q = tid; q < len; q += kBlockThreads) {
-    const uint32_t id = hrow[q];
+  auto add = [&](uint32_t q, uint32_t id) {
     if (id >= kVocab) {
       my_bad = q < my_bad ? q : my_bad;
     } else {
@@ -210,7 +225,14 @@ __global__ __launch_bounds__(kBlockThreads) void lm_prep_kernel(LmParams p) {
       if ((__hip_atomic_load(word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) & bit) == 0u)
         atomicOr(word, bit);
     }
+  };
+#pragma unroll
+  for (uint32_t u = 0; u < kEarlyIds; ++u) {
+    const uint32_t q = tid + u * kBlockThreads;
+    if (q < len) add(q, early[u]);
   }
+  for (uint32_t q = tid + kEarlyIds * kBlockThreads; q < len; q += kBlockThreads) add(q, hrow[q]);
+  if (quantiser) quantize_block(p, row, tid, x);
   if (my_bad != kNone) atomicMin(&bad, my_bad);
   __syncthreads();
   uint32_t* out = p.bitmap + (size_t)row * kWordsPerRow;
