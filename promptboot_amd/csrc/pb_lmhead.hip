@@ -528,21 +528,36 @@ __global__ __launch_bounds__(kBlockThreads) void lm_select_kernel(LmParams p, Ro
   __builtin_amdgcn_sched_barrier(0);
   uint64_t ek[kTopK];
   lane_best = 0;
+  // The 20 tiles' maxima are 20 distinct elements whose penalised values
+  // reach the 20th best tile's order word, so the row's 20th best key is at
+  // least (that word << 32): usually only a few more than 20 elements do.
+  const uint64_t tile_floor = shfl64(tile_key, kTopK - 1) & 0xffffffff00000000ull;
+  uint32_t at_floor = 0;
 #pragma unroll
   for (int i = 0; i < kTopK; ++i) {
     const uint32_t v = (0xffffu - (uint32_t)shfl64(tile_key, (uint32_t)i)) * kTileIds + lane;
     const uint32_t yb = ((hw[i] >> (v & 31u)) & 1u) ? penalize_bits(xb[i]) : xb[i];
     ek[i] = make_key(yb, v);
     lane_best = ek[i] > lane_best ? ek[i] : lane_best;
+    at_floor += (uint32_t)__popcll((unsigned long long)__ballot(ek[i] >= tile_floor));
   }
-  thr = shfl64(wave_sort_desc(lane_best, lane), kTopK - 1);
-  __builtin_amdgcn_wave_barrier();
-  count = collect_at_least(my_cand, ek, thr, 0);
-  if (lane < (uint32_t)kTopK) my_top[lane] = 0;
-  __builtin_amdgcn_wave_barrier();
-  merge_all(my_top, my_cand, count, lane);
-  const uint64_t key = lane < (uint32_t)kTopK ? my_top[lane] : 0;
-  finalize_row(rp, row, key, kNone, kNone, lane, r24);
+  uint64_t key;
+  if (at_floor <= 64u) {
+    // one sort of the elements at or above the floor
+    count = collect_at_least(my_cand, ek, tile_floor, 0);
+    __builtin_amdgcn_wave_barrier();
+    key = wave_sort_desc(lane < count ? my_cand[lane] : 0, lane);
+  } else {
+    // many ties at the floor: threshold from the lanes' best keys, then merge
+    thr = shfl64(wave_sort_desc(lane_best, lane), kTopK - 1);
+    __builtin_amdgcn_wave_barrier();
+    count = collect_at_least(my_cand, ek, thr, 0);
+    if (lane < (uint32_t)kTopK) my_top[lane] = 0;
+    __builtin_amdgcn_wave_barrier();
+    merge_all(my_top, my_cand, count, lane);
+    key = my_top[lane < (uint32_t)kTopK ? lane : 0];
+  }
+  finalize_row(rp, row, lane < (uint32_t)kTopK ? key : 0, kNone, kNone, lane, r24);
 }
 
 // MFMA layout self-test (one wave): A[i][k] = (7i + 3k) % 17 - 8 and
