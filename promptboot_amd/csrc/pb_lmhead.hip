@@ -404,34 +404,74 @@ __global__ __launch_bounds__(kGemmThreads) void lm_gemm_kernel(LmParams p) {
 
   // Logits, non-finite probe, history penalty and, per row, the order word of
   // the tile's largest penalised value.  Lanes 16q .. 16q+15 hold the 64 ids
-  // of rows 4q + i of each row tile, four consecutive ids per lane.
+  // of rows 4q + i of each row tile, four consecutive ids per lane.  Step
+  // s = 4 rt + i covers rows lrow0 + 16 rt + 4q + i.  The steps run in passes
+  // (stores and raw maxima, then the penalty, then the row maxima) so that the
+  // eight DPP chains interleave; the penalty sits behind one wave-uniform
+  // branch, since a wave's 32 rows rarely hold a history id in a 64-id tile.
+  // Bitmap words of rows past p.rows are zero.
+  uint32_t hb_all = 0;  // four history bits per step
+#pragma unroll
+  for (int s = 0; s < 8; ++s) {
+    const uint32_t lr = lrow0 + 16u * (uint32_t)(s >> 2) + 4u * q + (uint32_t)(s & 3);
+    hb_all |= ((hist_words[lr][n >> 3] >> (4u * (n & 7u))) & 0xfu) << (4 * s);
+  }
   float probe = 0.0f;
-  uint32_t* lbase = p.logits + (size_t)(group0 + lrow0 + 4u * q) * p.logits_ld + v0 + 4u * n;
+  float m[8];
+  const size_t ld = p.logits_ld;
+  uint32_t* lbase = p.logits + (size_t)(group0 + lrow0 + 4u * q) * ld + v0 + 4u * n;
+  const uint32_t first_row = group0 + lrow0 + 4u * q;  // row of step 0 in this lane
 #pragma unroll
-  for (int rt = 0; rt < 2; ++rt) {
+  for (int s = 0; s < 8; ++s) {
+    const int rt = s >> 2, i = s & 3;
+    const float y[4] = {total[rt][0][i], total[rt][1][i], total[rt][2][i], total[rt][3][i]};
+    if (first_row + 16u * (uint32_t)rt + (uint32_t)i < p.rows)
+      *reinterpret_cast<v4f*>(lbase + (size_t)(16 * rt + i) * ld) = v4f{y[0], y[1], y[2], y[3]};
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t lr = lrow0 + 16u * rt + 4u * q + (uint32_t)i;
-      const uint32_t row = group0 + lr;
-      const bool live = row < p.rows;
-      float y[4] = {total[rt][0][i], total[rt][1][i], total[rt][2][i], total[rt][3][i]};
-      if (live)
-        *reinterpret_cast<v4f*>(lbase + (size_t)(16u * rt + (uint32_t)i) * p.logits_ld) =
-            v4f{y[0], y[1], y[2], y[3]};
+    for (int c = 0; c < 4; ++c) probe = __builtin_fmaf(y[c], 0.0f, probe);
+    m[s] = fmaxf(fmaxf(y[0], y[1]), fmaxf(y[2], y[3]));
+  }
+  // The penalty is monotone (x <= y gives pen(x) <= pen(y)), so the largest
+  // penalised history value is the penalty of the largest history value: one
+  // penalty per lane and step.  NaN is the identity of fmaxf, so a side with
+  // no element stays NaN and drops out, and pen(NaN) is NaN.  (A lane whose
+  // four values are all NaN may give another NaN than the per-element form;
+  // such a row is an error row, whose tile maxima are not used.)
+  if (__ballot(hb_all != 0u)) {
+    const float kNaN = __builtin_nanf("");
 #pragma unroll
-      for (int c = 0; c < 4; ++c) probe = __builtin_fmaf(y[c], 0.0f, probe);
-      const uint32_t hb = live ? (hist_words[lr][n >> 3] >> (4u * (n & 7u))) & 0xfu : 0u;
+    for (int s = 0; s < 8; ++s) {
+      const int rt = s >> 2, i = s & 3;
+      const uint32_t hb = (hb_all >> (4 * s)) & 0xfu;
       if (hb != 0u) {
+        float h[4], u[4];
 #pragma unroll
-        for (int c = 0; c < 4; ++c)
-          if ((hb >> c) & 1u) y[c] = f_of(penalize_bits(b_of(y[c])));
+        for (int c = 0; c < 4; ++c) {
+          const bool hit = ((hb >> c) & 1u) != 0u;
+          h[c] = hit ? total[rt][c][i] : kNaN;
+          u[c] = hit ? kNaN : total[rt][c][i];
+        }
+        const float mh = fmaxf(fmaxf(h[0], h[1]), fmaxf(h[2], h[3]));
+        const float mu = fmaxf(fmaxf(u[0], u[1]), fmaxf(u[2], u[3]));
+        m[s] = fmaxf(mu, f_of(penalize_bits(b_of(mh))));
       }
-      // order word of the row's largest value in the tile (ord_of: adding +0
-      // turns -0 into +0, then negative values are inverted)
-      uint32_t o = b_of(fmaxf(fmaxf(y[0], y[1]), fmaxf(y[2], y[3])) + 0.0f);
-      o ^= (uint32_t)((int32_t)o >> 31) | 0x80000000u;
-      o = row16_max_u32(o);
-      if (live && n == 0u) p.tilemax[(size_t)row * kTilesPerRow + tile] = o;
+    }
+  }
+  // order word of each row's largest value in the tile (ord_of: adding +0
+  // turns -0 into +0, then negative values are inverted)
+  uint32_t o[8];
+#pragma unroll
+  for (int s = 0; s < 8; ++s) {
+    o[s] = b_of(m[s] + 0.0f);
+    o[s] ^= (uint32_t)((int32_t)o[s] >> 31) | 0x80000000u;
+  }
+#pragma unroll
+  for (int s = 0; s < 8; ++s) o[s] = row16_max_u32(o[s]);
+  if (n == 0u) {
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      const uint32_t row = first_row + 16u * (uint32_t)(s >> 2) + (uint32_t)(s & 3);
+      if (row < p.rows) p.tilemax[(size_t)row * kTilesPerRow + tile] = o[s];
     }
   }
   if (__ballot(probe != probe)) {

@@ -174,6 +174,79 @@ def test_special_weight_and_activation_scales(smp, head):
     assert rnan[0].any() and np.isinf(rlog.view(np.float32)[0]).any()
 
 
+def _top_histories(rlog, rows):
+    """Histories made of each row's best ids, so that the penalty lowers the
+    largest value of the tiles that decide the row's top-20: the top 20, the
+    top 64, every id of the tiles holding the top 5, every other id of the
+    top 40, and the top 3 repeated (the penalty applies once per unique id)."""
+    hists = []
+    for r in range(rows):
+        top = np.argsort(-rlog[r].view(np.float32), kind="stable")[:64].astype(np.uint32)
+        kind = r % 5
+        if kind == 0:
+            ids = top[:20]
+        elif kind == 1:
+            ids = top
+        elif kind == 2:
+            tiles = np.unique(top[:5] // 64)
+            ids = (tiles[:, None] * 64 + np.arange(64, dtype=np.uint32)).reshape(-1)
+        elif kind == 3:
+            ids = top[:40:2]
+        else:
+            ids = np.repeat(top[:3], 7)
+        hists.append(ids.astype(np.uint32))
+    ld = max(len(h) for h in hists)
+    hist = np.zeros((rows, ld), np.uint32)
+    hl = np.zeros(rows, np.uint32)
+    for r, h in enumerate(hists):
+        hist[r, :len(h)] = h
+        hl[r] = len(h)
+    return hist, hl
+
+
+def test_history_holds_the_best_ids(smp, head):
+    """Every tile maximum that decides a row's top-20 is a penalised value."""
+    w, packed = head
+    rows = 40
+    hidden = w["hidden"][:rows]
+    rlog = o.lmhead_logits(hidden, w["q4"], V, workloads.HIDDEN, threads=16)
+    hist, hl = _top_histories(rlog, rows)
+    r24 = w["random_24"][:rows]
+    glog, gtok, gdet, gerr = run_head(smp, packed, hidden, hist, hl, r24)
+    assert (glog == rlog).all()
+    rtok, rdet, rerr, _ = o.sample_batch(rlog, hist, hl, r24, threads=16)
+    assert (rerr["status"] == 0).all()
+    assert_rows_equal(gtok, gdet, gerr, rtok, rdet, rerr)
+
+
+def test_every_logit_negative(smp):
+    """A head whose logits are all negative: the tile maxima are negative, so
+    the penalty multiplies by 1.1 instead of dividing."""
+    import torch
+
+    rows, cols = 10, workloads.HIDDEN
+    rng = np.random.default_rng(23)
+    blocks = cols // 32
+    # nibbles 0..7 are quants -8..-1; with positive activations every dot is negative
+    lo = rng.integers(0, 8, (V, blocks, 16), dtype=np.uint8)
+    hi = rng.integers(0, 8, (V, blocks, 16), dtype=np.uint8)
+    q4 = np.zeros((V, blocks, 18), np.uint8)
+    q4[:, :, 2:] = lo | (hi << 4)
+    sc = rng.uniform(0.001, 0.02, (V, blocks)).astype(np.float16).view(np.uint16)
+    q4[:, :, 0] = sc & 0xFF
+    q4[:, :, 1] = sc >> 8
+    packed = smp.pack_lmhead(torch.from_numpy(q4.reshape(-1)).to("cuda:0"))
+    hidden = rng.uniform(0.5, 2.0, (rows, cols)).astype(np.float32)
+    rlog = o.lmhead_logits(hidden, q4.reshape(-1), V, cols, threads=16)
+    assert (rlog.view(np.float32) < 0).all()
+    hist, hl = _top_histories(rlog, rows)
+    r24 = (np.arange(rows, dtype=np.uint32) * 1_234_567) & 0xFFFFFF
+    glog, gtok, gdet, gerr = run_head(smp, packed, hidden, hist, hl, r24)
+    assert (glog == rlog).all()
+    rtok, rdet, rerr, _ = o.sample_batch(rlog, hist, hl, r24, threads=16)
+    assert_rows_equal(gtok, gdet, gerr, rtok, rdet, rerr)
+
+
 def test_widest_hidden_state(smp):
     """cols = 2048, the widest the head accepts (its per-block scales then take
     96 KB of the workgroup's LDS): logits bit-exact for three rows."""
