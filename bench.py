@@ -21,7 +21,10 @@ The printed JSON line also carries:
                      batch;
   adversarial_B1024  the flat / ties / dominant / half-vocabulary-history
                      sub-cases, each timed and checked against the oracle;
-  lmhead_fused       the fused Q4_0 LM head + sampler step (B=256).
+  lmhead_fused       the fused Q4_0 LM head + sampler step (B=256);
+  host_buffers       PCIe-inclusive rates: the single-row drop-in on host
+                     buffers, and the B=4096 batch copied from pinned host
+                     memory every step (not the headline value).
 
 Before the W warmup steps every batch size runs an untimed settle phase
 (the step repeated for 0.5 s) so the GPU is at its working clocks.
@@ -167,6 +170,70 @@ def time_batch(smp, w: dict, steps: int, warmup: int) -> dict:
             "_tokens": tokens, "_detail": detail}
 
 
+def time_host_buffers(smp, w1: dict, w: dict, calls: int = 200, steps: int = 5) -> dict:
+    """Rates with the inputs in host memory, so PCIe is included (never the
+    headline value, which is timed with the inputs resident in HBM):
+
+      dropin    pb_sample_token_with_repetition on host buffers, as the
+                reference's call sites pass them (one row, its history as the
+                token list): wall time per call;
+      batch     the B=4096 batch copied from pinned host memory every step
+                (logits, the padded history matrix, lengths, uniforms), then
+                pb_sample_batch, then the tokens copied back.
+    """
+    import torch
+
+    from promptboot_amd import sampler as s
+
+    row0 = np.ascontiguousarray(w1["logits"][0]).view(np.uint32)
+    prompt = np.ascontiguousarray(w1["hist"][0, :w1["hist_len"][0]])
+    seen = np.zeros(s.SEEN_BYTES, np.uint8)
+    state = s.SamplingState(int(w1["seeds"][0]))
+    times = []
+    for i in range(calls + 10):
+        row = row0.copy()
+        t0 = time.perf_counter()
+        s.sample_token_with_repetition(row, prompt, seen, state)
+        if i >= 10:
+            times.append(time.perf_counter() - t0)
+    times = np.array(times) * 1e6
+
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream(dev)
+    B = w["logits"].shape[0]
+    host = [torch.from_numpy(np.ascontiguousarray(w[k]).view(np.int32)).pin_memory()
+            for k in ("logits", "hist", "hist_len", "random_24")]
+    devs = [torch.empty_like(h, device=dev) for h in host]
+    token = torch.empty(B, dtype=torch.int32, device=dev)
+    h_token = torch.empty(B, dtype=torch.int32).pin_memory()
+    h2d = sum(h.numel() * 4 for h in host)
+
+    def step():
+        for d, h in zip(devs, host):
+            d.copy_(h, non_blocking=True)
+        smp.sample(devs[0], devs[3], devs[1], devs[2], token=token, stream=stream)
+        h_token.copy_(token, non_blocking=True)
+
+    step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    sec = (time.perf_counter() - t0) / steps
+    del host, devs
+    return {"dropin_us_per_call": {"median": round(float(np.median(times)), 1),
+                                   "p10": round(float(np.percentile(times, 10)), 1),
+                                   "p90": round(float(np.percentile(times, 90)), 1),
+                                   "calls": calls,
+                                   "row": "B=1 workload row 0, history of "
+                                          f"{int(w1['hist_len'][0])} ids"},
+            "batch_pcie_inclusive": {"rows": B, "rows_per_s": round(B / sec, 1),
+                                     "ms_per_step": round(sec * 1e3, 3),
+                                     "h2d_bytes_per_step": h2d,
+                                     "h2d_gbs": round(h2d / sec / 1e9, 1), "steps": steps}}
+
+
 MFMA_INT8_PEAK_TOPS = 5000.0     # dense int8 MFMA, MI355X
 VALU_LANE_OPS_PEAK = 256 * 4 * 16 * 2.4e9  # 32-bit VALU lane-ops/s, MI355X
 
@@ -301,6 +368,9 @@ def main() -> int:
                     help="skip the adversarial B=1024 sub-cases")
     ap.add_argument("--no-lmhead", action="store_true",
                     help="skip the fused Q4_0 LM head + sampler timing")
+    ap.add_argument("--no-host-buffers", action="store_true",
+                    help="skip the PCIe-inclusive timings (drop-in on host buffers, "
+                         "B=4096 copied from pinned host memory)")
     ap.add_argument("--batches", default="1,64,4096")
     ap.add_argument("--segments", type=int, default=0,
                     help="force the slices per row (0 = the library's choice)")
@@ -359,6 +429,10 @@ def main() -> int:
     if not args.no_lmhead:
         log("timing the fused Q4_0 LM head + sampler (B=256)")
         lmhead = time_lmhead(smp, min(args.steps, 50), args.warmup)
+    host_buffers = None
+    if not args.no_host_buffers and 1 in work and 4096 in work:
+        log("timing with the inputs in host memory (PCIe included)")
+        host_buffers = time_host_buffers(smp, work[1], work[4096])
     smp.close()
 
     main_res = results[head]
@@ -417,6 +491,7 @@ def main() -> int:
         "by_batch": by_batch,
         "adversarial_B1024": adversarial,
         "lmhead_fused": lmhead,
+        "host_buffers": host_buffers,
         "roofline": roof,
         "cpu_baseline": cpu,
         "parity": parity,
