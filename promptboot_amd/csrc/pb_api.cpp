@@ -68,23 +68,43 @@ struct pb_context {
   void* d_lm = nullptr;  // fused LM head workspace
   size_t lm_bytes = 0;
 
-  // single-row staging
+  // Single-row staging: one input region, pinned on the host and mirrored on
+  // the device ([history length, uniform, -, -][row][history ids]), and one
+  // output region ([token, -, -, -][error record][detail][penalised history
+  // values]), so that a call makes one copy each way.  The pointers below
+  // point into them; `seen` has its own pair, copied only when non-zero.
+  size_t hist_cap = 0;
+  uint8_t* d_in = nullptr;
+  uint8_t* h_in = nullptr;
+  uint8_t* d_out = nullptr;
+  uint8_t* h_out = nullptr;
+  uint32_t* d_small = nullptr;  // [0] history length, [1] uniform
   uint32_t* d_row = nullptr;
   uint32_t* d_hist = nullptr;
-  uint32_t* d_gather = nullptr;
-  size_t hist_cap = 0;
-  uint32_t* d_small = nullptr;  // [0] history length, [1] uniform, [2] token
-  pb_sample_detail* d_detail = nullptr;
+  uint32_t* d_token = nullptr;
   pb_inference_error* d_err = nullptr;
-  uint8_t* d_seen = nullptr;
-  uint32_t* h_row = nullptr;    // pinned
-  uint32_t* h_hist = nullptr;   // pinned
-  uint32_t* h_gather = nullptr; // pinned
-  uint32_t* h_small = nullptr;  // pinned
-  pb_sample_detail* h_detail = nullptr;
+  pb_sample_detail* d_detail = nullptr;
+  uint32_t* d_gather = nullptr;
+  uint32_t* h_small = nullptr;
+  uint32_t* h_row = nullptr;
+  uint32_t* h_hist = nullptr;
+  uint32_t* h_token = nullptr;
   pb_inference_error* h_err = nullptr;
+  pb_sample_detail* h_detail = nullptr;
+  uint32_t* h_gather = nullptr;
+  uint8_t* d_seen = nullptr;
   uint8_t* h_seen = nullptr;
 };
+
+// Offsets inside the staging regions.  The row starts 16 bytes in, so it
+// keeps the 16-byte alignment of the float4 loads, and so does the history.
+constexpr size_t kInRow = 16;
+constexpr size_t kInHist = kInRow + kRowBytes;
+constexpr size_t kOutErr = 16;
+constexpr size_t kOutDetail = 64;
+constexpr size_t kOutGather = (kOutDetail + sizeof(pb_sample_detail) + 15) / 16 * 16;
+static_assert(kOutErr + sizeof(pb_inference_error) <= kOutDetail, "error record overlaps");
+static_assert(kInHist % 16 == 0, "history ids must stay 16-byte aligned");
 
 // Workspace of the multi-slice path: the slice keys and slice records,
 // grown as needed (hipFree synchronises the device, so no launch still
@@ -103,22 +123,47 @@ static hipError_t ensure_workspace(pb_context* ctx, size_t list_bytes) {
   return hipSuccess;
 }
 
-static hipError_t ensure_hist_capacity(pb_context* ctx, size_t ids) {
-  if (ids <= ctx->hist_cap) return hipSuccess;
+static void free_staging(pb_context* ctx) {
+  if (ctx->d_in) (void)hipFree(ctx->d_in);
+  if (ctx->d_out) (void)hipFree(ctx->d_out);
+  if (ctx->h_in) (void)hipHostFree(ctx->h_in);
+  if (ctx->h_out) (void)hipHostFree(ctx->h_out);
+  ctx->d_in = ctx->d_out = ctx->h_in = ctx->h_out = nullptr;
+  ctx->hist_cap = 0;
+}
+
+// Staging regions for histories of up to `ids` ids.  The drop-ins hold the
+// context's lock and synchronise before they return, so no copy or launch
+// still uses the old regions when they are freed.
+static hipError_t ensure_staging(pb_context* ctx, size_t ids) {
+  if (ctx->d_in && ids <= ctx->hist_cap) return hipSuccess;
   size_t cap = ctx->hist_cap ? ctx->hist_cap : 1024;
   while (cap < ids) cap *= 2;
-  if (ctx->d_hist) (void)hipFree(ctx->d_hist);
-  if (ctx->d_gather) (void)hipFree(ctx->d_gather);
-  if (ctx->h_hist) (void)hipHostFree(ctx->h_hist);
-  if (ctx->h_gather) (void)hipHostFree(ctx->h_gather);
-  ctx->d_hist = ctx->d_gather = ctx->h_hist = ctx->h_gather = nullptr;
-  ctx->hist_cap = 0;
+  free_staging(ctx);
+  const size_t in_bytes = kInHist + cap * 4, out_bytes = kOutGather + cap * 4;
   hipError_t e;
-  if ((e = hipMalloc(&ctx->d_hist, cap * 4)) != hipSuccess) return e;
-  if ((e = hipMalloc(&ctx->d_gather, cap * 4)) != hipSuccess) return e;
-  if ((e = hipHostMalloc(&ctx->h_hist, cap * 4, hipHostMallocDefault)) != hipSuccess) return e;
-  if ((e = hipHostMalloc(&ctx->h_gather, cap * 4, hipHostMallocDefault)) != hipSuccess) return e;
+  if ((e = hipMalloc(&ctx->d_in, in_bytes)) != hipSuccess ||
+      (e = hipMalloc(&ctx->d_out, out_bytes)) != hipSuccess ||
+      (e = hipHostMalloc(&ctx->h_in, in_bytes, hipHostMallocDefault)) != hipSuccess ||
+      (e = hipHostMalloc(&ctx->h_out, out_bytes, hipHostMallocDefault)) != hipSuccess) {
+    free_staging(ctx);
+    return e;
+  }
   ctx->hist_cap = cap;
+  ctx->d_small = reinterpret_cast<uint32_t*>(ctx->d_in);
+  ctx->d_row = reinterpret_cast<uint32_t*>(ctx->d_in + kInRow);
+  ctx->d_hist = reinterpret_cast<uint32_t*>(ctx->d_in + kInHist);
+  ctx->d_token = reinterpret_cast<uint32_t*>(ctx->d_out);
+  ctx->d_err = reinterpret_cast<pb_inference_error*>(ctx->d_out + kOutErr);
+  ctx->d_detail = reinterpret_cast<pb_sample_detail*>(ctx->d_out + kOutDetail);
+  ctx->d_gather = reinterpret_cast<uint32_t*>(ctx->d_out + kOutGather);
+  ctx->h_small = reinterpret_cast<uint32_t*>(ctx->h_in);
+  ctx->h_row = reinterpret_cast<uint32_t*>(ctx->h_in + kInRow);
+  ctx->h_hist = reinterpret_cast<uint32_t*>(ctx->h_in + kInHist);
+  ctx->h_token = reinterpret_cast<uint32_t*>(ctx->h_out);
+  ctx->h_err = reinterpret_cast<pb_inference_error*>(ctx->h_out + kOutErr);
+  ctx->h_detail = reinterpret_cast<pb_sample_detail*>(ctx->h_out + kOutDetail);
+  ctx->h_gather = reinterpret_cast<uint32_t*>(ctx->h_out + kOutGather);
   return hipSuccess;
 }
 
@@ -126,14 +171,11 @@ static void release(pb_context* ctx) {
   if (!ctx) return;
   DeviceGuard guard(ctx->device);
   if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
-  void* dev[] = {ctx->d_work, ctx->d_lm,     ctx->d_row,    ctx->d_hist, ctx->d_gather,
-                 ctx->d_small, ctx->d_detail, ctx->d_err, ctx->d_seen};
+  free_staging(ctx);
+  void* dev[] = {ctx->d_work, ctx->d_lm, ctx->d_seen};
   for (void* p : dev)
     if (p) (void)hipFree(p);
-  void* host[] = {ctx->h_row, ctx->h_hist, ctx->h_gather, ctx->h_small, ctx->h_detail,
-                  ctx->h_err, ctx->h_seen};
-  for (void* p : host)
-    if (p) (void)hipHostFree(p);
+  if (ctx->h_seen) (void)hipHostFree(ctx->h_seen);
   if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
   delete ctx;
 }
@@ -199,19 +241,9 @@ uint32_t pb_context_create(int device, pb_context** out) {
   ctx->device = device;
   hipError_t e = hipSuccess;
   if (e == hipSuccess) e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
-  if (e == hipSuccess) e = hipMalloc(&ctx->d_row, kRowBytes);
-  if (e == hipSuccess) e = hipMalloc(&ctx->d_small, 16);
-  if (e == hipSuccess) e = hipMalloc(&ctx->d_detail, sizeof(pb_sample_detail));
-  if (e == hipSuccess) e = hipMalloc(&ctx->d_err, sizeof(pb_inference_error));
   if (e == hipSuccess) e = hipMalloc(&ctx->d_seen, PB_SEEN_BYTES);
-  if (e == hipSuccess) e = hipHostMalloc(&ctx->h_row, kRowBytes, hipHostMallocDefault);
-  if (e == hipSuccess) e = hipHostMalloc(&ctx->h_small, 16, hipHostMallocDefault);
-  if (e == hipSuccess)
-    e = hipHostMalloc(&ctx->h_detail, sizeof(pb_sample_detail), hipHostMallocDefault);
-  if (e == hipSuccess)
-    e = hipHostMalloc(&ctx->h_err, sizeof(pb_inference_error), hipHostMallocDefault);
   if (e == hipSuccess) e = hipHostMalloc(&ctx->h_seen, PB_SEEN_BYTES, hipHostMallocDefault);
-  if (e == hipSuccess) e = ensure_hist_capacity(ctx, 4096);
+  if (e == hipSuccess) e = ensure_staging(ctx, 4096);
   if (e != hipSuccess) {
     release(ctx);
     return PB_DEVICE;
@@ -561,47 +593,42 @@ static pb_context* default_context(pb_inference_error* err) {
 enum RowMode { kSample = 0, kSampleWithHistory = 1 };
 
 // Runs one row through the batched kernels on the context's own stream.
-// Fills ctx->h_small[2] (token), ctx->h_detail and ctx->h_err; when
-// `history` is non-null also the penalised write-back values in h_gather and,
-// with `seen_dirty`, the updated scratch in h_seen.
+// Fills *ctx->h_token, ctx->h_detail and ctx->h_err; when `history` is
+// non-null also the penalised write-back values in h_gather and, with
+// `seen_dirty`, the updated scratch in h_seen.  The scalars, the row and the
+// history go up in one copy and the results come back in one: each copy on
+// the stream costs several microseconds of latency, more than its bytes.
 static uint32_t run_single_row(pb_context* ctx, const uint32_t* logits, const uint32_t* history,
                                size_t history_len, const uint8_t* seen, bool seen_dirty,
                                uint32_t random_24, pb_inference_error* err) {
   DeviceGuard guard(ctx->device);
   hipStream_t s = ctx->stream;
   hipError_t e;
-  memcpy(ctx->h_row, logits, kRowBytes);
-  if ((e = hipMemcpyAsync(ctx->d_row, ctx->h_row, kRowBytes, hipMemcpyHostToDevice, s)) !=
-      hipSuccess)
+  const bool with_hist = history != nullptr && history_len > 0;
+  if (with_hist && (e = ensure_staging(ctx, history_len)) != hipSuccess)
     return device_error(err, e);
-  if (history) {
-    if ((e = ensure_hist_capacity(ctx, history_len ? history_len : 1)) != hipSuccess)
-      return device_error(err, e);
-    if (history_len) {
-      memcpy(ctx->h_hist, history, history_len * 4);
-      if ((e = hipMemcpyAsync(ctx->d_hist, ctx->h_hist, history_len * 4, hipMemcpyHostToDevice,
-                              s)) != hipSuccess)
-        return device_error(err, e);
-    }
-    if (seen_dirty) {
-      memcpy(ctx->h_seen, seen, PB_SEEN_BYTES);
-      if ((e = hipMemcpyAsync(ctx->d_seen, ctx->h_seen, PB_SEEN_BYTES, hipMemcpyHostToDevice,
-                              s)) != hipSuccess)
-        return device_error(err, e);
-    }
-  }
   ctx->h_small[0] = (uint32_t)history_len;
   ctx->h_small[1] = random_24;
-  if ((e = hipMemcpyAsync(ctx->d_small, ctx->h_small, 8, hipMemcpyHostToDevice, s)) != hipSuccess)
+  memcpy(ctx->h_row, logits, kRowBytes);
+  if (with_hist) memcpy(ctx->h_hist, history, history_len * 4);
+  const size_t in_bytes = kInHist + (with_hist ? history_len * 4 : 0);
+  if ((e = hipMemcpyAsync(ctx->d_in, ctx->h_in, in_bytes, hipMemcpyHostToDevice, s)) !=
+      hipSuccess)
     return device_error(err, e);
+  // Without history ids the scratch is returned as it came, so it stays on the host.
+  if (with_hist && seen_dirty) {
+    memcpy(ctx->h_seen, seen, PB_SEEN_BYTES);
+    if ((e = hipMemcpyAsync(ctx->d_seen, ctx->h_seen, PB_SEEN_BYTES, hipMemcpyHostToDevice, s)) !=
+        hipSuccess)
+      return device_error(err, e);
+  }
 
-  const bool with_hist = history != nullptr && history_len > 0;
-  uint8_t* seen_dev = seen_dirty ? ctx->d_seen : nullptr;
+  uint8_t* seen_dev = with_hist && seen_dirty ? ctx->d_seen : nullptr;
   pb_inference_error enqueue_err;
   uint32_t st = enqueue_sample(ctx, ctx->d_row, PB_VOCAB, PB_VOCAB, 1,
                                with_hist ? ctx->d_hist : nullptr, ctx->hist_cap,
                                with_hist ? ctx->d_small : nullptr, ctx->d_small + 1, seen_dev,
-                               ctx->d_small + 2, ctx->d_detail, ctx->d_err, s, &enqueue_err);
+                               ctx->d_token, ctx->d_detail, ctx->d_err, s, &enqueue_err);
   if (st != PB_OK) {
     if (err) *err = enqueue_err;
     return st;
@@ -615,23 +642,17 @@ static uint32_t run_single_row(pb_context* ctx, const uint32_t* logits, const ui
     w.hist_ld = ctx->hist_cap;
     w.hist_len = ctx->d_small;
     w.seen = seen_dev;
-    w.token = ctx->d_small + 2;
+    w.token = ctx->d_token;
     w.gather = ctx->d_gather;
     if ((e = pb::launch_writeback(w, s)) != hipSuccess) return device_error(err, e);
-    if ((e = hipMemcpyAsync(ctx->h_gather, ctx->d_gather, history_len * 4, hipMemcpyDeviceToHost,
-                            s)) != hipSuccess)
-      return device_error(err, e);
     if (seen_dirty &&
         (e = hipMemcpyAsync(ctx->h_seen, ctx->d_seen, PB_SEEN_BYTES, hipMemcpyDeviceToHost, s)) !=
             hipSuccess)
       return device_error(err, e);
   }
-  if ((e = hipMemcpyAsync(ctx->h_small + 2, ctx->d_small + 2, 4, hipMemcpyDeviceToHost, s)) !=
-          hipSuccess ||
-      (e = hipMemcpyAsync(ctx->h_detail, ctx->d_detail, sizeof(pb_sample_detail),
-                          hipMemcpyDeviceToHost, s)) != hipSuccess ||
-      (e = hipMemcpyAsync(ctx->h_err, ctx->d_err, sizeof(pb_inference_error),
-                          hipMemcpyDeviceToHost, s)) != hipSuccess)
+  const size_t out_bytes = kOutGather + (with_hist ? history_len * 4 : 0);
+  if ((e = hipMemcpyAsync(ctx->h_out, ctx->d_out, out_bytes, hipMemcpyDeviceToHost, s)) !=
+      hipSuccess)
     return device_error(err, e);
   if ((e = hipStreamSynchronize(s)) != hipSuccess) return device_error(err, e);
   return PB_OK;
@@ -681,9 +702,9 @@ uint32_t pb_sample_token_with_repetition(uint32_t* logits, size_t logits_len,
   }
   // success: publish the in-place penalty, the cleared scratch and the draw
   for (size_t q = 0; q < tokens_len; ++q) logits[tokens[q]] = ctx->h_gather[q];
-  if (seen_dirty) memcpy(seen, ctx->h_seen, PB_SEEN_BYTES);
+  if (seen_dirty && tokens != nullptr && tokens_len > 0) memcpy(seen, ctx->h_seen, PB_SEEN_BYTES);
   *state = next;
-  *out_token = ctx->h_small[2];
+  *out_token = *ctx->h_token;
   return PB_OK;
 }
 
@@ -706,7 +727,7 @@ uint32_t pb_sample_token(const uint32_t* logits, size_t logits_len, pb_sampling_
     return ctx->h_err->status;
   }
   *state = next;
-  *out_token = ctx->h_small[2];
+  *out_token = *ctx->h_token;
   return PB_OK;
 }
 

@@ -200,3 +200,26 @@ def test_preset_seen_bits_follow_the_reference_dedupe():
     t = s.sample_token_with_repetition(g, hist, gseen, gs)
     _, rt, _ = o.sample_token_with_repetition(r, hist, rseen, rs)
     assert t == rt and (g == r).all() and (gseen == rseen).all()
+
+
+def test_staging_grows_then_shorter_and_empty_histories():
+    """A 9,000-id history outgrows the drop-in's first staging buffers (4,096
+    ids); then a short history and an empty one follow on the regrown buffers.
+    Each call has preset scratch bits: with an empty history the scratch comes
+    back exactly as it went in."""
+    rng = np.random.default_rng(17)
+    base = rng.normal(0, 2.5, V).astype(np.float32).view(np.uint32)
+    top = np.argsort(-base.view(np.float32))[:40].astype(np.uint32)
+    long_hist = np.concatenate([rng.integers(0, V, 8960).astype(np.uint32), top])
+    seen0 = np.zeros(s.SEEN_BYTES, np.uint8)
+    for tok in list(top[::4]) + [9, 150_000]:
+        seen0[tok // 8] |= 1 << (tok % 8)
+    gs, rs = s.SamplingState(21), o.SamplingState(21)
+    for hist in (long_hist, top[:25], np.zeros(0, np.uint32)):
+        g, r = base.copy(), base.copy()
+        gseen, rseen = seen0.copy(), seen0.copy()
+        t = s.sample_token_with_repetition(g, hist, gseen, gs)
+        _, rt, _ = o.sample_token_with_repetition(r, hist, rseen, rs)
+        assert t == rt and (g == r).all() and (gseen == rseen).all()
+        assert gs.state() == rs.state() and gs.draws() == rs.draws()
+    assert (gseen == seen0).all()
