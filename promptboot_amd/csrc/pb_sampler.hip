@@ -488,11 +488,14 @@ __global__ __launch_bounds__(kBlock) void segment_kernel(RowParams p) {
 
 // Finishes the rows of a multi-slice launch, one wave per row: the S slice
 // lists are merged (merge_lists_by_threshold) and the row finished.
-__global__ __launch_bounds__(kBlock) void finish_kernel(RowParams p) {
-  __shared__ __align__(16) uint64_t staged[kWaves][kMaxSegments * kTopK + 64];
+// One row per workgroup: a batch's rows spread over as many CUs as there are
+// rows (B = 64: 22.6 against 23.0 us per step with four rows per workgroup).
+constexpr uint32_t kFinishWaves = 1;
+__global__ __launch_bounds__(64 * kFinishWaves) void finish_kernel(RowParams p) {
+  __shared__ __align__(16) uint64_t staged[kFinishWaves][kMaxSegments * kTopK + 64];
   const uint32_t lane = threadIdx.x & 63u;
   const uint32_t wave = threadIdx.x >> 6;
-  const uint32_t row = blockIdx.x * kWaves + wave;
+  const uint32_t row = blockIdx.x * kFinishWaves + wave;
   if (row >= p.rows) return;
   if (row_skipped(p, row)) return;  // decode loop: the token is already PB_NO_TOKEN
   // every load of the S lists and slice records is issued before the first wait
@@ -595,7 +598,8 @@ hipError_t launch_sample(const RowParams& p, hipStream_t stream) {
     hipLaunchKernelGGL((segment_kernel<kChunkF4, true>), dim3(blocks), dim3(kBlock), 0, stream, p);
   } else {
     hipLaunchKernelGGL((segment_kernel<kChunkF4, false>), dim3(blocks), dim3(kBlock), 0, stream, p);
-    hipLaunchKernelGGL(finish_kernel, dim3((p.rows + kWaves - 1) / kWaves), dim3(kBlock), 0, stream,
+    hipLaunchKernelGGL(finish_kernel, dim3((p.rows + kFinishWaves - 1) / kFinishWaves),
+                       dim3(64 * kFinishWaves), 0, stream,
                        p);
   }
   return hipGetLastError();
