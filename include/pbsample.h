@@ -27,7 +27,8 @@
  *   - batched device entry points (pointers to device memory, asynchronous on
  *     the given HIP stream): pb_sample_batch, pb_sample_batch_inplace;
  *   - the fused Q4_0 LM head + sampler: pb_lmhead_pack_q4_0,
- *     pb_lmhead_sample_batch;
+ *     pb_lmhead_sample_batch; the Q8_0 head: pb_lmhead_pack_q8_0,
+ *     pb_lmhead_q8_sample_batch, pb_lmhead_q8_decode_step;
  *   - one step of the REPL's decode loop for many sequences
  *     (src/model_repl.rs:928-1150): pb_decode_step, pb_lmhead_decode_step,
  *     with the host helpers pb_decode_draw and pb_decode_settle;
@@ -229,6 +230,35 @@ uint32_t pb_lmhead_sample_batch(pb_context *ctx, const uint8_t *d_packed, size_t
                                 pb_inference_error *d_err, uint32_t *d_logits, void *stream,
                                 pb_inference_error *err);
 
+/* ---- fused Q8_0 LM head + sampler ----
+ * The model's own output head is Q8_0 (tensor 290, model.rs:817-818;
+ * inference.rs:1739-1749 runs it through coordinator.q8).  These replace
+ * inference_prepare_q8 + inference_q8_matvec_rows_prepared
+ * (fp32_sse2.rs:956-983, 1251-1280) followed by the sampler, with the Q8_0
+ * head's own epilogue: total = add(total, mul(f32(dot), mul(w_scale,
+ * a_scale))) over the blocks in order.  Same arguments, limits and outputs
+ * as the Q4_0 functions above. */
+
+/* Bytes of the device layout of a Q8_0 head (equal to the source size:
+ * rows * cols / 32 blocks of 34 bytes). */
+size_t pb_lmhead_q8_packed_bytes(size_t vocab, size_t cols);
+
+/* Repacks a Q8_0 matrix in promptboot's layout (vocab rows of cols/32 blocks
+ * of 34 bytes: fp16 scale, 32 signed weights) into the device layout (tiles of
+ * 64 ids: vocab must be a multiple of 64).  Device pointers; d_packed 16-byte
+ * aligned and pb_lmhead_q8_packed_bytes long.  Once per model. */
+uint32_t pb_lmhead_pack_q8_0(const uint8_t *d_q8, size_t vocab, size_t cols, uint8_t *d_packed,
+                             void *stream, pb_inference_error *err);
+
+/* pb_lmhead_sample_batch for a head packed by pb_lmhead_pack_q8_0. */
+uint32_t pb_lmhead_q8_sample_batch(pb_context *ctx, const uint8_t *d_packed, size_t vocab,
+                                   size_t cols, const uint32_t *d_hidden, uint32_t rows,
+                                   const uint32_t *d_hist, size_t hist_ld,
+                                   const uint32_t *d_hist_len, const uint32_t *d_random_24,
+                                   uint32_t *d_token, pb_sample_detail *d_detail,
+                                   pb_inference_error *d_err, uint32_t *d_logits, void *stream,
+                                   pb_inference_error *err);
+
 /* ---- decode loop (src/model_repl.rs:928-1150) ----
  * One generation step for `rows` sequences at once, with the REPL's caller
  * contract kept on the device:
@@ -275,6 +305,16 @@ uint32_t pb_lmhead_decode_step(pb_context *ctx, const uint8_t *d_packed, size_t 
                                const uint32_t *d_random_24, uint32_t *d_token,
                                pb_sample_detail *d_detail, pb_inference_error *d_err,
                                uint32_t *d_logits, void *stream, pb_inference_error *err);
+
+/* The same step with the fused Q8_0 head (pb_lmhead_q8_sample_batch): the
+ * REPL's own configuration, whose logits come from the Q8_0 output tensor. */
+uint32_t pb_lmhead_q8_decode_step(pb_context *ctx, const uint8_t *d_packed, size_t vocab,
+                                  size_t cols, const uint32_t *d_hidden, uint32_t rows,
+                                  uint32_t *d_hist, size_t hist_ld, uint32_t *d_hist_len,
+                                  const uint32_t *d_max_len, uint32_t *d_row_state,
+                                  const uint32_t *d_random_24, uint32_t *d_token,
+                                  pb_sample_detail *d_detail, pb_inference_error *d_err,
+                                  uint32_t *d_logits, void *stream, pb_inference_error *err);
 
 /* Host side of a step: saves every states[i] into saved[i]; for each row with
  * row_state[i] == PB_ROW_ACTIVE writes out[i] = pb_next_24(&states[i]); other

@@ -114,6 +114,10 @@ def lib() -> ctypes.CDLL:
         L.pbo_q4_block_dot.restype = ctypes.c_int32
         L.pbo_q4_matvec_rows.argtypes = [vp, vp, vp, size_t, size_t]
         L.pbo_lmhead_logits.argtypes = [vp, u32, vp, size_t, size_t, vp, ctypes.c_int]
+        L.pbo_q8_block_dot.argtypes = [vp, vp]
+        L.pbo_q8_block_dot.restype = ctypes.c_int32
+        L.pbo_q8_matvec_rows.argtypes = [vp, vp, vp, size_t, size_t]
+        L.pbo_lmhead_q8_logits.argtypes = [vp, u32, vp, size_t, size_t, vp, ctypes.c_int]
         L.pbo_expf_array.argtypes = [vp, vp, size_t]
         L.pbo_penalize_array.argtypes = [vp, vp, size_t]
         for name in ("pbo_sizeof_detail", "pbo_sizeof_error", "pbo_sizeof_state"):
@@ -212,16 +216,31 @@ def q4_matvec(weights: np.ndarray, staging: np.ndarray, rows: int, columns: int)
     return out
 
 
+def q8_block_dot(weights32, activation32) -> int:
+    w = np.ascontiguousarray(weights32, dtype=np.int8)
+    a = np.ascontiguousarray(activation32, dtype=np.int8)
+    return lib().pbo_q8_block_dot(_ptr(w), _ptr(a))
+
+
+def q8_matvec(weights: np.ndarray, staging: np.ndarray, rows: int, columns: int) -> np.ndarray:
+    w = np.ascontiguousarray(weights, dtype=np.uint8)
+    out = np.zeros(rows, np.uint32)
+    lib().pbo_q8_matvec_rows(_ptr(w), _ptr(out), _ptr(staging), rows, columns)
+    return out
+
+
 def lmhead_logits(hidden, weights: np.ndarray, vocab: int, columns: int,
-                  threads: int = 1) -> np.ndarray:
-    """Logits [rows, vocab] (uint32 words) of each hidden row through a Q4_0 head
-    in the reference layout (vocab rows of columns/32 blocks of 18 bytes)."""
+                  threads: int = 1, q8: bool = False) -> np.ndarray:
+    """Logits [rows, vocab] (uint32 words) of each hidden row through a Q4_0
+    head (vocab rows of columns/32 blocks of 18 bytes) or, with q8, a Q8_0 head
+    (blocks of 34 bytes), both in the reference layout."""
     h = _u32(hidden)
     rows = h.shape[0]
     w = np.ascontiguousarray(weights, dtype=np.uint8)
-    assert w.size == vocab * columns // 32 * 18
+    assert w.size == vocab * columns // 32 * (34 if q8 else 18)
     out = np.zeros((rows, vocab), np.uint32)
-    lib().pbo_lmhead_logits(_ptr(h), rows, _ptr(w), vocab, columns, _ptr(out), threads)
+    fn = lib().pbo_lmhead_q8_logits if q8 else lib().pbo_lmhead_logits
+    fn(_ptr(h), rows, _ptr(w), vocab, columns, _ptr(out), threads)
     return out
 
 

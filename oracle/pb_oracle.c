@@ -15,6 +15,8 @@
  *   crates/promptboot-core/src/fp32_sse2.rs:147-345    scalar IEEE ops
  *   crates/promptboot-core/src/fp32_sse2.rs:378-469    scalbnf / expf
  *   crates/promptboot-core/src/fp32_sse2.rs:848-867    MXCSR 0x1f80 scope
+ *   crates/promptboot-core/src/fp32_sse2.rs:956-1062   Q8_0 activations, block dots
+ *   crates/promptboot-core/src/fp32_sse2.rs:1217-1280  Q4_0 / Q8_0 head matvecs
  *   crates/promptboot-core/src/fp32_sse2.rs:1772-1876  argmax, top-k/top-p
  *                                                      draw, repetition penalty
  *
@@ -24,7 +26,10 @@
  * row known answer (token 9707), the llama.cpp top-8 lists of the three real
  * rows, the error tuples, a stable-sort brute force of the top-20, an
  * independent float64 softmax, and an exhaustive sweep of all 2^24 uniforms
- * against the categorical CDF.
+ * against the categorical CDF.  The heads: the reference's q8.bin and dots.bin
+ * words (Q8_0 activations, one Q4_0 and one Q8_0 matvec), its block-dot
+ * extrema and deterministic cases, float64 heads, and per-head scale-order
+ * checks on rows where the two orders round differently.
  *
  * Build: oracle/Makefile (gcc -O2 -msse2 -mfpmath=sse -ffp-contract=off).
  */
@@ -688,12 +693,50 @@ void pbo_q4_matvec_rows(const uint8_t *weights, uint32_t *output, const uint8_t 
     exit_fp(saved);
 }
 
+/* Q8_0 x Q8_0 block dot (promptboot_inference_q8_block_dot,
+ * fp32_sse2.rs:1173-1181; scalar form tests.rs:4057-4064): 32 signed weight
+ * bytes against 32 signed activation bytes. */
+int32_t pbo_q8_block_dot(const int8_t *weights32, const int8_t *activation32) {
+    int32_t total = 0;
+    for (int i = 0; i < 32; ++i) total += (int32_t)weights32[i] * (int32_t)activation32[i];
+    return total;
+}
+
+/* inference_q8_matvec_rows_prepared (fp32_sse2.rs:1251-1280): per output row,
+ * total = add(total, mul(f32(dot), mul(weight_scale, activation_scale))) over
+ * the blocks in order -- the two scales are multiplied first, unlike the Q4_0
+ * head.  Weight rows are columns/32 blocks of 34 bytes (fp16 scale, 32 signed
+ * bytes); `staging` is pbo_prepare_q8's output. */
+void pbo_q8_matvec_rows(const uint8_t *weights, uint32_t *output, const uint8_t *staging,
+                        size_t rows, size_t columns) {
+    const unsigned int saved = enter_fp();
+    const size_t blocks = columns >> 5;
+    for (size_t row = 0; row < rows; ++row) {
+        float total = 0.0f;
+        const uint8_t *row_base = weights + row * blocks * 34;
+        for (size_t b = 0; b < blocks; ++b) {
+            const uint8_t *block = row_base + b * 34;
+            const uint8_t *activation = staging + b * 34;
+            const int32_t integer =
+                pbo_q8_block_dot((const int8_t *)(block + 2), (const int8_t *)(activation + 2));
+            const float ws = fb(pbo_half_to_f32_bits((uint16_t)(block[0] | (block[1] << 8))));
+            const float as =
+                fb(pbo_half_to_f32_bits((uint16_t)(activation[0] | (activation[1] << 8))));
+            const float scale = ws * as;
+            total = total + (float)integer * scale;
+        }
+        output[row] = bf(total);
+    }
+    exit_fp(saved);
+}
+
 typedef struct {
     const uint32_t *hidden;
     const uint8_t *weights;
     uint32_t *logits;
     size_t vocab, columns;
     uint32_t row_begin, row_end;
+    int q8;
 } lmhead_job;
 
 static void *lmhead_worker(void *arg) {
@@ -701,16 +744,18 @@ static void *lmhead_worker(void *arg) {
     uint8_t *staging = (uint8_t *)malloc(PBO_Q8_STAGING_BYTES);
     for (uint32_t r = job->row_begin; r < job->row_end; ++r) {
         pbo_prepare_q8(job->hidden + (size_t)r * job->columns, staging, job->columns);
-        pbo_q4_matvec_rows(job->weights, job->logits + (size_t)r * job->vocab, staging, job->vocab,
-                           job->columns);
+        uint32_t *out = job->logits + (size_t)r * job->vocab;
+        if (job->q8)
+            pbo_q8_matvec_rows(job->weights, out, staging, job->vocab, job->columns);
+        else
+            pbo_q4_matvec_rows(job->weights, out, staging, job->vocab, job->columns);
     }
     free(staging);
     return NULL;
 }
 
-/* Logits of `rows` hidden states through the Q4_0 head: logits[r][v]. */
-void pbo_lmhead_logits(const uint32_t *hidden, uint32_t rows, const uint8_t *weights,
-                       size_t vocab, size_t columns, uint32_t *logits, int threads) {
+static void lmhead_logits(const uint32_t *hidden, uint32_t rows, const uint8_t *weights,
+                          size_t vocab, size_t columns, uint32_t *logits, int threads, int q8) {
     if (threads < 1) threads = 1;
     if ((uint32_t)threads > rows) threads = rows ? (int)rows : 1;
     if (threads > 256) threads = 256;
@@ -719,10 +764,22 @@ void pbo_lmhead_logits(const uint32_t *hidden, uint32_t rows, const uint8_t *wei
     for (int t = 0; t < threads; ++t) {
         jobs[t] = (lmhead_job){hidden, weights, logits, vocab, columns,
                                (uint32_t)((uint64_t)rows * t / threads),
-                               (uint32_t)((uint64_t)rows * (t + 1) / threads)};
+                               (uint32_t)((uint64_t)rows * (t + 1) / threads), q8};
         pthread_create(&tid[t], NULL, lmhead_worker, &jobs[t]);
     }
     for (int t = 0; t < threads; ++t) pthread_join(tid[t], NULL);
+}
+
+/* Logits of `rows` hidden states through the Q4_0 head: logits[r][v]. */
+void pbo_lmhead_logits(const uint32_t *hidden, uint32_t rows, const uint8_t *weights,
+                       size_t vocab, size_t columns, uint32_t *logits, int threads) {
+    lmhead_logits(hidden, rows, weights, vocab, columns, logits, threads, 0);
+}
+
+/* Logits of `rows` hidden states through the Q8_0 head: logits[r][v]. */
+void pbo_lmhead_q8_logits(const uint32_t *hidden, uint32_t rows, const uint8_t *weights,
+                          size_t vocab, size_t columns, uint32_t *logits, int threads) {
+    lmhead_logits(hidden, rows, weights, vocab, columns, logits, threads, 1);
 }
 
 /* Single-threaded CPU baseline timer.  For each row: copy the logits into a

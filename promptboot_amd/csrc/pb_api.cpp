@@ -382,8 +382,13 @@ uint32_t pb_sample_batch_inplace(pb_context* ctx, uint32_t* d_logits, size_t voc
 
 size_t pb_lmhead_packed_bytes(size_t vocab, size_t cols) { return vocab * (cols / 32) * 18; }
 
-uint32_t pb_lmhead_pack_q4_0(const uint8_t* d_q4, size_t vocab, size_t cols, uint8_t* d_packed,
-                             void* stream, pb_inference_error* err) {
+size_t pb_lmhead_q8_packed_bytes(size_t vocab, size_t cols) { return vocab * (cols / 32) * 34; }
+
+}  // extern "C"
+
+// Argument checks shared by the Q4_0 and Q8_0 repacks.
+static uint32_t check_pack_args(size_t vocab, size_t cols, const uint8_t* d_packed,
+                                pb_inference_error* err) {
   clear_error(err);
   if (cols == 0 || cols % 32 != 0) {
     set_error(err, PB_CAPACITY, PB_DOMAIN_NONE, 32, cols, PB_FIELD_BYTES, 4);
@@ -399,8 +404,26 @@ uint32_t pb_lmhead_pack_q4_0(const uint8_t* d_q4, size_t vocab, size_t cols, uin
               PB_FIELD_ALIGNMENT, 1);
     return PB_ALIGNMENT;
   }
+  return PB_OK;
+}
+
+extern "C" {
+
+uint32_t pb_lmhead_pack_q4_0(const uint8_t* d_q4, size_t vocab, size_t cols, uint8_t* d_packed,
+                             void* stream, pb_inference_error* err) {
+  const uint32_t st = check_pack_args(vocab, cols, d_packed, err);
+  if (st != PB_OK) return st;
   hipError_t e = pb::launch_lm_pack(d_q4, d_packed, (uint32_t)vocab, (uint32_t)(cols / 32),
                                     static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? PB_OK : device_error(err, e);
+}
+
+uint32_t pb_lmhead_pack_q8_0(const uint8_t* d_q8, size_t vocab, size_t cols, uint8_t* d_packed,
+                             void* stream, pb_inference_error* err) {
+  const uint32_t st = check_pack_args(vocab, cols, d_packed, err);
+  if (st != PB_OK) return st;
+  hipError_t e = pb::launch_lm_pack_q8(d_q8, d_packed, (uint32_t)vocab, (uint32_t)(cols / 32),
+                                       static_cast<hipStream_t>(stream));
   return e == hipSuccess ? PB_OK : device_error(err, e);
 }
 
@@ -412,7 +435,7 @@ static uint32_t enqueue_lmhead(pb_context* ctx, const uint8_t* d_packed, size_t 
                                const uint32_t* d_hist_len, const uint32_t* d_random_24,
                                uint32_t* d_token, pb_sample_detail* d_detail,
                                pb_inference_error* d_err, uint32_t* d_logits, void* stream,
-                               pb_inference_error* err, const DecodeArgs* dec) {
+                               pb_inference_error* err, const DecodeArgs* dec, bool q8) {
   clear_error(err);
   if (vocab != PB_VOCAB) {
     set_error(err, PB_CAPACITY, PB_DOMAIN_LOGITS, PB_VOCAB, vocab, PB_FIELD_LOGITS, 0);
@@ -459,6 +482,7 @@ static uint32_t enqueue_lmhead(pb_context* ctx, const uint8_t* d_packed, size_t 
   char* base = static_cast<char*>(ctx->d_lm);
   pb::LmParams p;
   p.weights = d_packed;
+  p.q8 = q8;
   p.hidden = d_hidden;
   p.rows = rows;
   p.rows_pad = rows_pad;
@@ -504,7 +528,20 @@ uint32_t pb_lmhead_sample_batch(pb_context* ctx, const uint8_t* d_packed, size_t
                                 pb_inference_error* d_err, uint32_t* d_logits, void* stream,
                                 pb_inference_error* err) {
   return enqueue_lmhead(ctx, d_packed, vocab, cols, d_hidden, rows, d_hist, hist_ld, d_hist_len,
-                        d_random_24, d_token, d_detail, d_err, d_logits, stream, err, nullptr);
+                        d_random_24, d_token, d_detail, d_err, d_logits, stream, err, nullptr,
+                        false);
+}
+
+uint32_t pb_lmhead_q8_sample_batch(pb_context* ctx, const uint8_t* d_packed, size_t vocab,
+                                   size_t cols, const uint32_t* d_hidden, uint32_t rows,
+                                   const uint32_t* d_hist, size_t hist_ld,
+                                   const uint32_t* d_hist_len, const uint32_t* d_random_24,
+                                   uint32_t* d_token, pb_sample_detail* d_detail,
+                                   pb_inference_error* d_err, uint32_t* d_logits, void* stream,
+                                   pb_inference_error* err) {
+  return enqueue_lmhead(ctx, d_packed, vocab, cols, d_hidden, rows, d_hist, hist_ld, d_hist_len,
+                        d_random_24, d_token, d_detail, d_err, d_logits, stream, err, nullptr,
+                        true);
 }
 
 // ---- decode loop (src/model_repl.rs:928-1150) ----
@@ -534,7 +571,21 @@ uint32_t pb_lmhead_decode_step(pb_context* ctx, const uint8_t* d_packed, size_t 
   const DecodeArgs dec{d_hist, d_hist_len, d_max_len, d_row_state};
   if (rows != 0 && !decode_args_ok(dec, err)) return PB_CAPACITY;
   return enqueue_lmhead(ctx, d_packed, vocab, cols, d_hidden, rows, d_hist, hist_ld, d_hist_len,
-                        d_random_24, d_token, d_detail, d_err, d_logits, stream, err, &dec);
+                        d_random_24, d_token, d_detail, d_err, d_logits, stream, err, &dec, false);
+}
+
+uint32_t pb_lmhead_q8_decode_step(pb_context* ctx, const uint8_t* d_packed, size_t vocab,
+                                  size_t cols, const uint32_t* d_hidden, uint32_t rows,
+                                  uint32_t* d_hist, size_t hist_ld, uint32_t* d_hist_len,
+                                  const uint32_t* d_max_len, uint32_t* d_row_state,
+                                  const uint32_t* d_random_24, uint32_t* d_token,
+                                  pb_sample_detail* d_detail, pb_inference_error* d_err,
+                                  uint32_t* d_logits, void* stream, pb_inference_error* err) {
+  clear_error(err);
+  const DecodeArgs dec{d_hist, d_hist_len, d_max_len, d_row_state};
+  if (rows != 0 && !decode_args_ok(dec, err)) return PB_CAPACITY;
+  return enqueue_lmhead(ctx, d_packed, vocab, cols, d_hidden, rows, d_hist, hist_ld, d_hist_len,
+                        d_random_24, d_token, d_detail, d_err, d_logits, stream, err, &dec, true);
 }
 
 void pb_decode_draw(pb_sampling_state* states, const uint32_t* row_state, uint32_t rows,

@@ -53,7 +53,9 @@ struct WritebackParams {
 
 // Fused Q4_0 LM head + sampler (pb_lmhead.hip).
 struct LmParams {
-  const uint8_t* weights;   // packed head: [blocks][vocab][16] nibbles, [blocks][vocab] fp16
+  const uint8_t* weights;   // packed head: [blocks][vocab][16] nibbles (Q4_0) or [32] int8
+                            // (Q8_0), then [blocks][vocab] fp16 scales
+  bool q8;                  // the head is Q8_0 (else Q4_0)
   const uint32_t* hidden;   // rows x cols binary32 words
   uint32_t rows;
   uint32_t rows_pad;        // rows rounded up to 64
@@ -72,6 +74,8 @@ struct LmParams {
 
 hipError_t launch_lm_pack(const uint8_t* in, uint8_t* out, uint32_t vocab, uint32_t blocks,
                           hipStream_t stream);
+hipError_t launch_lm_pack_q8(const uint8_t* in, uint8_t* out, uint32_t vocab, uint32_t blocks,
+                             hipStream_t stream);
 hipError_t launch_lm_sample(const LmParams& p, const RowParams& rp, hipStream_t stream);
 hipError_t launch_mfma_selftest(int32_t* out, hipStream_t stream);
 

@@ -57,7 +57,8 @@ constexpr uint32_t kRowsPerGroup = 256;
 constexpr uint32_t kWordsPerRow = kVocab / 32;
 constexpr uint32_t kTilesPerRow = kVocab / kTileIds;  // 2,374
 constexpr uint32_t kCandCap = 800;       // >= 20 lanes x 38 tile keys
-constexpr uint32_t kTileBytes = kTileIds * 16;  // packed nibbles of one (block, tile)
+constexpr uint32_t kTileBytes = kTileIds * 16;    // packed Q4_0 nibbles of one (block, tile)
+constexpr uint32_t kTileBytesQ8 = kTileIds * 32;  // packed Q8_0 weights of one (block, tile)
 // M = 1.5 * 2^23: its binade has unit spacing, so M + i is exact for |i| < 2^22.
 constexpr uint32_t kMagicBits = 0x4b400000u;
 constexpr float kMagic = 12582912.0f;
@@ -142,6 +143,39 @@ __global__ __launch_bounds__(kBlockThreads) void lm_pack_kernel(const uint8_t* _
     tile[(q * 16u + n) * 4u + c] = w ^ 0x88888888u;
   }
   uint16_t* scales = reinterpret_cast<uint16_t*>(out + (size_t)blocks * vocab * 16);
+  scales[(size_t)b * vocab + v] = (uint16_t)(src[0] | (src[1] << 8));
+}
+
+// ---- repack: promptboot's Q8_0 rows -> the head's tile layout ----
+// in:  vocab rows of `blocks` x 34 bytes (fp16 scale, 32 signed weights; the
+//      output tensor of model.rs:817-818).
+// out: [blocks][vocab / 64 tiles][2 KB] weights, then [blocks][vocab] fp16
+//      scales.  In the 2 KB of (block b, tile t), lane l = 16 q + n of a head
+//      wave reads the 32 bytes at 32 l: bytes 8c .. 8c+7 of them are weights
+//      4q .. 4q+3 and 16+4q .. 16+4q+3 of id 64 t + 4 n + c, the contraction
+//      order of the activations.  vocab % 64 == 0.
+__global__ __launch_bounds__(kBlockThreads) void lm_pack_q8_kernel(const uint8_t* __restrict__ in,
+                                                                   uint8_t* __restrict__ out,
+                                                                   uint32_t vocab, uint32_t blocks) {
+  const size_t gid = (size_t)blockIdx.x * kBlockThreads + threadIdx.x;
+  if (gid >= (size_t)vocab * blocks) return;
+  const uint32_t v = (uint32_t)(gid / blocks);
+  const uint32_t b = (uint32_t)(gid % blocks);
+  const uint8_t* src = in + gid * 34;
+  const uint32_t t = v / kTileIds;
+  const uint32_t n = (v % kTileIds) / 4u;
+  const uint32_t c = v % 4u;
+  uint8_t* tile = out + ((size_t)b * (vocab / kTileIds) + t) * kTileBytesQ8;
+#pragma unroll
+  for (uint32_t q = 0; q < 4; ++q) {
+    uint8_t* dst = tile + (q * 16u + n) * 32u + c * 8u;
+#pragma unroll
+    for (uint32_t e = 0; e < 4; ++e) {
+      dst[e] = src[2 + 4 * q + e];
+      dst[4 + e] = src[2 + 16 + 4 * q + e];
+    }
+  }
+  uint16_t* scales = reinterpret_cast<uint16_t*>(out + (size_t)blocks * vocab * 32);
   scales[(size_t)b * vocab + v] = (uint16_t)(src[0] | (src[1] << 8));
 }
 
@@ -265,6 +299,14 @@ __global__ __launch_bounds__(kBlockThreads) void lm_prep_kernel(LmParams p) {
 // subnormal and overflow ranges.  A tile with an infinite or NaN fp16 weight
 // scale uses (x - M) * ws instead, which gives inf * 0 = NaN as the
 // reference does.
+//
+// The Q8_0 head (kQ8) reads both 4-byte halves of each B operand from the
+// packed weights as they are, starts the accumulator at zero and follows
+// inference_q8_matvec_rows_prepared (fp32_sse2.rs:1251-1280):
+// add(total, mul(f32(dot), mul(ws, a_scale))), four VALU ops per value.  (The
+// scales are both fp16 values, so ws * a_scale is exact, but the conversion
+// cannot be folded into an FMA as above: M * ws * a_scale may need 26 bits.)
+template <bool kQ8>
 __global__ __launch_bounds__(kGemmThreads) void lm_gemm_kernel(LmParams p) {
   // Dynamic LDS: the activation scales / 16 of every block for the group's
   // 256 rows, then this tile's weight scales and -M * weight scales by block.
@@ -283,7 +325,7 @@ __global__ __launch_bounds__(kGemmThreads) void lm_gemm_kernel(LmParams p) {
   const uint32_t v0 = tile * kTileIds;
   const uint32_t group0 = blockIdx.y * kRowsPerGroup;
   const uint16_t* wscale16 =
-      reinterpret_cast<const uint16_t*>(p.weights + (size_t)blocks * kVocab * 16);
+      reinterpret_cast<const uint16_t*>(p.weights + (size_t)blocks * kVocab * (kQ8 ? 32 : 16));
 
   uint32_t odd = 0;  // this tile has an infinite or NaN weight scale
   for (uint32_t i = tid; i < blocks * kTileIds; i += kGemmThreads) {
@@ -291,8 +333,10 @@ __global__ __launch_bounds__(kGemmThreads) void lm_gemm_kernel(LmParams p) {
     const float ws =
         __half2float(__ushort_as_half(wscale16[(size_t)b * kVocab + v0 + (i - b * kTileIds)]));
     w_scale[i] = ws;
-    w_neg[i] = ws * -kMagic;
-    odd |= (b_of(ws) & 0x7f800000u) == 0x7f800000u ? 1u : 0u;
+    if (!kQ8) {
+      w_neg[i] = ws * -kMagic;
+      odd |= (b_of(ws) & 0x7f800000u) == 0x7f800000u ? 1u : 0u;
+    }
   }
   for (uint32_t i = tid; i < kRowsPerGroup * 2; i += kGemmThreads) {
     const uint32_t r = group0 + i / 2;
@@ -301,7 +345,9 @@ __global__ __launch_bounds__(kGemmThreads) void lm_gemm_kernel(LmParams p) {
   for (uint32_t i = tid; i < blocks * kRowsPerGroup; i += kGemmThreads) {
     const uint32_t b = i / kRowsPerGroup;
     const uint32_t r = group0 + (i - b * kRowsPerGroup);
-    act_scale[i] = r < p.rows_pad ? p.act_s[(size_t)b * p.rows_pad + r] : 0.0f;
+    // lm_prep_kernel stores a_scale / 16 (exact); the Q8_0 epilogue needs a_scale
+    const float as16 = r < p.rows_pad ? p.act_s[(size_t)b * p.rows_pad + r] : 0.0f;
+    act_scale[i] = kQ8 ? as16 * 16.0f : as16;
   }
   const bool odd_tile = __syncthreads_or((int)odd) != 0;
 
@@ -320,8 +366,11 @@ __global__ __launch_bounds__(kGemmThreads) void lm_gemm_kernel(LmParams p) {
   const v4i magic = {(int)kMagicBits, (int)kMagicBits, (int)kMagicBits, (int)kMagicBits};
   const uint8_t* a_base = reinterpret_cast<const uint8_t*>(p.act_q) + ((size_t)rw0 + n) * 32 + 8u * q;
   const size_t a_stride = (size_t)p.rows_pad * 32;  // bytes per block
-  const v4u* w_base = reinterpret_cast<const v4u*>(p.weights + (size_t)tile * kTileBytes) + lane;
-  const size_t w_stride = (size_t)kTilesPerRow * (kTileBytes / 16);  // uint4 per block
+  constexpr uint32_t kWords = kQ8 ? 2u : 1u;  // uint4 of packed weights per lane and block
+  const v4u* w_base =
+      reinterpret_cast<const v4u*>(p.weights + (size_t)tile * (kQ8 ? kTileBytesQ8 : kTileBytes)) +
+      kWords * lane;
+  const size_t w_stride = (size_t)kTilesPerRow * ((kQ8 ? kTileBytesQ8 : kTileBytes) / 16);
 
   // Operands of one block: both row tiles' activation fragments and the
   // lane's packed weight words (one per column tile).  Two sets alternate
@@ -329,13 +378,14 @@ __global__ __launch_bounds__(kGemmThreads) void lm_gemm_kernel(LmParams p) {
   // while the current block runs and no registers are copied.
   struct Operands {
     uint64_t a[2];
-    v4u raw;
+    v4u raw[kWords];
   };
   auto load = [&](uint32_t b, Operands& o) {
     const uint8_t* ab = a_base + (size_t)b * a_stride;
     o.a[0] = *reinterpret_cast<const uint64_t*>(ab);
     o.a[1] = *reinterpret_cast<const uint64_t*>(ab + 16u * 32u);
-    o.raw = w_base[(size_t)b * w_stride];
+#pragma unroll
+    for (uint32_t k = 0; k < kWords; ++k) o.raw[k] = w_base[(size_t)b * w_stride + k];
   };
   auto run = [&](uint32_t b, const Operands& o, auto odd_tag) {
     constexpr bool kOdd = decltype(odd_tag)::value;
@@ -346,15 +396,29 @@ __global__ __launch_bounds__(kGemmThreads) void lm_gemm_kernel(LmParams p) {
     for (int rt = 0; rt < 2; ++rt)
       as[rt] = *reinterpret_cast<const v4f*>(
           &act_scale[b * kRowsPerGroup + lrow0 + 16u * rt + 4u * q]);
-    const uint32_t raw[4] = {o.raw.x, o.raw.y, o.raw.z, o.raw.w};
     v4i d[2][4];
+    if constexpr (kQ8) {
+      const uint32_t raw[8] = {o.raw[0].x, o.raw[0].y, o.raw[0].z, o.raw[0].w,
+                               o.raw[kWords - 1].x, o.raw[kWords - 1].y, o.raw[kWords - 1].z,
+                               o.raw[kWords - 1].w};
+      const v4i zero = {0, 0, 0, 0};
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const uint64_t w = (uint64_t)((raw[c] << 4) & 0xf0f0f0f0u) |
-                         ((uint64_t)(raw[c] & 0xf0f0f0f0u) << 32);
+      for (int c = 0; c < 4; ++c) {
+        const uint64_t w = (uint64_t)raw[2 * c] | ((uint64_t)raw[2 * c + 1] << 32);
 #pragma unroll
-      for (int rt = 0; rt < 2; ++rt)
-        d[rt][c] = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)o.a[rt], (long)w, magic, 0, 0, 0);
+        for (int rt = 0; rt < 2; ++rt)
+          d[rt][c] = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)o.a[rt], (long)w, zero, 0, 0, 0);
+      }
+    } else {
+      const uint32_t raw[4] = {o.raw[0].x, o.raw[0].y, o.raw[0].z, o.raw[0].w};
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const uint64_t w = (uint64_t)((raw[c] << 4) & 0xf0f0f0f0u) |
+                           ((uint64_t)(raw[c] & 0xf0f0f0f0u) << 32);
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt)
+          d[rt][c] = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)o.a[rt], (long)w, magic, 0, 0, 0);
+      }
     }
     const float wsv[4] = {ws.x, ws.y, ws.z, ws.w};
     const float wnv[4] = {wn.x, wn.y, wn.z, wn.w};
@@ -365,9 +429,14 @@ __global__ __launch_bounds__(kGemmThreads) void lm_gemm_kernel(LmParams p) {
       for (int c = 0; c < 4; ++c) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float x = __int_as_float(d[rt][c][i]);
-          const float y = kOdd ? (x - kMagic) * wsv[c] : __builtin_fmaf(x, wsv[c], wnv[c]);
-          total[rt][c][i] = total[rt][c][i] + y * asv[i];
+          if constexpr (kQ8) {
+            const float scale = wsv[c] * asv[i];
+            total[rt][c][i] = total[rt][c][i] + (float)d[rt][c][i] * scale;
+          } else {
+            const float x = __int_as_float(d[rt][c][i]);
+            const float y = kOdd ? (x - kMagic) * wsv[c] : __builtin_fmaf(x, wsv[c], wnv[c]);
+            total[rt][c][i] = total[rt][c][i] + y * asv[i];
+          }
         }
       }
     }
@@ -396,7 +465,9 @@ __global__ __launch_bounds__(kGemmThreads) void lm_gemm_kernel(LmParams p) {
     }
     if (blocks & 1u) run(last, even, odd_tag);
   };
-  if (odd_tile) {
+  if constexpr (kQ8) {
+    gemm(std::false_type{});
+  } else if (odd_tile) {
     gemm(std::true_type{});
   } else {
     gemm(std::false_type{});
@@ -643,15 +714,27 @@ hipError_t launch_lm_pack(const uint8_t* in, uint8_t* out, uint32_t vocab, uint3
   return hipGetLastError();
 }
 
+hipError_t launch_lm_pack_q8(const uint8_t* in, uint8_t* out, uint32_t vocab, uint32_t blocks,
+                             hipStream_t stream) {
+  const size_t n = (size_t)vocab * blocks;
+  hipLaunchKernelGGL(lm_pack_q8_kernel, dim3((uint32_t)((n + kBlockThreads - 1) / kBlockThreads)),
+                     dim3(kBlockThreads), 0, stream, in, out, vocab, blocks);
+  return hipGetLastError();
+}
+
 size_t gemm_lds_bytes(uint32_t cols) {
   return (size_t)(cols / 32u) * (kRowsPerGroup + 2u * kTileIds) * sizeof(float);
 }
 
 hipError_t launch_lm_sample(const LmParams& p, const RowParams& rp, hipStream_t stream) {
   hipLaunchKernelGGL(lm_prep_kernel, dim3(p.rows_pad), dim3(kBlockThreads), 0, stream, p);
-  hipLaunchKernelGGL(lm_gemm_kernel,
-                     dim3(kTilesPerRow, (p.rows_pad + kRowsPerGroup - 1) / kRowsPerGroup),
-                     dim3(kGemmThreads), gemm_lds_bytes(p.cols), stream, p);
+  const dim3 gemm_grid(kTilesPerRow, (p.rows_pad + kRowsPerGroup - 1) / kRowsPerGroup);
+  if (p.q8)
+    hipLaunchKernelGGL(lm_gemm_kernel<true>, gemm_grid, dim3(kGemmThreads), gemm_lds_bytes(p.cols),
+                       stream, p);
+  else
+    hipLaunchKernelGGL(lm_gemm_kernel<false>, gemm_grid, dim3(kGemmThreads), gemm_lds_bytes(p.cols),
+                       stream, p);
   hipLaunchKernelGGL(lm_select_kernel, dim3((p.rows + kSelectWaves - 1) / kSelectWaves),
                      dim3(64 * kSelectWaves), 0, stream,
                      p, rp);

@@ -120,6 +120,14 @@ EXPORTS = {
     "pb_lmhead_decode_step": (
         u32, [vp, vp, size_t, size_t, vp, u32, vp, size_t, vp, vp, vp, vp, vp, vp, vp, vp,
               vp, ctypes.POINTER(_Error)]),
+    "pb_lmhead_q8_packed_bytes": (size_t, [size_t, size_t]),
+    "pb_lmhead_pack_q8_0": (u32, [vp, size_t, size_t, vp, vp, ctypes.POINTER(_Error)]),
+    "pb_lmhead_q8_sample_batch": (
+        u32, [vp, vp, size_t, size_t, vp, u32, vp, size_t, vp, vp, vp, vp, vp, vp, vp,
+              ctypes.POINTER(_Error)]),
+    "pb_lmhead_q8_decode_step": (
+        u32, [vp, vp, size_t, size_t, vp, u32, vp, size_t, vp, vp, vp, vp, vp, vp, vp, vp,
+              vp, ctypes.POINTER(_Error)]),
     "pb_decode_draw": (None, [vp, vp, u32, vp, vp]),
     "pb_decode_settle": (u32, [vp, vp, vp, vp, u32]),
     "pb_version": (ctypes.c_char_p, []),
@@ -334,25 +342,30 @@ class BatchSampler:
                 ctypes.byref(e))
         _check(st, e)
 
-    def pack_lmhead(self, q4_weights, vocab: int = VOCAB, cols: int = 896, stream=None):
-        """Repacks a Q4_0 head (torch uint8 device tensor in promptboot's
-        layout) into the device layout; returns the packed uint8 tensor."""
+    def pack_lmhead(self, weights, vocab: int = VOCAB, cols: int = 896, stream=None,
+                    q8: bool = False):
+        """Repacks a Q4_0 head (or, with q8, a Q8_0 head) given as a torch uint8
+        device tensor in promptboot's layout into the device layout; returns
+        the packed uint8 tensor."""
         import torch
 
-        packed = torch.empty(lib().pb_lmhead_packed_bytes(vocab, cols), dtype=torch.uint8,
-                             device=q4_weights.device)
-        s = stream if stream is not None else torch.cuda.current_stream(q4_weights.device)
+        nbytes = (lib().pb_lmhead_q8_packed_bytes if q8 else lib().pb_lmhead_packed_bytes)(
+            vocab, cols)
+        packed = torch.empty(nbytes, dtype=torch.uint8, device=weights.device)
+        s = stream if stream is not None else torch.cuda.current_stream(weights.device)
         e = _Error()
-        st = lib().pb_lmhead_pack_q4_0(ctypes.c_void_p(q4_weights.data_ptr()), vocab, cols,
-                                       ctypes.c_void_p(packed.data_ptr()),
-                                       ctypes.c_void_p(s.cuda_stream), ctypes.byref(e))
+        pack = lib().pb_lmhead_pack_q8_0 if q8 else lib().pb_lmhead_pack_q4_0
+        st = pack(ctypes.c_void_p(weights.data_ptr()), vocab, cols,
+                  ctypes.c_void_p(packed.data_ptr()), ctypes.c_void_p(s.cuda_stream),
+                  ctypes.byref(e))
         _check(st, e)
         return packed
 
     def lmhead_sample(self, packed, hidden, random_24, history=None, history_len=None, *,
                       token, detail=None, err=None, logits=None, cols: int = 896,
-                      stream=None) -> None:
-        """Enqueues the fused Q4_0 LM head + sampler for hidden [B, cols]."""
+                      stream=None, q8: bool = False) -> None:
+        """Enqueues the fused Q4_0 (or, with q8, Q8_0) LM head + sampler for
+        hidden [B, cols]; `packed` comes from pack_lmhead with the same q8."""
         import torch
 
         rows = hidden.shape[0]
@@ -363,7 +376,8 @@ class BatchSampler:
         def p(t):
             return None if t is None else ctypes.c_void_p(t.data_ptr())
 
-        st = lib().pb_lmhead_sample_batch(
+        fn = lib().pb_lmhead_q8_sample_batch if q8 else lib().pb_lmhead_sample_batch
+        st = fn(
             self._ctx, p(packed), VOCAB, cols, p(hidden), rows, p(history), hist_ld,
             p(history_len), p(random_24), p(token), p(detail), p(err), p(logits),
             ctypes.c_void_p(s.cuda_stream), ctypes.byref(e))
@@ -481,14 +495,17 @@ class DecodeBatch:
         _check(st, e)
         return self._settle(before)
 
-    def lmhead_step(self, packed, hidden, cols: int = 896, stream=None) -> np.ndarray:
-        """One step through the fused Q4_0 LM head on hidden [rows, cols]."""
+    def lmhead_step(self, packed, hidden, cols: int = 896, stream=None,
+                    q8: bool = False) -> np.ndarray:
+        """One step through the fused Q4_0 (or, with q8, Q8_0) LM head on
+        hidden [rows, cols]."""
         import torch
 
         before, r24 = self._draw()
         s = stream if stream is not None else torch.cuda.current_stream(self.dev)
         e = _Error()
-        st = lib().pb_lmhead_decode_step(
+        fn = lib().pb_lmhead_q8_decode_step if q8 else lib().pb_lmhead_decode_step
+        st = fn(
             self.sampler._ctx, ctypes.c_void_p(packed.data_ptr()), VOCAB, cols,
             ctypes.c_void_p(hidden.data_ptr()), self.rows,
             ctypes.c_void_p(self.hist.data_ptr()), self.hist_ld,

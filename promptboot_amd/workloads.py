@@ -150,11 +150,24 @@ def make_lmhead(rows: int = 256, seed: int = 20240601, base_seed: int = 42) -> d
                 random_24=next_24_stream(seeds), seeds=seeds)
 
 
-def lmhead_algorithmic_bytes(rows: int, hist_len: np.ndarray) -> int:
-    """HBM bytes of one fused step: the Q4_0 head once (18 B per 32 weights),
-    the hidden states, the valid history ids, and per-row length, uniform and
-    token words."""
-    return (VOCAB * HIDDEN // 32 * 18 + rows * HIDDEN * 4 + 12 * rows
+def make_q8_head(seed: int = 20240601, cols: int = HIDDEN) -> np.ndarray:
+    """A Q8_0 head of 151,936 x cols in promptboot's layout (the model's output
+    tensor, model.rs:817-818): vocab rows of cols/32 blocks of 34 bytes, fp16
+    scale ~ U(0.0005, 0.004) and 32 signed weights over the whole int8 range."""
+    rng = np.random.default_rng([seed, 88])
+    blocks = cols // 32
+    q8 = np.empty((VOCAB, blocks, 34), np.uint8)
+    scales = rng.uniform(0.0005, 0.004, (VOCAB, blocks)).astype(np.float16)
+    q8[:, :, 0:2] = scales.view(np.uint8).reshape(VOCAB, blocks, 2)
+    q8[:, :, 2:] = rng.integers(0, 256, (VOCAB, blocks, 32), dtype=np.uint8)
+    return q8.reshape(-1)
+
+
+def lmhead_algorithmic_bytes(rows: int, hist_len: np.ndarray, q8: bool = False) -> int:
+    """HBM bytes of one fused step: the head once (18 B per 32 Q4_0 weights, 34
+    B per 32 Q8_0 weights), the hidden states, the valid history ids, and
+    per-row length, uniform and token words."""
+    return (VOCAB * HIDDEN // 32 * (34 if q8 else 18) + rows * HIDDEN * 4 + 12 * rows
             + 4 * int(np.asarray(hist_len, np.int64).sum()))
 
 

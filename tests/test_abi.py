@@ -163,13 +163,19 @@ def test_decode_step_argument_errors_need_no_device():
 
 
 def test_lmhead_pack_argument_errors_need_no_device():
-    """The packed head groups the vocabulary in 64-id tiles; other sizes and
-    hidden widths that are not whole Q4_0 blocks are rejected before any
-    device work."""
+    """The packed heads group the vocabulary in 64-id tiles; other sizes,
+    hidden widths that are not whole blocks and unaligned outputs are rejected
+    before any device work, by the Q4_0 and the Q8_0 repack alike."""
     import ctypes
 
     e = s._Error()
-    st = s.lib().pb_lmhead_pack_q4_0(None, s.VOCAB + 32, 896, None, None, ctypes.byref(e))
-    assert st == s.CAPACITY and e.needed == 64 and e.available == s.VOCAB + 32
-    st = s.lib().pb_lmhead_pack_q4_0(None, s.VOCAB, 900, None, None, ctypes.byref(e))
-    assert st == s.CAPACITY and e.needed == 32 and e.available == 900
+    for pack in (s.lib().pb_lmhead_pack_q4_0, s.lib().pb_lmhead_pack_q8_0):
+        st = pack(None, s.VOCAB + 32, 896, None, None, ctypes.byref(e))
+        assert st == s.CAPACITY and e.needed == 64 and e.available == s.VOCAB + 32
+        st = pack(None, s.VOCAB, 900, None, None, ctypes.byref(e))
+        assert st == s.CAPACITY and e.needed == 32 and e.available == 900
+        st = pack(None, s.VOCAB, 896, ctypes.c_void_p(8), None, ctypes.byref(e))
+        assert st == s.ALIGNMENT and e.needed == 16 and e.available == 8
+    # both layouts are as large as their source matrices
+    assert s.lib().pb_lmhead_packed_bytes(s.VOCAB, 896) == s.VOCAB * 28 * 18
+    assert s.lib().pb_lmhead_q8_packed_bytes(s.VOCAB, 896) == s.VOCAB * 28 * 34

@@ -56,7 +56,7 @@ def test_mfma_fragment_layout():
     assert (out.cpu().numpy().reshape(32, 32) == want).all()
 
 
-def run_head(smp, packed, hidden, hist, hist_len, r24):
+def run_head(smp, packed, hidden, hist, hist_len, r24, q8=False, cols=workloads.HIDDEN):
     import torch
 
     B = hidden.shape[0]
@@ -65,7 +65,7 @@ def run_head(smp, packed, hidden, hist, hist_len, r24):
     err = torch.empty((B, s.ERROR_DTYPE.itemsize // 4), dtype=torch.int32, device="cuda:0")
     logits = torch.empty((B, V), dtype=torch.int32, device="cuda:0")
     smp.lmhead_sample(packed, to_dev(hidden), to_dev(r24), to_dev(hist), to_dev(hist_len),
-                      token=token, detail=det, err=err, logits=logits)
+                      token=token, detail=det, err=err, logits=logits, q8=q8, cols=cols)
     torch.cuda.synchronize()
     return (logits.cpu().numpy().view(np.uint32), token.cpu().numpy().view(np.uint32),
             det.cpu().numpy().view(s.DETAIL_DTYPE).reshape(B),

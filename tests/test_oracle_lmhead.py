@@ -184,3 +184,104 @@ def test_q4_head_scale_order_and_block_order_are_the_references():
         assert got[v] == t4.view(np.uint32), v
         differs += t4 != t8
     assert differs > 0
+
+
+# ---- the Q8_0 head (fp32_sse2.rs:1251-1280) ----
+
+def reference_q8_weights():
+    """The Q8_0 rows of tests.rs:4152-4158: two blocks with fp16 scale 1.0 and
+    weight i = (i % 17) - 8."""
+    q8 = np.zeros(68, np.uint8)
+    for block in range(2):
+        q8[block * 34:block * 34 + 2] = [0x00, 0x3C]
+        q8[block * 34 + 2:block * 34 + 34] = (np.arange(32) % 17 - 8).astype(np.int8).view(np.uint8)
+    return q8
+
+
+def test_q8_matvec_matches_pinned_dot():
+    x, _ = reference_matvec_input()
+    staging = o.prepare_q8(x)
+    out = o.q8_matvec(reference_q8_weights(), staging, rows=1, columns=64)
+    dots = np.fromfile(GOLDEN / "q4_q8_dots.bin", dtype="<u4")
+    assert int(out[0]) == int(dots[1]) == 0x44388000
+
+
+def test_q8_block_dot_extrema_and_the_references_deterministic_cases():
+    """tests.rs:4026-4050 (signed extrema, dot 8) and tests.rs:4053-4100: the
+    reference's 256 generated cases, against an integer dot product."""
+    w = np.array([-128 if (i & 3) in (0, 1) else 127 for i in range(32)], np.int8)
+    a = np.array([-128 if (i & 3) in (0, 2) else 127 for i in range(32)], np.int8)
+    assert o.q8_block_dot(w, a) == 8
+    state = 0x243F6A88
+
+    def nxt():
+        nonlocal state
+        state = (state * 1_664_525 + 1_013_904_223) & 0xFFFFFFFF
+        return state >> 24
+
+    for _ in range(256):
+        q4w = np.array([nxt() for _ in range(16)], np.uint8)
+        q8w = np.array([nxt() for _ in range(32)], np.uint8).view(np.int8)
+        act = np.array([nxt() for _ in range(32)], np.uint8).view(np.int8)
+        assert o.q8_block_dot(q8w, act) == int(q8w.astype(np.int64) @ act.astype(np.int64))
+        assert o.q4_block_dot(q4w, act) == numpy_q4_dot(q4w, act)
+
+
+def test_q8_lmhead_logits_against_float64():
+    rng = np.random.default_rng(5)
+    vocab, cols, rows = 96, 896, 3
+    hidden = rng.standard_normal((rows, cols)).astype(np.float32)
+    blocks = cols // 32
+    w = np.zeros((vocab, blocks, 34), np.uint8)
+    scales = rng.uniform(0.001, 0.02, (vocab, blocks)).astype(np.float16)
+    w[:, :, 0:2] = scales.view(np.uint8).reshape(vocab, blocks, 2)
+    w[:, :, 2:] = rng.integers(0, 256, (vocab, blocks, 32))
+    logits = o.lmhead_logits(hidden, w.reshape(-1), vocab, cols, threads=2, q8=True)
+    wq = w[:, :, 2:].view(np.int8).astype(np.int64)
+    for r in range(rows):
+        st = o.prepare_q8(hidden[r])
+        sb = st[:blocks * 34].reshape(blocks, 34)
+        a_scale = sb[:, 0:2].copy().view(np.float16).astype(np.float64).reshape(blocks)
+        a = sb[:, 2:].view(np.int8).astype(np.int64)
+        dots = np.einsum("vbk,bk->vb", wq, a)
+        want = (dots * scales.astype(np.float64) * a_scale).sum(axis=1)
+        got = logits[r].view(np.float32).astype(np.float64)
+        assert np.allclose(got, want, rtol=1e-5, atol=1e-6)
+        assert (o.q8_matvec(w.reshape(-1), st, vocab, cols) == logits[r]).all()
+
+
+def test_q8_head_scale_order_is_the_references():
+    """fp32_sse2.rs:1271-1274 multiplies the two scales first:
+    mul(f32(dot), mul(w_scale, a_scale)).  (Both are fp16 values, so their
+    product is exact and each term is rounded once.)  Rows where the Q4_0
+    head's order would round differently must follow the Q8_0 order."""
+    rng = np.random.default_rng(6)
+    vocab, cols = 64, 896
+    blocks = cols // 32
+    hidden = rng.standard_normal(cols).astype(np.float32) * np.float32(3)
+    st = o.prepare_q8(hidden)
+    sb = st[:blocks * 34].reshape(blocks, 34)
+    a_scale = sb[:, 0:2].copy().view(np.float16).astype(np.float32).reshape(blocks)
+    a = sb[:, 2:].view(np.int8).astype(np.int64)
+    w = np.zeros((vocab, blocks, 34), np.uint8)
+    scales = rng.uniform(0.001, 0.02, (vocab, blocks)).astype(np.float16)
+    w[:, :, 0:2] = scales.view(np.uint8).reshape(vocab, blocks, 2)
+    # weights aligned with the activations' signs: |dot| large, so f32(dot) * ws needs
+    # more than 24 bits and the two orders can round differently
+    sign = np.sign(a).astype(np.int64)
+    mag = rng.integers(64, 128, (vocab, blocks, 32))
+    w[:, :, 2:] = (sign[None] * mag).astype(np.int8).view(np.uint8)
+    got = o.q8_matvec(w.reshape(-1), st, vocab, cols)
+    wq = w[:, :, 2:].view(np.int8).astype(np.int64)
+    differs = 0
+    for v in range(vocab):
+        t8 = np.float32(0)
+        t4 = np.float32(0)
+        for b in range(blocks):
+            d = np.float32(int(wq[v, b] @ a[b]))
+            ws = np.float32(scales[v, b])
+            t8 = np.float32(t8 + np.float32(d * np.float32(ws * a_scale[b])))
+            t4 = np.float32(t4 + np.float32(np.float32(d * ws) * a_scale[b]))
+        assert got[v] == t8.view(np.uint32), v
+        differs += t4 != t8
+    assert differs > 0
