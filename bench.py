@@ -22,6 +22,7 @@ The printed JSON line also carries:
   adversarial_B1024  the flat / ties / dominant / half-vocabulary-history
                      sub-cases, each timed and checked against the oracle;
   lmhead_fused       the fused Q4_0 LM head + sampler step (B=256);
+  lmhead_q8_fused    the same with the Q8_0 head (the model's output head);
   host_buffers       PCIe-inclusive rates: the single-row drop-in on host
                      buffers, and the B=4096 batch copied from pinned host
                      memory every step (not the headline value).
@@ -238,33 +239,35 @@ MFMA_INT8_PEAK_TOPS = 5000.0     # dense int8 MFMA, MI355X
 VALU_LANE_OPS_PEAK = 256 * 4 * 16 * 2.4e9  # 32-bit VALU lane-ops/s, MI355X
 
 
-def time_lmhead(smp, steps: int, warmup: int) -> dict:
-    """Fused Q4_0 LM head + sampler, B=256 hidden states of width 896."""
+def time_lmhead(smp, steps: int, warmup: int, q8: bool = False) -> dict:
+    """Fused Q4_0 (or, with q8, Q8_0) LM head + sampler, B=256 hidden states of
+    width 896."""
     import torch
 
     from promptboot_amd import sampler as s
     from promptboot_amd import workloads
 
     w = workloads.make_lmhead(rows=256)
+    head = workloads.make_q8_head() if q8 else w["q4"]
     dev = torch.device("cuda:0")
 
     def t(a):
         return torch.from_numpy(np.ascontiguousarray(a).view(np.int32)).to(dev)
 
-    packed = smp.pack_lmhead(torch.from_numpy(w["q4"]).to(dev))
+    packed = smp.pack_lmhead(torch.from_numpy(head).to(dev), q8=q8)
     hidden, hist, hl, r24 = t(w["hidden"]), t(w["hist"]), t(w["hist_len"]), t(w["random_24"])
     B = hidden.shape[0]
     token = torch.empty(B, dtype=torch.int32, device=dev)
     stream = torch.cuda.current_stream(dev)
 
     def step():
-        smp.lmhead_sample(packed, hidden, r24, hist, hl, token=token, stream=stream)
+        smp.lmhead_sample(packed, hidden, r24, hist, hl, token=token, stream=stream, q8=q8)
 
     # one step with the logits and detail kept, for the parity check below
     logits = torch.empty((B, s.VOCAB), dtype=torch.int32, device=dev)
     det = torch.empty((B, s.DETAIL_DTYPE.itemsize // 4), dtype=torch.int32, device=dev)
     smp.lmhead_sample(packed, hidden, r24, hist, hl, token=token, detail=det, logits=logits,
-                      stream=stream)
+                      stream=stream, q8=q8)
     torch.cuda.synchronize()
     n_check = PARITY_LMHEAD_ROWS
     g_logits = logits[:n_check].cpu().numpy().view(np.uint32)
@@ -289,13 +292,13 @@ def time_lmhead(smp, steps: int, warmup: int) -> dict:
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     step_ms = float(np.mean([a.elapsed_time(b) for a, b in zip(starts, ends)]))
-    # parity on a bounded sample: the oracle's Q4_0 head and sampler on the
-    # first rows (bit-exact logits; token agreement on non-boundary rows)
+    # parity on a bounded sample: the oracle's head and sampler on the first
+    # rows (bit-exact logits; token agreement on non-boundary rows)
     from oracle import oracle as o
 
     threads = min(16, len(os.sched_getaffinity(0)))
-    r_logits = o.lmhead_logits(w["hidden"][:n_check], w["q4"], workloads.VOCAB,
-                               workloads.HIDDEN, threads=threads)
+    r_logits = o.lmhead_logits(w["hidden"][:n_check], head, workloads.VOCAB,
+                               workloads.HIDDEN, threads=threads, q8=q8)
     r_tok, _, _, _ = o.sample_batch(r_logits, w["hist"][:n_check], w["hist_len"][:n_check],
                                     w["random_24"][:n_check], threads=threads)
     rl = r_logits.view(np.float32).astype(np.float64)
@@ -309,9 +312,11 @@ def time_lmhead(smp, steps: int, warmup: int) -> dict:
               if (~boundary).any() else None,
               "boundary_rows": int(boundary.sum())}
     ops = 2.0 * B * workloads.VOCAB * workloads.HIDDEN
-    # three IEEE roundings per (row, id, block): f32(dot) * w_scale, * a_scale, + total
-    epilogue = 3.0 * B * workloads.VOCAB * (workloads.HIDDEN // 32)
-    alg = workloads.lmhead_algorithmic_bytes(B, w["hist_len"])
+    # VALU ops per (row, id, block).  Q4_0: three IEEE roundings, f32(dot) *
+    # w_scale, * a_scale, + total (the conversion folds into the first).  Q8_0:
+    # the conversion, w_scale * a_scale, the product and the sum.
+    epilogue = (4.0 if q8 else 3.0) * B * workloads.VOCAB * (workloads.HIDDEN // 32)
+    alg = workloads.lmhead_algorithmic_bytes(B, w["hist_len"], q8=q8)
     return {"rows": B, "ms_per_step": round(wall / steps * 1e3, 4),
             "launch_ms": round(step_ms, 4),
             "rows_per_s": round(B / (wall / steps), 1),
@@ -321,9 +326,12 @@ def time_lmhead(smp, steps: int, warmup: int) -> dict:
             "hbm_gbs": round(alg / (step_ms / 1e3) / 1e9, 1),
             "hbm_frac": round(alg / (step_ms / 1e3) / 1e9 / PEAK_HBM_GBS, 4),
             "parity": parity,
-            "workload": "B=256 hidden N(0,1) x 896, Q4_0 head 151936x896 (fp16 scales "
-                        "U(0.001,0.02)), histories U[16,1024] Zipf; logits bit-exact to the "
-                        "reference Q4 head"}
+            "workload": ("B=256 hidden N(0,1) x 896, Q8_0 head 151936x896 (fp16 scales "
+                         "U(0.0005,0.004), int8 weights), histories U[16,1024] Zipf; logits "
+                         "bit-exact to the reference Q8 head" if q8 else
+                         "B=256 hidden N(0,1) x 896, Q4_0 head 151936x896 (fp16 scales "
+                         "U(0.001,0.02)), histories U[16,1024] Zipf; logits bit-exact to the "
+                         "reference Q4 head")}
 
 
 ADVERSARIAL = ("flat", "ties", "dominant", "half")
@@ -425,10 +433,12 @@ def main() -> int:
     adversarial = None
     if not args.no_adversarial:
         adversarial = time_adversarial(smp, min(args.steps, 50), args.warmup, threads)
-    lmhead = None
+    lmhead = lmhead_q8 = None
     if not args.no_lmhead:
         log("timing the fused Q4_0 LM head + sampler (B=256)")
         lmhead = time_lmhead(smp, min(args.steps, 50), args.warmup)
+        log("timing the fused Q8_0 LM head + sampler (B=256)")
+        lmhead_q8 = time_lmhead(smp, min(args.steps, 50), args.warmup, q8=True)
     host_buffers = None
     if not args.no_host_buffers and 1 in work and 4096 in work:
         log("timing with the inputs in host memory (PCIe included)")
@@ -491,6 +501,7 @@ def main() -> int:
         "by_batch": by_batch,
         "adversarial_B1024": adversarial,
         "lmhead_fused": lmhead,
+        "lmhead_q8_fused": lmhead_q8,
         "host_buffers": host_buffers,
         "roofline": roof,
         "cpu_baseline": cpu,

@@ -304,8 +304,9 @@ __global__ __launch_bounds__(kBlockThreads) void lm_prep_kernel(LmParams p) {
 // packed weights as they are, starts the accumulator at zero and follows
 // inference_q8_matvec_rows_prepared (fp32_sse2.rs:1251-1280):
 // add(total, mul(f32(dot), mul(ws, a_scale))), four VALU ops per value.  (The
-// scales are both fp16 values, so ws * a_scale is exact, but the conversion
-// cannot be folded into an FMA as above: M * ws * a_scale may need 26 bits.)
+// scales are both fp16 values, so ws * a_scale is exact, with at most 22
+// significant bits.  Folding the conversion into an FMA as above would work,
+// but it needs -M * ws * a_scale per value: one op either way.)
 template <bool kQ8>
 __global__ __launch_bounds__(kGemmThreads) void lm_gemm_kernel(LmParams p) {
   // Dynamic LDS: the activation scales / 16 of every block for the group's
