@@ -466,8 +466,34 @@ __global__ __launch_bounds__(kGemmThreads) void lm_gemm_kernel(LmParams p) {
     }
     if (blocks & 1u) run(last, even, odd_tag);
   };
+  // The Q8_0 head reads twice the weight bytes per block: its loads run two
+  // blocks ahead (three operand sets in rotation, the same clamped loads).
+  auto gemm_ahead2 = [&]() {
+    const uint32_t last = blocks - 1u;
+    Operands s0, s1, s2;
+    load(0, s0);
+    load(min(1u, last), s1);
+    uint32_t b = 0;
+#pragma unroll 1
+    for (; b + 2u < blocks; b += 3) {
+      load(min(b + 2u, last), s2);
+      __builtin_amdgcn_sched_barrier(0);
+      run(b, s0, std::false_type{});
+      __builtin_amdgcn_sched_barrier(0);
+      load(min(b + 3u, last), s0);
+      __builtin_amdgcn_sched_barrier(0);
+      run(b + 1u, s1, std::false_type{});
+      __builtin_amdgcn_sched_barrier(0);
+      load(min(b + 4u, last), s1);
+      __builtin_amdgcn_sched_barrier(0);
+      run(b + 2u, s2, std::false_type{});
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (b < blocks) run(b, s0, std::false_type{});
+    if (b + 1u < blocks) run(b + 1u, s1, std::false_type{});
+  };
   if constexpr (kQ8) {
-    gemm(std::false_type{});
+    gemm_ahead2();
   } else if (odd_tile) {
     gemm(std::true_type{});
   } else {
