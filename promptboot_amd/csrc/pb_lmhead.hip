@@ -54,6 +54,10 @@ constexpr uint32_t kTileIds = 64;        // vocabulary ids per tile and per work
 constexpr uint32_t kRowsPerWave = 32;   // two 16-row MFMA row tiles per wave in the head
 constexpr uint32_t kGemmThreads = 512;  // eight waves
 constexpr uint32_t kRowsPerGroup = 256;
+// Batches up to this size take lm_gemm_narrow_kernel (measured per step, Q4_0 /
+// Q8_0: B = 64 74.8 / 73.7 us against 92.0 / 98.1 with the wide kernel; B = 128
+// 119.2 / 121.9 against 103.6 / 108.6).
+constexpr uint32_t kNarrowRows = 64;
 constexpr uint32_t kWordsPerRow = kVocab / 32;
 constexpr uint32_t kTilesPerRow = kVocab / kTileIds;  // 2,374
 constexpr uint32_t kCandCap = 800;       // >= 20 lanes x 38 tile keys
@@ -274,6 +278,94 @@ __global__ __launch_bounds__(kBlockThreads) void lm_prep_kernel(LmParams p) {
   if (tid == 0) {
     p.meta[row * 2 + 0] = kNone;  // first non-finite logit, lowered by the GEMM
     p.meta[row * 2 + 1] = bad;
+  }
+}
+
+// ---- a wave's results for one 64-id tile ----
+// total[rt][c][i] is row first_row + 16 rt + i, id 64 tile + 4n + c, where
+// first_row is the lane's row of step 0 (lanes 16q .. 16q+15 hold rows 4q + i
+// of each row tile, four consecutive ids per lane).  hb_all holds four
+// history bits per step s = 4 rt + i.  Writes the raw logits, lowers each
+// row's first non-finite index, and writes per row the order word of the
+// tile's largest penalised value.  The steps run in passes (stores and raw
+// maxima, then the penalty, then the row maxima) so that the DPP chains
+// interleave; the penalty sits behind one wave-uniform branch, since a wave's
+// rows rarely hold a history id in a 64-id tile.
+template <int kRT>
+__device__ __forceinline__ void write_tile(const LmParams& p, const float (&total)[kRT][4][4],
+                                           uint32_t hb_all, uint32_t first_row, uint32_t tile,
+                                           uint32_t n) {
+  constexpr int kSteps = 4 * kRT;
+  const uint32_t v0 = tile * kTileIds;
+  float probe = 0.0f;
+  float m[kSteps];
+  const size_t ld = p.logits_ld;
+  uint32_t* lbase = p.logits + (size_t)first_row * ld + v0 + 4u * n;
+#pragma unroll
+  for (int s = 0; s < kSteps; ++s) {
+    const int rt = s >> 2, i = s & 3;
+    const float y[4] = {total[rt][0][i], total[rt][1][i], total[rt][2][i], total[rt][3][i]};
+    if (first_row + 16u * (uint32_t)rt + (uint32_t)i < p.rows)
+      *reinterpret_cast<v4f*>(lbase + (size_t)(16 * rt + i) * ld) = v4f{y[0], y[1], y[2], y[3]};
+#pragma unroll
+    for (int c = 0; c < 4; ++c) probe = __builtin_fmaf(y[c], 0.0f, probe);
+    m[s] = fmaxf(fmaxf(y[0], y[1]), fmaxf(y[2], y[3]));
+  }
+  // The penalty is monotone (x <= y gives pen(x) <= pen(y)), so the largest
+  // penalised history value is the penalty of the largest history value: one
+  // penalty per lane and step.  NaN is the identity of fmaxf, so a side with
+  // no element stays NaN and drops out, and pen(NaN) is NaN.  (A lane whose
+  // four values are all NaN may give another NaN than the per-element form;
+  // such a row is an error row, whose tile maxima are not used.)
+  if (__ballot(hb_all != 0u)) {
+    const float kNaN = __builtin_nanf("");
+#pragma unroll
+    for (int s = 0; s < kSteps; ++s) {
+      const int rt = s >> 2, i = s & 3;
+      const uint32_t hb = (hb_all >> (4 * s)) & 0xfu;
+      if (hb != 0u) {
+        float h[4], u[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const bool hit = ((hb >> c) & 1u) != 0u;
+          h[c] = hit ? total[rt][c][i] : kNaN;
+          u[c] = hit ? kNaN : total[rt][c][i];
+        }
+        const float mh = fmaxf(fmaxf(h[0], h[1]), fmaxf(h[2], h[3]));
+        const float mu = fmaxf(fmaxf(u[0], u[1]), fmaxf(u[2], u[3]));
+        m[s] = fmaxf(mu, f_of(penalize_bits(b_of(mh))));
+      }
+    }
+  }
+  // order word of each row's largest value in the tile (ord_of: adding +0
+  // turns -0 into +0, then negative values are inverted)
+  uint32_t o[kSteps];
+#pragma unroll
+  for (int s = 0; s < kSteps; ++s) {
+    o[s] = b_of(m[s] + 0.0f);
+    o[s] ^= (uint32_t)((int32_t)o[s] >> 31) | 0x80000000u;
+  }
+#pragma unroll
+  for (int s = 0; s < kSteps; ++s) o[s] = row16_max_u32(o[s]);
+  if (n == 0u) {
+#pragma unroll
+    for (int s = 0; s < kSteps; ++s) {
+      const uint32_t row = first_row + 16u * (uint32_t)(s >> 2) + (uint32_t)(s & 3);
+      if (row < p.rows) p.tilemax[(size_t)row * kTilesPerRow + tile] = o[s];
+    }
+  }
+  if (__ballot(probe != probe)) {
+    // a non-finite raw logit in this wave's rows: lower each row's first index
+#pragma unroll
+    for (int s = 0; s < kSteps; ++s) {
+      const int rt = s >> 2, i = s & 3;
+      const uint32_t row = first_row + 16u * (uint32_t)rt + (uint32_t)i;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        if (row < p.rows && (b_of(total[rt][c][i]) & 0x7f800000u) == 0x7f800000u)
+          atomicMin(&p.meta[row * 2], v0 + 4u * n + (uint32_t)c);
+      }
+    }
   }
 }
 
@@ -500,93 +592,183 @@ __global__ __launch_bounds__(kGemmThreads) void lm_gemm_kernel(LmParams p) {
     gemm(std::false_type{});
   }
 
-  // Logits, non-finite probe, history penalty and, per row, the order word of
-  // the tile's largest penalised value.  Lanes 16q .. 16q+15 hold the 64 ids
-  // of rows 4q + i of each row tile, four consecutive ids per lane.  Step
-  // s = 4 rt + i covers rows lrow0 + 16 rt + 4q + i.  The steps run in passes
-  // (stores and raw maxima, then the penalty, then the row maxima) so that the
-  // eight DPP chains interleave; the penalty sits behind one wave-uniform
-  // branch, since a wave's 32 rows rarely hold a history id in a 64-id tile.
-  // Bitmap words of rows past p.rows are zero.
-  uint32_t hb_all = 0;  // four history bits per step
+  // history bits of the lane's four ids for each step s = 4 rt + i (row
+  // lrow0 + 16 rt + 4q + i); bitmap words of rows past p.rows are zero
+  uint32_t hb_all = 0;
 #pragma unroll
   for (int s = 0; s < 8; ++s) {
     const uint32_t lr = lrow0 + 16u * (uint32_t)(s >> 2) + 4u * q + (uint32_t)(s & 3);
     hb_all |= ((hist_words[lr][n >> 3] >> (4u * (n & 7u))) & 0xfu) << (4 * s);
   }
-  float probe = 0.0f;
-  float m[8];
-  const size_t ld = p.logits_ld;
-  uint32_t* lbase = p.logits + (size_t)(group0 + lrow0 + 4u * q) * ld + v0 + 4u * n;
-  const uint32_t first_row = group0 + lrow0 + 4u * q;  // row of step 0 in this lane
+  write_tile<2>(p, total, hb_all, group0 + lrow0 + 4u * q, tile, n);
+}
+
+// ---- the head for narrow batches (up to 64 rows) ----
+// The wide kernel stages the scales of 256 rows in LDS and gives each wave
+// 32 rows of one 64-id tile; with few rows most of that work is padding.
+// Here one wave takes one 64-id tile and 16 kRT rows (one MFMA row tile up
+// to 32 rows, two above), four waves per workgroup over consecutive tiles,
+// the grid's y over the row groups.  Each block's weight and activation scales are loaded with
+// its operands (four fp16 weight scales and 4 kRT activation scales per
+// lane), and the loads run kSets - 1 blocks ahead in rotating operand sets:
+// with one wave per tile, the memory in flight per wave is what keeps the
+// weights streaming.  The epilogue is the wide kernel's, for both formats; a
+// block whose four weight scales in some lane include an infinite or NaN one
+// takes the subtract-then-multiply form of the Q4_0 epilogue for the whole
+// wave (a wave-uniform branch).
+template <bool kQ8, int kRT, int kSets>
+__global__ __launch_bounds__(256) void lm_gemm_narrow_kernel(LmParams p) {
+  const uint32_t lane = threadIdx.x & 63u;
+  const uint32_t tile = blockIdx.x * 4u + (threadIdx.x >> 6);
+  if (tile >= kTilesPerRow) return;  // whole wave, no barrier follows
+  const uint32_t n = lane & 15u;
+  const uint32_t q = lane >> 4;
+  const uint32_t row0 = blockIdx.y * (16u * kRT);  // first row of the wave's group
+  const uint32_t v0 = tile * kTileIds;
+  const uint32_t blocks = p.cols / 32u;
+  const uint32_t last = blocks - 1u;
+  constexpr uint32_t kWords = kQ8 ? 2u : 1u;  // uint4 of packed weights per lane and block
+  constexpr uint32_t kTile = kQ8 ? kTileBytesQ8 : kTileBytes;
+
+  // history words of the lane's rows, requested before the loop
+  constexpr int kSteps = 4 * kRT;
+  uint32_t hw[kSteps];
 #pragma unroll
-  for (int s = 0; s < 8; ++s) {
-    const int rt = s >> 2, i = s & 3;
-    const float y[4] = {total[rt][0][i], total[rt][1][i], total[rt][2][i], total[rt][3][i]};
-    if (first_row + 16u * (uint32_t)rt + (uint32_t)i < p.rows)
-      *reinterpret_cast<v4f*>(lbase + (size_t)(16 * rt + i) * ld) = v4f{y[0], y[1], y[2], y[3]};
-#pragma unroll
-    for (int c = 0; c < 4; ++c) probe = __builtin_fmaf(y[c], 0.0f, probe);
-    m[s] = fmaxf(fmaxf(y[0], y[1]), fmaxf(y[2], y[3]));
+  for (int s = 0; s < kSteps; ++s) {
+    const uint32_t row = row0 + 16u * (uint32_t)(s >> 2) + 4u * q + (uint32_t)(s & 3);
+    hw[s] = row < p.rows ? p.bitmap[(size_t)row * kWordsPerRow + (v0 >> 5) + (n >> 3)] : 0u;
   }
-  // The penalty is monotone (x <= y gives pen(x) <= pen(y)), so the largest
-  // penalised history value is the penalty of the largest history value: one
-  // penalty per lane and step.  NaN is the identity of fmaxf, so a side with
-  // no element stays NaN and drops out, and pen(NaN) is NaN.  (A lane whose
-  // four values are all NaN may give another NaN than the per-element form;
-  // such a row is an error row, whose tile maxima are not used.)
-  if (__ballot(hb_all != 0u)) {
-    const float kNaN = __builtin_nanf("");
+
+  const uint8_t* a_base = reinterpret_cast<const uint8_t*>(p.act_q) + ((size_t)row0 + n) * 32 + 8u * q;
+  const size_t a_stride = (size_t)p.rows_pad * 32;  // bytes per block
+  const v4u* w_base = reinterpret_cast<const v4u*>(p.weights + (size_t)tile * kTile) + kWords * lane;
+  const size_t w_stride = (size_t)kTilesPerRow * (kTile / 16);  // uint4 per block
+  const uint16_t* ws_base = reinterpret_cast<const uint16_t*>(
+                                p.weights + (size_t)blocks * kVocab * (kQ8 ? 32 : 16)) +
+                            v0 + 4u * n;
+  const float* as_base = p.act_s + row0 + 4u * q;
+
+  struct Operands {
+    uint64_t a[kRT];
+    v4u raw[kWords];
+    uint64_t ws;    // four fp16 weight scales, ids 4n .. 4n+3
+    v4f as[kRT];    // activation scales / 16 of rows 16 rt + 4q .. +3
+  };
+  auto load = [&](uint32_t b, Operands& o) {
+    const uint8_t* ab = a_base + (size_t)b * a_stride;
 #pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      const int rt = s >> 2, i = s & 3;
-      const uint32_t hb = (hb_all >> (4 * s)) & 0xfu;
-      if (hb != 0u) {
-        float h[4], u[4];
+    for (int rt = 0; rt < kRT; ++rt)
+      o.a[rt] = *reinterpret_cast<const uint64_t*>(ab + 16u * 32u * (uint32_t)rt);
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const bool hit = ((hb >> c) & 1u) != 0u;
-          h[c] = hit ? total[rt][c][i] : kNaN;
-          u[c] = hit ? kNaN : total[rt][c][i];
+    for (uint32_t k = 0; k < kWords; ++k) o.raw[k] = w_base[(size_t)b * w_stride + k];
+    o.ws = *reinterpret_cast<const uint64_t*>(ws_base + (size_t)b * kVocab);
+#pragma unroll
+    for (int rt = 0; rt < kRT; ++rt)
+      o.as[rt] = *reinterpret_cast<const v4f*>(as_base + (size_t)b * p.rows_pad + 16u * rt);
+  };
+
+  float total[kRT][4][4];
+#pragma unroll
+  for (int rt = 0; rt < kRT; ++rt)
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) total[rt][c][i] = 0.0f;
+  const v4i magic = {(int)kMagicBits, (int)kMagicBits, (int)kMagicBits, (int)kMagicBits};
+  const v4i zero = {0, 0, 0, 0};
+
+  auto run = [&](const Operands& o) {
+    float wsv[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      wsv[c] = __half2float(__ushort_as_half((unsigned short)(o.ws >> (16 * c))));
+    v4i d[kRT][4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      uint64_t w;
+      if constexpr (kQ8) {
+        const uint32_t raw[8] = {o.raw[0].x, o.raw[0].y, o.raw[0].z, o.raw[0].w,
+                                 o.raw[kWords - 1].x, o.raw[kWords - 1].y, o.raw[kWords - 1].z,
+                                 o.raw[kWords - 1].w};
+        w = (uint64_t)raw[2 * c] | ((uint64_t)raw[2 * c + 1] << 32);
+      } else {
+        const uint32_t raw[4] = {o.raw[0].x, o.raw[0].y, o.raw[0].z, o.raw[0].w};
+        w = (uint64_t)((raw[c] << 4) & 0xf0f0f0f0u) | ((uint64_t)(raw[c] & 0xf0f0f0f0u) << 32);
+      }
+#pragma unroll
+      for (int rt = 0; rt < kRT; ++rt)
+        d[rt][c] = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)o.a[rt], (long)w,
+                                                         kQ8 ? zero : magic, 0, 0, 0);
+    }
+    if constexpr (kQ8) {
+#pragma unroll
+      for (int rt = 0; rt < kRT; ++rt) {
+        const float asv[4] = {o.as[rt].x * 16.0f, o.as[rt].y * 16.0f, o.as[rt].z * 16.0f,
+                              o.as[rt].w * 16.0f};
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float scale = wsv[c] * asv[i];
+            total[rt][c][i] = total[rt][c][i] + (float)d[rt][c][i] * scale;
+          }
+      }
+    } else {
+      // x * 0 is NaN exactly for an infinite or NaN x
+      float odd_probe = 0.0f;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) odd_probe = __builtin_fmaf(wsv[c], 0.0f, odd_probe);
+      if (__ballot(odd_probe != odd_probe)) {
+#pragma unroll
+        for (int rt = 0; rt < kRT; ++rt) {
+          const float asv[4] = {o.as[rt].x, o.as[rt].y, o.as[rt].z, o.as[rt].w};
+#pragma unroll
+          for (int c = 0; c < 4; ++c)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const float y = (__int_as_float(d[rt][c][i]) - kMagic) * wsv[c];
+              total[rt][c][i] = total[rt][c][i] + y * asv[i];
+            }
         }
-        const float mh = fmaxf(fmaxf(h[0], h[1]), fmaxf(h[2], h[3]));
-        const float mu = fmaxf(fmaxf(u[0], u[1]), fmaxf(u[2], u[3]));
-        m[s] = fmaxf(mu, f_of(penalize_bits(b_of(mh))));
+      } else {
+        float wnv[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) wnv[c] = wsv[c] * -kMagic;
+#pragma unroll
+        for (int rt = 0; rt < kRT; ++rt) {
+          const float asv[4] = {o.as[rt].x, o.as[rt].y, o.as[rt].z, o.as[rt].w};
+#pragma unroll
+          for (int c = 0; c < 4; ++c)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const float y = __builtin_fmaf(__int_as_float(d[rt][c][i]), wsv[c], wnv[c]);
+              total[rt][c][i] = total[rt][c][i] + y * asv[i];
+            }
+        }
       }
     }
-  }
-  // order word of each row's largest value in the tile (ord_of: adding +0
-  // turns -0 into +0, then negative values are inverted)
-  uint32_t o[8];
+  };
+
+  // Block t sits in set t % kSets.  Loads are unconditional (clamped to the
+  // last block); only the compute of a final partial round is guarded.
+  Operands ops[kSets];
 #pragma unroll
-  for (int s = 0; s < 8; ++s) {
-    o[s] = b_of(m[s] + 0.0f);
-    o[s] ^= (uint32_t)((int32_t)o[s] >> 31) | 0x80000000u;
-  }
+  for (int k = 0; k < kSets - 1; ++k) load(min((uint32_t)k, last), ops[k]);
+#pragma unroll 1
+  for (uint32_t b = 0; b < blocks; b += kSets) {
 #pragma unroll
-  for (int s = 0; s < 8; ++s) o[s] = row16_max_u32(o[s]);
-  if (n == 0u) {
-#pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      const uint32_t row = first_row + 16u * (uint32_t)(s >> 2) + (uint32_t)(s & 3);
-      if (row < p.rows) p.tilemax[(size_t)row * kTilesPerRow + tile] = o[s];
+    for (int k = 0; k < kSets; ++k) {
+      load(min(b + (uint32_t)(k + kSets - 1), last), ops[(k + kSets - 1) % kSets]);
+      __builtin_amdgcn_sched_barrier(0);
+      if (b + (uint32_t)k < blocks) run(ops[k]);
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
-  if (__ballot(probe != probe)) {
-    // a non-finite raw logit in this wave's rows: lower each row's first index
+
+  uint32_t hb_all = 0;
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint32_t row = group0 + lrow0 + 16u * rt + 4u * q + (uint32_t)i;
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          if (row < p.rows && (b_of(total[rt][c][i]) & 0x7f800000u) == 0x7f800000u)
-            atomicMin(&p.meta[row * 2], v0 + 4u * n + (uint32_t)c);
-        }
-      }
-    }
-  }
+  for (int s = 0; s < kSteps; ++s) hb_all |= ((hw[s] >> (4u * (n & 7u))) & 0xfu) << (4 * s);
+  write_tile<kRT>(p, total, hb_all, row0 + 4u * q, tile, n);
 }
 
 // Collects into `cand` every key of this lane (keys[0..N)) that reaches thr.
@@ -755,13 +937,30 @@ size_t gemm_lds_bytes(uint32_t cols) {
 
 hipError_t launch_lm_sample(const LmParams& p, const RowParams& rp, hipStream_t stream) {
   hipLaunchKernelGGL(lm_prep_kernel, dim3(p.rows_pad), dim3(kBlockThreads), 0, stream, p);
-  const dim3 gemm_grid(kTilesPerRow, (p.rows_pad + kRowsPerGroup - 1) / kRowsPerGroup);
-  if (p.q8)
-    hipLaunchKernelGGL(lm_gemm_kernel<true>, gemm_grid, dim3(kGemmThreads), gemm_lds_bytes(p.cols),
-                       stream, p);
-  else
-    hipLaunchKernelGGL(lm_gemm_kernel<false>, gemm_grid, dim3(kGemmThreads), gemm_lds_bytes(p.cols),
-                       stream, p);
+  if (p.rows <= kNarrowRows) {
+    // Measured (Q4_0 step, us): one row tile with loads three blocks ahead
+    // gives B = 1 37.0, B = 8 39.7, B = 32 51.2 (five ahead: 38.5, 41.0, 53.4;
+    // seven: 42.5, 44.8); two row tiles with one block ahead give B = 64 70.8
+    // (two ahead: 73.8; one tile: 75.3).
+    const uint32_t rt = p.rows <= 32u ? 1u : 2u;
+    const dim3 grid((kTilesPerRow + 3) / 4, (p.rows + 16u * rt - 1) / (16u * rt));
+    if (p.q8 && rt == 1)
+      hipLaunchKernelGGL((lm_gemm_narrow_kernel<true, 1, 4>), grid, dim3(256), 0, stream, p);
+    else if (p.q8)
+      hipLaunchKernelGGL((lm_gemm_narrow_kernel<true, 2, 2>), grid, dim3(256), 0, stream, p);
+    else if (rt == 1)
+      hipLaunchKernelGGL((lm_gemm_narrow_kernel<false, 1, 4>), grid, dim3(256), 0, stream, p);
+    else
+      hipLaunchKernelGGL((lm_gemm_narrow_kernel<false, 2, 2>), grid, dim3(256), 0, stream, p);
+  } else {
+    const dim3 gemm_grid(kTilesPerRow, (p.rows_pad + kRowsPerGroup - 1) / kRowsPerGroup);
+    if (p.q8)
+      hipLaunchKernelGGL(lm_gemm_kernel<true>, gemm_grid, dim3(kGemmThreads),
+                         gemm_lds_bytes(p.cols), stream, p);
+    else
+      hipLaunchKernelGGL(lm_gemm_kernel<false>, gemm_grid, dim3(kGemmThreads),
+                         gemm_lds_bytes(p.cols), stream, p);
+  }
   hipLaunchKernelGGL(lm_select_kernel, dim3((p.rows + kSelectWaves - 1) / kSelectWaves),
                      dim3(64 * kSelectWaves), 0, stream,
                      p, rp);

@@ -79,7 +79,9 @@ def oracle_head(w, hidden, rows):
     return logits, tok, det, err
 
 
-@pytest.mark.parametrize("rows", [5, 64, 300])
+# up to 64 rows the head runs lm_gemm_narrow_kernel (one 16-row tile per wave up
+# to 32 rows, two above), beyond that lm_gemm_kernel: both sides of each switch
+@pytest.mark.parametrize("rows", [5, 16, 17, 32, 33, 64, 65, 129, 300])
 def test_head_logits_and_draws_are_bit_exact(smp, head, rows):
     w, packed = head
     hidden = w["hidden"][:rows]
@@ -132,7 +134,8 @@ def _set_scales(q4, edits):
         q4[v, b, 1] = bits >> 8
 
 
-def test_special_weight_and_activation_scales(smp, head):
+@pytest.mark.parametrize("rows", [4, 160])
+def test_special_weight_and_activation_scales(smp, head, rows):
     """Edge scales through both epilogue forms of the head.  Finite scales
     (signed zeros, +-1, fp16 subnormals, +-65504) sit in tiles that take the
     fused multiply-add form; +-inf and NaN sit in tiles of their own, which
@@ -162,8 +165,9 @@ def test_special_weight_and_activation_scales(smp, head):
     hidden[2] = rng.standard_normal(workloads.HIDDEN)
     hidden[2, 64:96] = 0.0                                                # one all-zero block
     hidden[3] = rng.standard_normal(workloads.HIDDEN) * np.float32(1e7)    # amax / 127 -> inf
-    glog, _, _, _ = run_head(smp, packed, hidden, w["hist"][:4], w["hist_len"][:4],
-                             w["random_24"][:4])
+    hidden = np.tile(hidden, (rows // 4, 1))  # 160 rows: the wide kernel
+    glog, _, _, _ = run_head(smp, packed, hidden, w["hist"][:rows], w["hist_len"][:rows],
+                             w["random_24"][:rows])
     rlog = o.lmhead_logits(hidden, q4.reshape(-1), V, workloads.HIDDEN, threads=16)
     gnan = np.isnan(glog.view(np.float32))
     rnan = np.isnan(rlog.view(np.float32))
@@ -247,12 +251,14 @@ def test_every_logit_negative(smp):
     assert_rows_equal(gtok, gdet, gerr, rtok, rdet, rerr)
 
 
-def test_widest_hidden_state(smp):
-    """cols = 2048, the widest the head accepts (its per-block scales then take
-    96 KB of the workgroup's LDS): logits bit-exact for three rows."""
+@pytest.mark.parametrize("rows", [3, 140])
+def test_widest_hidden_state(smp, rows):
+    """cols = 2048, the widest the head accepts: logits bit-exact through the
+    narrow kernel (3 rows) and the wide one (140 rows, whose per-block scales
+    then take 96 KB of the workgroup's LDS)."""
     import torch
 
-    cols, rows = 2048, 3
+    cols = 2048
     rng = np.random.default_rng(11)
     blocks = cols // 32
     q4 = rng.integers(0, 256, (V, blocks, 18), dtype=np.uint8)

@@ -74,7 +74,7 @@ def test_the_references_dots_row_on_the_device(smp):
     assert (glog == oracle_logits(hidden, q8.reshape(-1), cols)).all()
 
 
-@pytest.mark.parametrize("rows", [5, 64, 300])
+@pytest.mark.parametrize("rows", [5, 16, 17, 32, 33, 64, 65, 129, 300])
 def test_q8_head_logits_and_draws_are_bit_exact(smp, head, rows):
     w, q8, packed = head
     hidden = w["hidden"][:rows]
@@ -88,7 +88,8 @@ def test_q8_head_logits_and_draws_are_bit_exact(smp, head, rows):
     assert_rows_equal(gtok, gdet, gerr, rtok, rdet, rerr)
 
 
-def test_int8_extremes_and_special_scales(smp, head):
+@pytest.mark.parametrize("rows", [5, 160])
+def test_int8_extremes_and_special_scales(smp, head, rows):
     """Weights of -128 and 127 against saturated activations (the largest
     dots, |dot| up to 2^19), and weight scales of signed zero, +-1, fp16
     subnormals, +-65504, +-inf and NaN; hidden rows with normal, fp16-subnormal,
@@ -113,8 +114,9 @@ def test_int8_extremes_and_special_scales(smp, head):
     hidden[2, 64:96] = 0.0
     hidden[3] = rng.standard_normal(workloads.HIDDEN) * np.float32(1e7)
     hidden[4] = np.where(np.arange(workloads.HIDDEN) % 2 == 0, -3.0, 3.0)  # |q| = 127 everywhere
-    glog, _, _, _ = run_head(smp, packed, hidden, w["hist"][:5], w["hist_len"][:5],
-                             w["random_24"][:5], q8=True)
+    hidden = np.tile(hidden, (rows // 5, 1))  # 160 rows: the wide kernel
+    glog, _, _, _ = run_head(smp, packed, hidden, w["hist"][:rows], w["hist_len"][:rows],
+                             w["random_24"][:rows], q8=True)
     rlog = oracle_logits(hidden, h.reshape(-1))
     gnan = np.isnan(glog.view(np.float32))
     rnan = np.isnan(rlog.view(np.float32))
