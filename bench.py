@@ -23,6 +23,7 @@ The printed JSON line also carries:
                      sub-cases, each timed and checked against the oracle;
   lmhead_fused       the fused Q4_0 LM head + sampler step (B=256);
   lmhead_q8_fused    the same with the Q8_0 head (the model's output head);
+  lmhead_B1          one conversation's step (B=1) through each head;
   host_buffers       PCIe-inclusive rates: the single-row drop-in on host
                      buffers, and the B=4096 batch copied from pinned host
                      memory every step (not the headline value).
@@ -239,15 +240,15 @@ MFMA_INT8_PEAK_TOPS = 5000.0     # dense int8 MFMA, MI355X
 VALU_LANE_OPS_PEAK = 256 * 4 * 16 * 2.4e9  # 32-bit VALU lane-ops/s, MI355X
 
 
-def time_lmhead(smp, steps: int, warmup: int, q8: bool = False) -> dict:
-    """Fused Q4_0 (or, with q8, Q8_0) LM head + sampler, B=256 hidden states of
-    width 896."""
+def time_lmhead(smp, steps: int, warmup: int, q8: bool = False, rows: int = 256) -> dict:
+    """Fused Q4_0 (or, with q8, Q8_0) LM head + sampler, `rows` hidden states of
+    width 896 (256 by default; 1 is one conversation's decode step)."""
     import torch
 
     from promptboot_amd import sampler as s
     from promptboot_amd import workloads
 
-    w = workloads.make_lmhead(rows=256)
+    w = workloads.make_lmhead(rows=rows)
     head = workloads.make_q8_head() if q8 else w["q4"]
     dev = torch.device("cuda:0")
 
@@ -269,7 +270,7 @@ def time_lmhead(smp, steps: int, warmup: int, q8: bool = False) -> dict:
     smp.lmhead_sample(packed, hidden, r24, hist, hl, token=token, detail=det, logits=logits,
                       stream=stream, q8=q8)
     torch.cuda.synchronize()
-    n_check = PARITY_LMHEAD_ROWS
+    n_check = min(PARITY_LMHEAD_ROWS, B)
     g_logits = logits[:n_check].cpu().numpy().view(np.uint32)
     g_tokens = token.cpu().numpy().view(np.uint32)[:n_check].copy()
     g_flags = det.cpu().numpy().view(s.DETAIL_DTYPE).reshape(B)["flags"][:n_check].copy()
@@ -326,10 +327,10 @@ def time_lmhead(smp, steps: int, warmup: int, q8: bool = False) -> dict:
             "hbm_gbs": round(alg / (step_ms / 1e3) / 1e9, 1),
             "hbm_frac": round(alg / (step_ms / 1e3) / 1e9 / PEAK_HBM_GBS, 4),
             "parity": parity,
-            "workload": ("B=256 hidden N(0,1) x 896, Q8_0 head 151936x896 (fp16 scales "
+            "workload": (f"B={B} hidden N(0,1) x 896, Q8_0 head 151936x896 (fp16 scales "
                          "U(0.0005,0.004), int8 weights), histories U[16,1024] Zipf; logits "
                          "bit-exact to the reference Q8 head" if q8 else
-                         "B=256 hidden N(0,1) x 896, Q4_0 head 151936x896 (fp16 scales "
+                         f"B={B} hidden N(0,1) x 896, Q4_0 head 151936x896 (fp16 scales "
                          "U(0.001,0.02)), histories U[16,1024] Zipf; logits bit-exact to the "
                          "reference Q4 head")}
 
@@ -433,12 +434,16 @@ def main() -> int:
     adversarial = None
     if not args.no_adversarial:
         adversarial = time_adversarial(smp, min(args.steps, 50), args.warmup, threads)
-    lmhead = lmhead_q8 = None
+    lmhead = lmhead_q8 = lmhead_b1 = None
     if not args.no_lmhead:
         log("timing the fused Q4_0 LM head + sampler (B=256)")
         lmhead = time_lmhead(smp, min(args.steps, 50), args.warmup)
         log("timing the fused Q8_0 LM head + sampler (B=256)")
         lmhead_q8 = time_lmhead(smp, min(args.steps, 50), args.warmup, q8=True)
+        log("timing one conversation's step through each head (B=1)")
+        lmhead_b1 = {"q4_0": time_lmhead(smp, min(args.steps, 100), args.warmup, rows=1),
+                     "q8_0": time_lmhead(smp, min(args.steps, 100), args.warmup, q8=True,
+                                         rows=1)}
     host_buffers = None
     if not args.no_host_buffers and 1 in work and 4096 in work:
         log("timing with the inputs in host memory (PCIe included)")
@@ -502,6 +507,7 @@ def main() -> int:
         "adversarial_B1024": adversarial,
         "lmhead_fused": lmhead,
         "lmhead_q8_fused": lmhead_q8,
+        "lmhead_B1": lmhead_b1,
         "host_buffers": host_buffers,
         "roofline": roof,
         "cpu_baseline": cpu,

@@ -202,8 +202,8 @@ uint32_t pb_sample_batch_inplace(pb_context *ctx, uint32_t *d_logits, size_t voc
  * The logits are bit-identical to the reference's Q4 head (int8 MFMA for the
  * exact block dots, the reference's per-block binary32 epilogue in order). */
 
-/* Bytes of the device layout of a Q4_0 head (equal to the source size:
- * rows * cols / 32 blocks of 18 bytes). */
+/* Bytes of the device layout of a Q4_0 head: the source size (rows * cols /
+ * 32 blocks of 18 bytes) plus one flag word per 64-id tile. */
 size_t pb_lmhead_packed_bytes(size_t vocab, size_t cols);
 
 /* Repacks a Q4_0 matrix in promptboot's layout (vocab rows of cols/32 blocks

@@ -380,7 +380,11 @@ uint32_t pb_sample_batch_inplace(pb_context* ctx, uint32_t* d_logits, size_t voc
 
 // ---- fused Q4_0 LM head + sampler ----
 
-size_t pb_lmhead_packed_bytes(size_t vocab, size_t cols) { return vocab * (cols / 32) * 18; }
+// The Q4_0 layout ends with one flag word per 64-id tile (a tile with an
+// infinite or NaN weight scale).
+size_t pb_lmhead_packed_bytes(size_t vocab, size_t cols) {
+  return vocab * (cols / 32) * 18 + vocab / 64 * 4;
+}
 
 size_t pb_lmhead_q8_packed_bytes(size_t vocab, size_t cols) { return vocab * (cols / 32) * 34; }
 
@@ -413,8 +417,10 @@ uint32_t pb_lmhead_pack_q4_0(const uint8_t* d_q4, size_t vocab, size_t cols, uin
                              void* stream, pb_inference_error* err) {
   const uint32_t st = check_pack_args(vocab, cols, d_packed, err);
   if (st != PB_OK) return st;
-  hipError_t e = pb::launch_lm_pack(d_q4, d_packed, (uint32_t)vocab, (uint32_t)(cols / 32),
-                                    static_cast<hipStream_t>(stream));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t e = hipMemsetAsync(d_packed + vocab * (cols / 32) * 18, 0, vocab / 64 * 4, s);
+  if (e == hipSuccess)
+    e = pb::launch_lm_pack(d_q4, d_packed, (uint32_t)vocab, (uint32_t)(cols / 32), s);
   return e == hipSuccess ? PB_OK : device_error(err, e);
 }
 

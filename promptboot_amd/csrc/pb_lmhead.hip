@@ -125,7 +125,8 @@ __device__ __forceinline__ uint32_t f32_bits_to_half(uint32_t bits) {
 // in:  vocab rows of `blocks` x 18 bytes (fp16 scale, 16 nibble bytes: byte j
 //      holds element j in the low and element 16 + j in the high nibble).
 // out: [blocks][vocab / 64 tiles][1 KB] nibbles, then [blocks][vocab] fp16
-//      scales.  In the kilobyte of (block b, tile t), lane l = 16 q + n of a
+//      scales, then one word per tile, non-zero when one of the tile's scales
+//      is infinite or NaN (cleared by the caller before the launch).  In the kilobyte of (block b, tile t), lane l = 16 q + n of a
 //      head wave reads the 16 bytes at 16 l: word c of them is bytes
 //      4q .. 4q+3 of id 64 t + 4 n + c, every nibble XOR 8.  vocab % 64 == 0.
 __global__ __launch_bounds__(kBlockThreads) void lm_pack_kernel(const uint8_t* __restrict__ in,
@@ -147,7 +148,13 @@ __global__ __launch_bounds__(kBlockThreads) void lm_pack_kernel(const uint8_t* _
     tile[(q * 16u + n) * 4u + c] = w ^ 0x88888888u;
   }
   uint16_t* scales = reinterpret_cast<uint16_t*>(out + (size_t)blocks * vocab * 16);
-  scales[(size_t)b * vocab + v] = (uint16_t)(src[0] | (src[1] << 8));
+  const uint16_t h = (uint16_t)(src[0] | (src[1] << 8));
+  scales[(size_t)b * vocab + v] = h;
+  // tiles with an infinite or NaN weight scale (the flags start at zero)
+  if ((h & 0x7c00u) == 0x7c00u) {
+    uint32_t* flags = reinterpret_cast<uint32_t*>(scales + (size_t)blocks * vocab);
+    atomicOr(&flags[t], 1u);
+  }
 }
 
 // ---- repack: promptboot's Q8_0 rows -> the head's tile layout ----
@@ -613,11 +620,15 @@ __global__ __launch_bounds__(kGemmThreads) void lm_gemm_kernel(LmParams p) {
 // lane), and the loads run kSets - 1 blocks ahead in rotating operand sets:
 // with one wave per tile, the memory in flight per wave is what keeps the
 // weights streaming.  The epilogue is the wide kernel's, for both formats; a
-// block whose four weight scales in some lane include an infinite or NaN one
-// takes the subtract-then-multiply form of the Q4_0 epilogue for the whole
-// wave (a wave-uniform branch).
-template <bool kQ8, int kRT, int kSets>
+// Q4_0 tile flagged at pack time for an infinite or NaN weight scale takes the
+// subtract-then-multiply form for all its blocks.  The loop body has no branch:
+// at a branch's join the compiler waits for every load in flight, which would
+// undo the loads issued ahead.  With at most four rows every real row is
+// result register i < kI of lanes 0 .. 15, so the epilogue of the other
+// registers (padding rows) is left out: kI = 1 for one conversation.
+template <bool kQ8, int kRT, int kSets, int kI>
 __global__ __launch_bounds__(256) void lm_gemm_narrow_kernel(LmParams p) {
+  static_assert(kI == 4 || kRT == 1, "partial rows only with one row tile");
   const uint32_t lane = threadIdx.x & 63u;
   const uint32_t tile = blockIdx.x * 4u + (threadIdx.x >> 6);
   if (tile >= kTilesPerRow) return;  // whole wave, no barrier follows
@@ -648,11 +659,15 @@ __global__ __launch_bounds__(256) void lm_gemm_narrow_kernel(LmParams p) {
                             v0 + 4u * n;
   const float* as_base = p.act_s + row0 + 4u * q;
 
+  // Only the kI activation scales a lane uses are loaded: a register of a
+  // wider load left unused would be taken for a temporary while the load is
+  // in flight, and writing it would wait for every load.
+  typedef float vIf __attribute__((ext_vector_type(kI)));
   struct Operands {
     uint64_t a[kRT];
     v4u raw[kWords];
     uint64_t ws;    // four fp16 weight scales, ids 4n .. 4n+3
-    v4f as[kRT];    // activation scales / 16 of rows 16 rt + 4q .. +3
+    vIf as[kRT];    // activation scales / 16 of rows 16 rt + 4q .. 4q + kI - 1
   };
   auto load = [&](uint32_t b, Operands& o) {
     const uint8_t* ab = a_base + (size_t)b * a_stride;
@@ -664,7 +679,7 @@ __global__ __launch_bounds__(256) void lm_gemm_narrow_kernel(LmParams p) {
     o.ws = *reinterpret_cast<const uint64_t*>(ws_base + (size_t)b * kVocab);
 #pragma unroll
     for (int rt = 0; rt < kRT; ++rt)
-      o.as[rt] = *reinterpret_cast<const v4f*>(as_base + (size_t)b * p.rows_pad + 16u * rt);
+      o.as[rt] = *reinterpret_cast<const vIf*>(as_base + (size_t)b * p.rows_pad + 16u * rt);
   };
 
   float total[kRT][4][4];
@@ -677,7 +692,8 @@ __global__ __launch_bounds__(256) void lm_gemm_narrow_kernel(LmParams p) {
   const v4i magic = {(int)kMagicBits, (int)kMagicBits, (int)kMagicBits, (int)kMagicBits};
   const v4i zero = {0, 0, 0, 0};
 
-  auto run = [&](const Operands& o) {
+  auto run = [&](const Operands& o, auto odd_tag) {
+    constexpr bool kOdd = decltype(odd_tag)::value;
     float wsv[4];
 #pragma unroll
     for (int c = 0; c < 4; ++c)
@@ -703,29 +719,28 @@ __global__ __launch_bounds__(256) void lm_gemm_narrow_kernel(LmParams p) {
     if constexpr (kQ8) {
 #pragma unroll
       for (int rt = 0; rt < kRT; ++rt) {
-        const float asv[4] = {o.as[rt].x * 16.0f, o.as[rt].y * 16.0f, o.as[rt].z * 16.0f,
-                              o.as[rt].w * 16.0f};
+        float asv[kI];
+#pragma unroll
+        for (int i = 0; i < kI; ++i) asv[i] = o.as[rt][i] * 16.0f;
 #pragma unroll
         for (int c = 0; c < 4; ++c)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
+          for (int i = 0; i < kI; ++i) {
             const float scale = wsv[c] * asv[i];
             total[rt][c][i] = total[rt][c][i] + (float)d[rt][c][i] * scale;
           }
       }
     } else {
-      // x * 0 is NaN exactly for an infinite or NaN x
-      float odd_probe = 0.0f;
-#pragma unroll
-      for (int c = 0; c < 4; ++c) odd_probe = __builtin_fmaf(wsv[c], 0.0f, odd_probe);
-      if (__ballot(odd_probe != odd_probe)) {
+      if constexpr (kOdd) {
 #pragma unroll
         for (int rt = 0; rt < kRT; ++rt) {
-          const float asv[4] = {o.as[rt].x, o.as[rt].y, o.as[rt].z, o.as[rt].w};
+          float asv[kI];
+#pragma unroll
+          for (int i = 0; i < kI; ++i) asv[i] = o.as[rt][i];
 #pragma unroll
           for (int c = 0; c < 4; ++c)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
+            for (int i = 0; i < kI; ++i) {
               const float y = (__int_as_float(d[rt][c][i]) - kMagic) * wsv[c];
               total[rt][c][i] = total[rt][c][i] + y * asv[i];
             }
@@ -736,11 +751,13 @@ __global__ __launch_bounds__(256) void lm_gemm_narrow_kernel(LmParams p) {
         for (int c = 0; c < 4; ++c) wnv[c] = wsv[c] * -kMagic;
 #pragma unroll
         for (int rt = 0; rt < kRT; ++rt) {
-          const float asv[4] = {o.as[rt].x, o.as[rt].y, o.as[rt].z, o.as[rt].w};
+          float asv[kI];
+#pragma unroll
+          for (int i = 0; i < kI; ++i) asv[i] = o.as[rt][i];
 #pragma unroll
           for (int c = 0; c < 4; ++c)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
+            for (int i = 0; i < kI; ++i) {
               const float y = __builtin_fmaf(__int_as_float(d[rt][c][i]), wsv[c], wnv[c]);
               total[rt][c][i] = total[rt][c][i] + y * asv[i];
             }
@@ -750,18 +767,36 @@ __global__ __launch_bounds__(256) void lm_gemm_narrow_kernel(LmParams p) {
   };
 
   // Block t sits in set t % kSets.  Loads are unconditional (clamped to the
-  // last block); only the compute of a final partial round is guarded.
-  Operands ops[kSets];
+  // last block).  Whole rounds of kSets blocks run in the loop; the last
+  // blocks (fewer than kSets, already loaded) run after it.
+  auto gemm = [&](auto odd_tag) {
+    Operands ops[kSets];
 #pragma unroll
-  for (int k = 0; k < kSets - 1; ++k) load(min((uint32_t)k, last), ops[k]);
+    for (int k = 0; k < kSets - 1; ++k) load(min((uint32_t)k, last), ops[k]);
+    const uint32_t whole = blocks / kSets * kSets;
 #pragma unroll 1
-  for (uint32_t b = 0; b < blocks; b += kSets) {
+    for (uint32_t b = 0; b < whole; b += kSets) {
 #pragma unroll
-    for (int k = 0; k < kSets; ++k) {
-      load(min(b + (uint32_t)(k + kSets - 1), last), ops[(k + kSets - 1) % kSets]);
-      __builtin_amdgcn_sched_barrier(0);
-      if (b + (uint32_t)k < blocks) run(ops[k]);
-      __builtin_amdgcn_sched_barrier(0);
+      for (int k = 0; k < kSets; ++k) {
+        load(min(b + (uint32_t)(k + kSets - 1), last), ops[(k + kSets - 1) % kSets]);
+        __builtin_amdgcn_sched_barrier(0);
+        run(ops[k], odd_tag);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < kSets - 1; ++k)
+      if (whole + (uint32_t)k < blocks) run(ops[k], odd_tag);
+  };
+  if constexpr (kQ8) {
+    gemm(std::false_type{});
+  } else {
+    const uint32_t* flags =
+        reinterpret_cast<const uint32_t*>(p.weights + (size_t)blocks * kVocab * 18);
+    if (flags[tile] != 0u) {
+      gemm(std::true_type{});
+    } else {
+      gemm(std::false_type{});
     }
   }
 
@@ -944,14 +979,26 @@ hipError_t launch_lm_sample(const LmParams& p, const RowParams& rp, hipStream_t 
     // (two ahead: 73.8; one tile: 75.3).
     const uint32_t rt = p.rows <= 32u ? 1u : 2u;
     const dim3 grid((kTilesPerRow + 3) / 4, (p.rows + 16u * rt - 1) / (16u * rt));
-    if (p.q8 && rt == 1)
-      hipLaunchKernelGGL((lm_gemm_narrow_kernel<true, 1, 4>), grid, dim3(256), 0, stream, p);
-    else if (p.q8)
-      hipLaunchKernelGGL((lm_gemm_narrow_kernel<true, 2, 2>), grid, dim3(256), 0, stream, p);
-    else if (rt == 1)
-      hipLaunchKernelGGL((lm_gemm_narrow_kernel<false, 1, 4>), grid, dim3(256), 0, stream, p);
-    else
-      hipLaunchKernelGGL((lm_gemm_narrow_kernel<false, 2, 2>), grid, dim3(256), 0, stream, p);
+    const dim3 block(256);
+    if (p.q8) {
+      if (p.rows == 1)
+        hipLaunchKernelGGL((lm_gemm_narrow_kernel<true, 1, 4, 1>), grid, block, 0, stream, p);
+      else if (p.rows == 2)
+        hipLaunchKernelGGL((lm_gemm_narrow_kernel<true, 1, 4, 2>), grid, block, 0, stream, p);
+      else if (rt == 1)
+        hipLaunchKernelGGL((lm_gemm_narrow_kernel<true, 1, 4, 4>), grid, block, 0, stream, p);
+      else
+        hipLaunchKernelGGL((lm_gemm_narrow_kernel<true, 2, 2, 4>), grid, block, 0, stream, p);
+    } else {
+      if (p.rows == 1)
+        hipLaunchKernelGGL((lm_gemm_narrow_kernel<false, 1, 4, 1>), grid, block, 0, stream, p);
+      else if (p.rows == 2)
+        hipLaunchKernelGGL((lm_gemm_narrow_kernel<false, 1, 4, 2>), grid, block, 0, stream, p);
+      else if (rt == 1)
+        hipLaunchKernelGGL((lm_gemm_narrow_kernel<false, 1, 4, 4>), grid, block, 0, stream, p);
+      else
+        hipLaunchKernelGGL((lm_gemm_narrow_kernel<false, 2, 2, 4>), grid, block, 0, stream, p);
+    }
   } else {
     const dim3 gemm_grid(kTilesPerRow, (p.rows_pad + kRowsPerGroup - 1) / kRowsPerGroup);
     if (p.q8)

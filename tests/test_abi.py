@@ -176,6 +176,6 @@ def test_lmhead_pack_argument_errors_need_no_device():
         assert st == s.CAPACITY and e.needed == 32 and e.available == 900
         st = pack(None, s.VOCAB, 896, ctypes.c_void_p(8), None, ctypes.byref(e))
         assert st == s.ALIGNMENT and e.needed == 16 and e.available == 8
-    # both layouts are as large as their source matrices
-    assert s.lib().pb_lmhead_packed_bytes(s.VOCAB, 896) == s.VOCAB * 28 * 18
+    # the source matrices, plus the Q4_0 layout's flag word per 64-id tile
+    assert s.lib().pb_lmhead_packed_bytes(s.VOCAB, 896) == s.VOCAB * 28 * 18 + s.VOCAB // 64 * 4
     assert s.lib().pb_lmhead_q8_packed_bytes(s.VOCAB, 896) == s.VOCAB * 28 * 34

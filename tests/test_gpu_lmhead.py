@@ -81,7 +81,7 @@ def oracle_head(w, hidden, rows):
 
 # up to 64 rows the head runs lm_gemm_narrow_kernel (one 16-row tile per wave up
 # to 32 rows, two above), beyond that lm_gemm_kernel: both sides of each switch
-@pytest.mark.parametrize("rows", [5, 16, 17, 32, 33, 64, 65, 129, 300])
+@pytest.mark.parametrize("rows", [1, 2, 5, 16, 17, 32, 33, 64, 65, 129, 300])
 def test_head_logits_and_draws_are_bit_exact(smp, head, rows):
     w, packed = head
     hidden = w["hidden"][:rows]

@@ -74,7 +74,7 @@ def test_the_references_dots_row_on_the_device(smp):
     assert (glog == oracle_logits(hidden, q8.reshape(-1), cols)).all()
 
 
-@pytest.mark.parametrize("rows", [5, 16, 17, 32, 33, 64, 65, 129, 300])
+@pytest.mark.parametrize("rows", [1, 2, 5, 16, 17, 32, 33, 64, 65, 129, 300])
 def test_q8_head_logits_and_draws_are_bit_exact(smp, head, rows):
     w, q8, packed = head
     hidden = w["hidden"][:rows]
