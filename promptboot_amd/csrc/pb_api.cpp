@@ -417,10 +417,8 @@ uint32_t pb_lmhead_pack_q4_0(const uint8_t* d_q4, size_t vocab, size_t cols, uin
                              void* stream, pb_inference_error* err) {
   const uint32_t st = check_pack_args(vocab, cols, d_packed, err);
   if (st != PB_OK) return st;
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  hipError_t e = hipMemsetAsync(d_packed + vocab * (cols / 32) * 18, 0, vocab / 64 * 4, s);
-  if (e == hipSuccess)
-    e = pb::launch_lm_pack(d_q4, d_packed, (uint32_t)vocab, (uint32_t)(cols / 32), s);
+  hipError_t e = pb::launch_lm_pack(d_q4, d_packed, (uint32_t)vocab, (uint32_t)(cols / 32),
+                                    static_cast<hipStream_t>(stream));
   return e == hipSuccess ? PB_OK : device_error(err, e);
 }
 

@@ -126,7 +126,7 @@ __device__ __forceinline__ uint32_t f32_bits_to_half(uint32_t bits) {
 //      holds element j in the low and element 16 + j in the high nibble).
 // out: [blocks][vocab / 64 tiles][1 KB] nibbles, then [blocks][vocab] fp16
 //      scales, then one word per tile, non-zero when one of the tile's scales
-//      is infinite or NaN (cleared by the caller before the launch).  In the kilobyte of (block b, tile t), lane l = 16 q + n of a
+//      is infinite or NaN (cleared by lm_clear_kernel before the launch).  In the kilobyte of (block b, tile t), lane l = 16 q + n of a
 //      head wave reads the 16 bytes at 16 l: word c of them is bytes
 //      4q .. 4q+3 of id 64 t + 4 n + c, every nibble XOR 8.  vocab % 64 == 0.
 __global__ __launch_bounds__(kBlockThreads) void lm_pack_kernel(const uint8_t* __restrict__ in,
@@ -155,6 +155,11 @@ __global__ __launch_bounds__(kBlockThreads) void lm_pack_kernel(const uint8_t* _
     uint32_t* flags = reinterpret_cast<uint32_t*>(scales + (size_t)blocks * vocab);
     atomicOr(&flags[t], 1u);
   }
+}
+
+__global__ __launch_bounds__(kBlockThreads) void lm_clear_kernel(uint32_t* words, uint32_t n) {
+  const uint32_t i = blockIdx.x * kBlockThreads + threadIdx.x;
+  if (i < n) words[i] = 0u;
 }
 
 // ---- repack: promptboot's Q8_0 rows -> the head's tile layout ----
@@ -953,6 +958,11 @@ __global__ __launch_bounds__(64) void mfma_selftest_kernel(int32_t* out) {
 hipError_t launch_lm_pack(const uint8_t* in, uint8_t* out, uint32_t vocab, uint32_t blocks,
                           hipStream_t stream) {
   const size_t n = (size_t)vocab * blocks;
+  // the tile flags start at zero: a fill kernel rather than a memset, which a
+  // caller capturing the repack in a graph could not replay reliably
+  uint32_t* flags = reinterpret_cast<uint32_t*>(out + n * 18);
+  hipLaunchKernelGGL(lm_clear_kernel, dim3((vocab / kTileIds + kBlockThreads - 1) / kBlockThreads),
+                     dim3(kBlockThreads), 0, stream, flags, vocab / kTileIds);
   hipLaunchKernelGGL(lm_pack_kernel, dim3((uint32_t)((n + kBlockThreads - 1) / kBlockThreads)),
                      dim3(kBlockThreads), 0, stream, in, out, vocab, blocks);
   return hipGetLastError();
