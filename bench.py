@@ -152,17 +152,23 @@ def time_batch(smp, w: dict, steps: int, warmup: int) -> dict:
         torch.cuda.synchronize()
     for _ in range(warmup):
         step()
+    # Two timed passes of the same K steps: HIP events around each launch give
+    # the kernel time (the roofline); a pass with no events in it gives the
+    # wall time per step (the rows/s value), free of the events' own markers.
     starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
     ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
     for i in range(steps):
         starts[i].record(stream)
         step()
         ends[i].record(stream)
     torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
     kernel_ms = float(np.mean([a.elapsed_time(b) for a, b in zip(starts, ends)]))
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
     ms_per_step = wall / steps * 1e3
     alg = workloads.algorithmic_bytes(w["hist_len"])
     return {"rows": B, "ms_per_step": ms_per_step, "rows_per_s": B / (ms_per_step / 1e3),
@@ -282,17 +288,21 @@ def time_lmhead(smp, steps: int, warmup: int, q8: bool = False, rows: int = 256)
         torch.cuda.synchronize()
     for _ in range(warmup):
         step()
+    # events around each step for its time; a pass without events for rows/s
     starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
     ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
     for i in range(steps):
         starts[i].record(stream)
         step()
         ends[i].record(stream)
     torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
     step_ms = float(np.mean([a.elapsed_time(b) for a, b in zip(starts, ends)]))
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
     # parity on a bounded sample: the oracle's head and sampler on the first
     # rows (bit-exact logits; token agreement on non-boundary rows)
     from oracle import oracle as o
