@@ -472,10 +472,12 @@ __global__ __launch_bounds__(kGemmThreads) void lm_gemm_kernel(LmParams p) {
   const uint8_t* a_base = reinterpret_cast<const uint8_t*>(p.act_q) + ((size_t)rw0 + n) * 32 + 8u * q;
   const size_t a_stride = (size_t)p.rows_pad * 32;  // bytes per block
   constexpr uint32_t kWords = kQ8 ? 2u : 1u;  // uint4 of packed weights per lane and block
-  const v4u* w_base =
-      reinterpret_cast<const v4u*>(p.weights + (size_t)tile * (kQ8 ? kTileBytesQ8 : kTileBytes)) +
-      kWords * lane;
-  const size_t w_stride = (size_t)kTilesPerRow * ((kQ8 ? kTileBytesQ8 : kTileBytes) / 16);
+  constexpr uint32_t kTile = kQ8 ? kTileBytesQ8 : kTileBytes;
+  // The weights are read at the kernel argument plus one 32-bit byte offset
+  // (a scalar base, no 64-bit lane arithmetic): widths of at most 2048 keep
+  // the packed head under 330 MB.
+  const uint32_t w_stride = kTilesPerRow * kTile;  // bytes per block
+  const uint32_t w_off = tile * kTile + 16u * kWords * lane;
 
   // Operands of one block: both row tiles' activation fragments and the
   // lane's packed weight words (one per column tile).  Two sets alternate
@@ -489,8 +491,10 @@ __global__ __launch_bounds__(kGemmThreads) void lm_gemm_kernel(LmParams p) {
     const uint8_t* ab = a_base + (size_t)b * a_stride;
     o.a[0] = *reinterpret_cast<const uint64_t*>(ab);
     o.a[1] = *reinterpret_cast<const uint64_t*>(ab + 16u * 32u);
+    const uint32_t wo = b * w_stride + w_off;
 #pragma unroll
-    for (uint32_t k = 0; k < kWords; ++k) o.raw[k] = w_base[(size_t)b * w_stride + k];
+    for (uint32_t k = 0; k < kWords; ++k)
+      o.raw[k] = *reinterpret_cast<const v4u*>(p.weights + (wo + 16u * k));
   };
   auto run = [&](uint32_t b, const Operands& o, auto odd_tag) {
     constexpr bool kOdd = decltype(odd_tag)::value;
@@ -635,7 +639,10 @@ template <bool kQ8, int kRT, int kSets, int kI>
 __global__ __launch_bounds__(256) void lm_gemm_narrow_kernel(LmParams p) {
   static_assert(kI == 4 || kRT == 1, "partial rows only with one row tile");
   const uint32_t lane = threadIdx.x & 63u;
-  const uint32_t tile = blockIdx.x * 4u + (threadIdx.x >> 6);
+  // the tile is wave-uniform: held in scalar registers, so every load below
+  // is a scalar base plus a 32-bit lane offset, with no 64-bit address
+  // arithmetic per lane
+  const uint32_t tile = blockIdx.x * 4u + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (tile >= kTilesPerRow) return;  // whole wave, no barrier follows
   const uint32_t n = lane & 15u;
   const uint32_t q = lane >> 4;
@@ -655,14 +662,20 @@ __global__ __launch_bounds__(256) void lm_gemm_narrow_kernel(LmParams p) {
     hw[s] = row < p.rows ? p.bitmap[(size_t)row * kWordsPerRow + (v0 >> 5) + (n >> 3)] : 0u;
   }
 
-  const uint8_t* a_base = reinterpret_cast<const uint8_t*>(p.act_q) + ((size_t)row0 + n) * 32 + 8u * q;
-  const size_t a_stride = (size_t)p.rows_pad * 32;  // bytes per block
-  const v4u* w_base = reinterpret_cast<const v4u*>(p.weights + (size_t)tile * kTile) + kWords * lane;
-  const size_t w_stride = (size_t)kTilesPerRow * (kTile / 16);  // uint4 per block
-  const uint16_t* ws_base = reinterpret_cast<const uint16_t*>(
-                                p.weights + (size_t)blocks * kVocab * (kQ8 ? 32 : 16)) +
-                            v0 + 4u * n;
-  const float* as_base = p.act_s + row0 + 4u * q;
+  // Each load is a wave-uniform base plus one 32-bit byte offset (the block's
+  // uniform part + the lane's part).  The widths of at most 2048 keep the
+  // packed head under 330 MB, so every offset fits.
+  const uint8_t* a_base = reinterpret_cast<const uint8_t*>(p.act_q);
+  const uint32_t a_stride = p.rows_pad * 32u;  // bytes per block
+  const uint32_t a_off = (row0 + n) * 32u + 8u * q;
+  const uint8_t* w_base = p.weights;
+  const uint32_t w_stride = kTilesPerRow * kTile;  // bytes per block
+  const uint32_t w_off = tile * kTile + 16u * kWords * lane;
+  const uint8_t* ws_base = p.weights;
+  const uint32_t ws_off = blocks * kVocab * (kQ8 ? 32u : 16u) + 2u * v0 + 8u * n;
+  const uint8_t* as_base = reinterpret_cast<const uint8_t*>(p.act_s);
+  const uint32_t as_stride = p.rows_pad * 4u;
+  const uint32_t as_off = (row0 + 4u * q) * 4u;
 
   // Only the kI activation scales a lane uses are loaded: a register of a
   // wider load left unused would be taken for a temporary while the load is
@@ -675,16 +688,19 @@ __global__ __launch_bounds__(256) void lm_gemm_narrow_kernel(LmParams p) {
     vIf as[kRT];    // activation scales / 16 of rows 16 rt + 4q .. 4q + kI - 1
   };
   auto load = [&](uint32_t b, Operands& o) {
-    const uint8_t* ab = a_base + (size_t)b * a_stride;
+    const uint32_t ao = b * a_stride + a_off;
 #pragma unroll
     for (int rt = 0; rt < kRT; ++rt)
-      o.a[rt] = *reinterpret_cast<const uint64_t*>(ab + 16u * 32u * (uint32_t)rt);
+      o.a[rt] = *reinterpret_cast<const uint64_t*>(a_base + (ao + 16u * 32u * (uint32_t)rt));
+    const uint32_t wo = b * w_stride + w_off;
 #pragma unroll
-    for (uint32_t k = 0; k < kWords; ++k) o.raw[k] = w_base[(size_t)b * w_stride + k];
-    o.ws = *reinterpret_cast<const uint64_t*>(ws_base + (size_t)b * kVocab);
+    for (uint32_t k = 0; k < kWords; ++k)
+      o.raw[k] = *reinterpret_cast<const v4u*>(w_base + (wo + 16u * k));
+    o.ws = *reinterpret_cast<const uint64_t*>(ws_base + (b * (kVocab * 2u) + ws_off));
+    const uint32_t so = b * as_stride + as_off;
 #pragma unroll
     for (int rt = 0; rt < kRT; ++rt)
-      o.as[rt] = *reinterpret_cast<const vIf*>(as_base + (size_t)b * p.rows_pad + 16u * rt);
+      o.as[rt] = *reinterpret_cast<const vIf*>(as_base + (so + 64u * (uint32_t)rt));
   };
 
   float total[kRT][4][4];
