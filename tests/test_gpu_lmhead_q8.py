@@ -182,3 +182,34 @@ def test_q8_decode_steps_match_the_oracle_loop(smp, head):
             assert dec.sampling_states()[r].draws() == d.state.draws()
     finally:
         dec.close()
+
+
+@pytest.mark.parametrize("rows", [3, 140])
+def test_widest_hidden_state_q8(smp, rows):
+    """cols = 2048, the widest the head accepts: the packed Q8_0 head is then
+    330 MB, the largest byte offsets the GEMMs' weight and scale loads take.
+    Logits bit-exact through the narrow kernel (3 rows) and the wide one
+    (140 rows), and tokens equal to the oracle sampler's."""
+    import torch
+
+    cols = 2048
+    rng = np.random.default_rng(12)
+    blocks = cols // 32
+    q8 = rng.integers(0, 256, (V, blocks, 34), dtype=np.uint8)
+    sc = rng.uniform(0.0005, 0.004, (V, blocks)).astype(np.float16).view(np.uint16)
+    q8[:, :, 0] = sc & 0xFF
+    q8[:, :, 1] = sc >> 8
+    packed = smp.pack_lmhead(torch.from_numpy(q8.reshape(-1)).to("cuda:0"), cols=cols, q8=True)
+    hidden = rng.standard_normal((rows, cols)).astype(np.float32)
+    r24 = np.arange(rows, dtype=np.uint32) * 977
+    token = torch.empty(rows, dtype=torch.int32, device="cuda:0")
+    logits = torch.empty((rows, V), dtype=torch.int32, device="cuda:0")
+    smp.lmhead_sample(packed, to_dev(hidden), to_dev(r24), token=token, logits=logits, cols=cols,
+                      q8=True)
+    torch.cuda.synchronize()
+    glog = logits.cpu().numpy().view(np.uint32)
+    rlog = oracle_logits(hidden, q8.reshape(-1), cols)
+    assert (glog == rlog).all()
+    rtok, _, _, _ = o.sample_batch(rlog, np.zeros((rows, 1), np.uint32),
+                                   np.zeros(rows, np.uint32), r24, threads=4)
+    assert (token.cpu().numpy().view(np.uint32) == rtok).all()
