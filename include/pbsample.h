@@ -89,6 +89,26 @@ typedef struct pb_top_logit {
   uint32_t logit_bits;
 } pb_top_logit;
 
+/* Layout checks at compile time, as the reference makes them for its repr(C)
+ * types (InferenceError: inference.rs:287-288; SamplingState: :812).  A C11
+ * or C++11 consumer whose struct layout differs does not compile. */
+#ifdef __cplusplus
+#define PB_STATIC_ASSERT(cond, msg) static_assert(cond, msg)
+#define PB_ALIGNOF(type) alignof(type)
+#else
+#define PB_STATIC_ASSERT(cond, msg) _Static_assert(cond, msg)
+#define PB_ALIGNOF(type) _Alignof(type)
+#endif
+PB_STATIC_ASSERT(sizeof(pb_sampling_state) == 16, "SamplingState is 16 bytes");
+PB_STATIC_ASSERT(PB_ALIGNOF(pb_sampling_state) == 8, "SamplingState is 8-byte aligned");
+PB_STATIC_ASSERT(sizeof(pb_inference_error) == 48, "InferenceError is 48 bytes");
+PB_STATIC_ASSERT(PB_ALIGNOF(pb_inference_error) == 8, "InferenceError is 8-byte aligned");
+PB_STATIC_ASSERT(offsetof(pb_inference_error, tensor_id) == 16, "InferenceError.tensor_id at 16");
+PB_STATIC_ASSERT(offsetof(pb_inference_error, needed) == 24, "InferenceError.needed at 24");
+PB_STATIC_ASSERT(offsetof(pb_inference_error, available) == 32, "InferenceError.available at 32");
+PB_STATIC_ASSERT(offsetof(pb_inference_error, detail) == 40, "InferenceError.detail at 40");
+PB_STATIC_ASSERT(sizeof(pb_top_logit) == 8, "TopLogit is 8 bytes");
+
 /* Per-row evidence beside each draw.  Not in the reference (it returns only the
  * token): the top-20 in rank order, their penalised logits and softmax
  * weights, the kept-survivor probabilities w[i]/kept_total (0 past `kept`),
@@ -104,6 +124,7 @@ typedef struct pb_sample_detail {
   uint32_t flags;
   uint32_t token;
 } pb_sample_detail;
+PB_STATIC_ASSERT(sizeof(pb_sample_detail) == 336, "pb_sample_detail is 84 words");
 
 #define PB_FLAG_DRAW_BOUNDARY 1u   /* target within 1e-6 * kept_total of a CDF step */
 #define PB_FLAG_CUTOFF_BOUNDARY 2u /* top-p cutoff within 1e-6 * total of a prefix */
@@ -150,9 +171,31 @@ uint32_t pb_top_logits_8(const uint32_t *logits, size_t logits_len, pb_top_logit
 typedef struct pb_context pb_context;
 
 /* Creates a context on `device` (-1 = current device).  The context owns the
- * inter-kernel workspace and the staging buffers of the drop-ins. */
+ * inter-kernel workspace of the batched calls and the staging buffers of the
+ * drop-ins; every allocation happens here or in pb_context_reserve.  At
+ * creation it holds the sampler's workspace for any batch under the
+ * automatic slice plan and the drop-ins' staging for histories of up to
+ * PB_CONTEXT_IDS ids; the LM head needs pb_context_reserve first. */
+#define PB_CONTEXT_IDS 32768u /* CONTEXT_LIMIT, inference.rs:13 */
 uint32_t pb_context_create(int device, pb_context **out);
 void pb_context_destroy(pb_context *ctx);
+
+/* Sizes the context's workspace for batched calls of up to `rows` rows:
+ * the sampler's slice workspace under the context's current slice plan
+ * (pb_context_set_segments), and, when cols > 0, the fused LM head's
+ * workspace for hidden states of up to `cols` columns (either head format,
+ * logits included).  Allocates (and waits for the device) only when the
+ * workspace grows; never shrinks it.  Call it at set-up: the batched entry
+ * points below never allocate, never wait, and return PB_CAPACITY
+ * (needed/available = workspace bytes) when a call needs more than was
+ * reserved, so a reserved context's calls can be captured in a HIP graph. */
+uint32_t pb_context_reserve(pb_context *ctx, uint32_t rows, size_t cols, pb_inference_error *err);
+
+/* Threading and streams: one context's batched calls share its workspace.
+ * Calls on one context must be ordered -- issued on one stream, or the
+ * caller orders the streams -- and calls that overlap on the device race on
+ * the workspace.  The host side takes the context's lock, so concurrent
+ * host threads are safe; different contexts are independent. */
 
 /*
  * Samples `rows` independent rows.  All pointers are device pointers; the
@@ -219,11 +262,15 @@ uint32_t pb_lmhead_pack_q4_0(const uint8_t *d_q4, size_t vocab, size_t cols, uin
  * words) through the packed head, then the sampler exactly as pb_sample_batch
  * on the resulting logits (repetition penalty, top-k 20, temperature 0.7,
  * top-p 0.8, draw).  vocab must be PB_VOCAB, cols a multiple of 32 up to 2048
- * (896 for Qwen2.5-0.5B).  d_logits (optional, rows x vocab words) receives the raw
- * logits; without it they live in the context's workspace.  Per-row outputs
- * and error records as pb_sample_batch (non-finite logit, bad history id). */
-uint32_t pb_lmhead_sample_batch(pb_context *ctx, const uint8_t *d_packed, size_t vocab,
-                                size_t cols, const uint32_t *d_hidden, uint32_t rows,
+ * (896 for Qwen2.5-0.5B).  packed_bytes is the size of d_packed and must be
+ * pb_lmhead_packed_bytes(vocab, cols): a head packed for another width or
+ * format is refused (PB_CAPACITY) before anything is enqueued.  d_logits
+ * (optional, rows x vocab words) receives the raw logits; without it they
+ * live in the context's workspace.  Per-row outputs and error records as
+ * pb_sample_batch (non-finite logit, bad history id).  Needs a context
+ * reserved (pb_context_reserve) for at least `rows` rows and `cols` columns. */
+uint32_t pb_lmhead_sample_batch(pb_context *ctx, const uint8_t *d_packed, size_t packed_bytes,
+                                size_t vocab, size_t cols, const uint32_t *d_hidden, uint32_t rows,
                                 const uint32_t *d_hist, size_t hist_ld,
                                 const uint32_t *d_hist_len, const uint32_t *d_random_24,
                                 uint32_t *d_token, pb_sample_detail *d_detail,
@@ -250,9 +297,10 @@ size_t pb_lmhead_q8_packed_bytes(size_t vocab, size_t cols);
 uint32_t pb_lmhead_pack_q8_0(const uint8_t *d_q8, size_t vocab, size_t cols, uint8_t *d_packed,
                              void *stream, pb_inference_error *err);
 
-/* pb_lmhead_sample_batch for a head packed by pb_lmhead_pack_q8_0. */
-uint32_t pb_lmhead_q8_sample_batch(pb_context *ctx, const uint8_t *d_packed, size_t vocab,
-                                   size_t cols, const uint32_t *d_hidden, uint32_t rows,
+/* pb_lmhead_sample_batch for a head packed by pb_lmhead_pack_q8_0
+ * (packed_bytes = pb_lmhead_q8_packed_bytes(vocab, cols)). */
+uint32_t pb_lmhead_q8_sample_batch(pb_context *ctx, const uint8_t *d_packed,
+                                   size_t packed_bytes, size_t vocab, size_t cols, const uint32_t *d_hidden, uint32_t rows,
                                    const uint32_t *d_hist, size_t hist_ld,
                                    const uint32_t *d_hist_len, const uint32_t *d_random_24,
                                    uint32_t *d_token, pb_sample_detail *d_detail,
@@ -271,7 +319,11 @@ uint32_t pb_lmhead_q8_sample_batch(pb_context *ctx, const uint8_t *d_packed, siz
  *     1119-1150);
  *   - a row whose context reaches its length limit ends (the REPL's
  *     MAX_NEW_TOKENS / CONTEXT_LIMIT stop);
- *   - a row error ends the row with no append and no draw.
+ *   - a row error ends the row with no append and no draw;
+ *   - a row whose context is already at its limit when the step starts is
+ *     not sampled (the REPL stops before sampling when there is no room):
+ *     it ends with PB_ROW_LIMIT and token PB_NO_TOKEN, and its draw is
+ *     returned by pb_decode_settle.
  * Row states (d_row_state, one word per row, updated in place): */
 enum pb_row_state {
   PB_ROW_ACTIVE = 0, /* sampled this step */
@@ -298,8 +350,8 @@ uint32_t pb_decode_step(pb_context *ctx, const uint32_t *d_logits, size_t vocab,
 
 /* The same step with the fused Q4_0 LM head in front (pb_lmhead_sample_batch
  * for the active rows, then the decode-loop bookkeeping above). */
-uint32_t pb_lmhead_decode_step(pb_context *ctx, const uint8_t *d_packed, size_t vocab,
-                               size_t cols, const uint32_t *d_hidden, uint32_t rows,
+uint32_t pb_lmhead_decode_step(pb_context *ctx, const uint8_t *d_packed, size_t packed_bytes,
+                               size_t vocab, size_t cols, const uint32_t *d_hidden, uint32_t rows,
                                uint32_t *d_hist, size_t hist_ld, uint32_t *d_hist_len,
                                const uint32_t *d_max_len, uint32_t *d_row_state,
                                const uint32_t *d_random_24, uint32_t *d_token,
@@ -308,8 +360,8 @@ uint32_t pb_lmhead_decode_step(pb_context *ctx, const uint8_t *d_packed, size_t 
 
 /* The same step with the fused Q8_0 head (pb_lmhead_q8_sample_batch): the
  * REPL's own configuration, whose logits come from the Q8_0 output tensor. */
-uint32_t pb_lmhead_q8_decode_step(pb_context *ctx, const uint8_t *d_packed, size_t vocab,
-                                  size_t cols, const uint32_t *d_hidden, uint32_t rows,
+uint32_t pb_lmhead_q8_decode_step(pb_context *ctx, const uint8_t *d_packed,
+                                  size_t packed_bytes, size_t vocab, size_t cols, const uint32_t *d_hidden, uint32_t rows,
                                   uint32_t *d_hist, size_t hist_ld, uint32_t *d_hist_len,
                                   const uint32_t *d_max_len, uint32_t *d_row_state,
                                   const uint32_t *d_random_24, uint32_t *d_token,
@@ -322,12 +374,12 @@ uint32_t pb_lmhead_q8_decode_step(pb_context *ctx, const uint8_t *d_packed, size
  * token and never for a failed sample (inference.rs:954-963). */
 void pb_decode_draw(pb_sampling_state *states, const uint32_t *row_state, uint32_t rows,
                     uint32_t *out, pb_sampling_state *saved);
-/* After the step: rows that were PB_ROW_ACTIVE before it and are
- * PB_ROW_ERROR after it get their saved state back (the failed sample
- * consumed no draw).  Returns the number of rows restored. */
+/* After the step: rows that were PB_ROW_ACTIVE before it and got no token
+ * (tokens[i] == PB_NO_TOKEN: a row error, or a row already at its limit) get
+ * their saved state back, since no sample consumed their draw.  Returns the
+ * number of rows restored. */
 uint32_t pb_decode_settle(pb_sampling_state *states, const pb_sampling_state *saved,
-                          const uint32_t *state_before, const uint32_t *state_after,
-                          uint32_t rows);
+                          const uint32_t *state_before, const uint32_t *tokens, uint32_t rows);
 
 /* Segments per row the batched sampler will use for `rows` (diagnostic). */
 uint32_t pb_segments_for_rows(uint32_t rows);

@@ -59,10 +59,10 @@ struct DeviceGuard {
 struct pb_context {
   int device = 0;
   hipStream_t stream = nullptr;  // used by the single-row drop-ins
-  std::mutex mu;                 // serialises the drop-ins on this context
+  std::mutex mu;                 // held by every call on this context
 
   uint32_t forced_segments = 0;  // 0 = automatic slices per row
-  void* d_work = nullptr;  // multi-slice workspace: row counters, slice top-20 lists
+  void* d_work = nullptr;  // multi-slice workspace: slice top-20 lists and slice records
   size_t list_bytes = 0;
 
   void* d_lm = nullptr;  // fused LM head workspace
@@ -106,21 +106,51 @@ constexpr size_t kOutGather = (kOutDetail + sizeof(pb_sample_detail) + 15) / 16 
 static_assert(kOutErr + sizeof(pb_inference_error) <= kOutDetail, "error record overlaps");
 static_assert(kInHist % 16 == 0, "history ids must stay 16-byte aligned");
 
-// Workspace of the multi-slice path: the slice keys and slice records,
-// grown as needed (hipFree synchronises the device, so no launch still
-// reads the old buffer).
-static hipError_t ensure_workspace(pb_context* ctx, size_t list_bytes) {
-  if (list_bytes <= ctx->list_bytes) return hipSuccess;
-  if (ctx->d_work) {
-    hipError_t e = hipFree(ctx->d_work);
-    ctx->d_work = nullptr;
-    ctx->list_bytes = 0;
+// Grows a device workspace to `bytes` (never shrinks it).  Only set-up calls
+// (pb_context_create, pb_context_reserve) use it: hipFree waits for the
+// device, so no launch still reads the old buffer.
+static hipError_t grow_device(void** buf, size_t* have, size_t bytes) {
+  if (bytes <= *have) return hipSuccess;
+  if (*buf) {
+    hipError_t e = hipFree(*buf);
+    *buf = nullptr;
+    *have = 0;
     if (e != hipSuccess) return e;
   }
-  hipError_t e = hipMalloc(&ctx->d_work, list_bytes);
+  hipError_t e = hipMalloc(buf, bytes);
   if (e != hipSuccess) return e;
-  ctx->list_bytes = list_bytes;
+  *have = bytes;
   return hipSuccess;
+}
+
+// Slice workspace of `slots` (row, slice) pairs: 20 keys and 2 words each.
+static size_t slice_workspace_bytes(size_t slots) { return slots * (PB_TOP_K * 8 + 8); }
+
+// Largest rows x slices a batch of up to `rows` rows uses under the slice
+// plan (forced slices, or the automatic plan, which uses one slice per row
+// from 256 rows on and needs no workspace there).
+static size_t max_slots(uint32_t rows, uint32_t forced_segments) {
+  size_t best = 0;
+  const uint32_t top = forced_segments ? rows : (rows < 256u ? rows : 255u);
+  const uint32_t from = forced_segments ? rows : 1u;
+  for (uint32_t r = from; r <= top && r > 0; ++r) {
+    uint32_t segs = 0, seg_f4 = 0;
+    pb::plan_segments(r, forced_segments, &segs, &seg_f4);
+    if (segs > 1 && (size_t)r * segs > best) best = (size_t)r * segs;
+  }
+  return best;
+}
+
+// Fused LM head workspace for `rows` rows of `cols` columns (either format),
+// logits included.
+static size_t lm_workspace_bytes(uint32_t rows, size_t cols, bool with_logits) {
+  auto align = [](size_t x) { return (x + 255) & ~(size_t)255; };
+  const size_t rows_pad = ((size_t)rows + 63u) & ~(size_t)63u;
+  const size_t blocks = cols / 32;
+  return align((size_t)rows * (PB_VOCAB / 32) * 4) + align((size_t)rows * 8) +
+         align(blocks * rows_pad * 32) + align(blocks * rows_pad * 4) +
+         align((size_t)rows * (PB_VOCAB / 64) * 4) +
+         (with_logits ? align((size_t)rows * PB_VOCAB * 4) : 0);
 }
 
 static void free_staging(pb_context* ctx) {
@@ -243,7 +273,11 @@ uint32_t pb_context_create(int device, pb_context** out) {
   if (e == hipSuccess) e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
   if (e == hipSuccess) e = hipMalloc(&ctx->d_seen, PB_SEEN_BYTES);
   if (e == hipSuccess) e = hipHostMalloc(&ctx->h_seen, PB_SEEN_BYTES, hipHostMallocDefault);
-  if (e == hipSuccess) e = ensure_staging(ctx, 4096);
+  // the drop-ins' staging for a whole context, and the slice workspace of
+  // the automatic plan for any batch
+  if (e == hipSuccess) e = ensure_staging(ctx, PB_CONTEXT_IDS);
+  if (e == hipSuccess)
+    e = grow_device(&ctx->d_work, &ctx->list_bytes, slice_workspace_bytes(max_slots(255, 0)));
   if (e != hipSuccess) {
     release(ctx);
     return PB_DEVICE;
@@ -253,6 +287,21 @@ uint32_t pb_context_create(int device, pb_context** out) {
 }
 
 void pb_context_destroy(pb_context* ctx) { release(ctx); }
+
+uint32_t pb_context_reserve(pb_context* ctx, uint32_t rows, size_t cols, pb_inference_error* err) {
+  clear_error(err);
+  if (cols != 0 && (cols % 32 != 0 || cols > 2048)) {
+    set_error(err, PB_CAPACITY, PB_DOMAIN_NONE, 32, cols, PB_FIELD_BYTES, 4);
+    return PB_CAPACITY;
+  }
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  DeviceGuard guard(ctx->device);
+  hipError_t e = grow_device(&ctx->d_work, &ctx->list_bytes,
+                             slice_workspace_bytes(max_slots(rows, ctx->forced_segments)));
+  if (e == hipSuccess && cols != 0 && rows != 0)
+    e = grow_device(&ctx->d_lm, &ctx->lm_bytes, lm_workspace_bytes(rows, cols, true));
+  return e == hipSuccess ? PB_OK : device_error(err, e);
+}
 
 }  // extern "C"
 
@@ -279,14 +328,17 @@ static bool decode_args_ok(const DecodeArgs& dec, pb_inference_error* err) {
   return true;
 }
 
-// Validates and enqueues one batched sample (every variant).
-static uint32_t enqueue_sample(pb_context* ctx, const uint32_t* d_logits, size_t vocab, size_t ld,
-                               uint32_t rows, const uint32_t* d_hist, size_t hist_ld,
-                               const uint32_t* d_hist_len, const uint32_t* d_random_24,
-                               const uint8_t* d_excl, uint32_t* d_token,
-                               pb_sample_detail* d_detail, pb_inference_error* d_err,
-                               hipStream_t stream, pb_inference_error* err,
-                               const DecodeArgs* dec = nullptr) {
+// Validates and enqueues one batched sample (every variant) with the slice
+// workspace `work` of `work_bytes` bytes.  Never allocates: a plan that
+// needs more workspace than that is refused with PB_CAPACITY.
+static uint32_t enqueue_sample_in(int device, uint32_t forced_segments, void* work,
+                                  size_t work_bytes, const uint32_t* d_logits, size_t vocab,
+                                  size_t ld, uint32_t rows, const uint32_t* d_hist,
+                                  size_t hist_ld, const uint32_t* d_hist_len,
+                                  const uint32_t* d_random_24, const uint8_t* d_excl,
+                                  uint32_t* d_token, pb_sample_detail* d_detail,
+                                  pb_inference_error* d_err, hipStream_t stream,
+                                  pb_inference_error* err, const DecodeArgs* dec = nullptr) {
   clear_error(err);
   if (vocab != PB_VOCAB) {
     // logits_error (inference.rs:737-754)
@@ -322,23 +374,51 @@ static uint32_t enqueue_sample(pb_context* ctx, const uint32_t* d_logits, size_t
   p.err = d_err;
   p.hist_vec4 = (p.hist != nullptr && hist_ld >= 4u && (hist_ld & 3u) == 0 &&
                  ((uintptr_t)d_hist & 15u) == 0);
-  pb::plan_segments(rows, ctx->forced_segments, &p.segs, &p.seg_f4);
+  pb::plan_segments(rows, forced_segments, &p.segs, &p.seg_f4);
   p.part_keys = nullptr;
   p.part_meta = nullptr;
   set_decode(p, dec);
-  DeviceGuard guard(ctx->device);
   if (p.segs > 1) {
     const size_t slots = (size_t)rows * p.segs;
-    const size_t key_bytes = slots * PB_TOP_K * 8;
-    hipError_t e = ensure_workspace(ctx, key_bytes + slots * 8);
-    if (e != hipSuccess) return device_error(err, e);
-    char* base = static_cast<char*>(ctx->d_work);
+    const size_t need = slice_workspace_bytes(slots);
+    if (need > work_bytes || work == nullptr) {
+      set_error(err, PB_CAPACITY, PB_DOMAIN_NONE, need, work_bytes, PB_FIELD_BYTES, 6);
+      return PB_CAPACITY;
+    }
+    char* base = static_cast<char*>(work);
     p.part_keys = reinterpret_cast<uint64_t*>(base);
-    p.part_meta = reinterpret_cast<uint32_t*>(base + key_bytes);
+    p.part_meta = reinterpret_cast<uint32_t*>(base + slots * PB_TOP_K * 8);
   }
+  DeviceGuard guard(device);
   hipError_t e = pb::launch_sample(p, stream);
   if (e != hipSuccess) return device_error(err, e);
   return PB_OK;
+}
+
+// enqueue_sample_in on the context's own workspace.  The arguments are
+// checked before the context is touched; then the context's lock is taken
+// unless the caller (a drop-in) already holds it.
+static uint32_t enqueue_sample(pb_context* ctx, const uint32_t* d_logits, size_t vocab, size_t ld,
+                               uint32_t rows, const uint32_t* d_hist, size_t hist_ld,
+                               const uint32_t* d_hist_len, const uint32_t* d_random_24,
+                               const uint8_t* d_excl, uint32_t* d_token,
+                               pb_sample_detail* d_detail, pb_inference_error* d_err,
+                               hipStream_t stream, pb_inference_error* err,
+                               const DecodeArgs* dec = nullptr, bool locked = false) {
+  uint32_t st = enqueue_sample_in(-1, 0, nullptr, 0, d_logits, vocab, ld, 0, d_hist, hist_ld,
+                                  d_hist_len, d_random_24, d_excl, d_token, d_detail, d_err,
+                                  stream, err, dec);
+  if (st != PB_OK || rows == 0) return st;
+  if (d_logits == nullptr || d_random_24 == nullptr || d_token == nullptr ||
+      (d_hist_len != nullptr && d_hist == nullptr)) {
+    set_error(err, PB_CAPACITY, PB_DOMAIN_ARGMAX, 1, 0, PB_FIELD_BYTES, 3);
+    return PB_CAPACITY;
+  }
+  std::unique_lock<std::mutex> lock(ctx->mu, std::defer_lock);
+  if (!locked) lock.lock();
+  return enqueue_sample_in(ctx->device, ctx->forced_segments, ctx->d_work, ctx->list_bytes,
+                           d_logits, vocab, ld, rows, d_hist, hist_ld, d_hist_len, d_random_24,
+                           d_excl, d_token, d_detail, d_err, stream, err, dec);
 }
 
 extern "C" {
@@ -362,6 +442,9 @@ uint32_t pb_sample_batch_inplace(pb_context* ctx, uint32_t* d_logits, size_t voc
   uint32_t st = enqueue_sample(ctx, d_logits, vocab, ld, rows, d_hist, hist_ld, d_hist_len,
                                d_random_24, d_seen, d_token, d_detail, d_err, s, err);
   if (st != PB_OK || rows == 0 || d_hist_len == nullptr) return st;
+  // Both launches go out under one hold of the lock: no other call on this
+  // context lands between them.  (The sample launch above took and released
+  // it; the write-back uses no context workspace.)
   pb::WritebackParams w;
   w.logits = d_logits;
   w.ld = ld;
@@ -433,8 +516,8 @@ uint32_t pb_lmhead_pack_q8_0(const uint8_t* d_q8, size_t vocab, size_t cols, uin
 
 }  // extern "C"
 
-static uint32_t enqueue_lmhead(pb_context* ctx, const uint8_t* d_packed, size_t vocab,
-                               size_t cols, const uint32_t* d_hidden, uint32_t rows,
+static uint32_t enqueue_lmhead(pb_context* ctx, const uint8_t* d_packed, size_t packed_bytes,
+                               size_t vocab, size_t cols, const uint32_t* d_hidden, uint32_t rows,
                                const uint32_t* d_hist, size_t hist_ld,
                                const uint32_t* d_hist_len, const uint32_t* d_random_24,
                                uint32_t* d_token, pb_sample_detail* d_detail,
@@ -449,6 +532,12 @@ static uint32_t enqueue_lmhead(pb_context* ctx, const uint8_t* d_packed, size_t 
   // LDS: up to 2,048 columns (Qwen2.5-0.5B has 896).
   if (cols == 0 || cols % 32 != 0 || cols > 2048) {
     set_error(err, PB_CAPACITY, PB_DOMAIN_NONE, 32, cols, PB_FIELD_BYTES, 4);
+    return PB_CAPACITY;
+  }
+  // the head must have been packed for this width and format
+  const size_t want = q8 ? pb_lmhead_q8_packed_bytes(vocab, cols) : pb_lmhead_packed_bytes(vocab, cols);
+  if (packed_bytes != want) {
+    set_error(err, PB_CAPACITY, PB_DOMAIN_NONE, want, packed_bytes, PB_FIELD_BYTES, 7);
     return PB_CAPACITY;
   }
   if (((uintptr_t)d_packed & 15u) != 0 || ((uintptr_t)d_logits & 15u) != 0) {
@@ -469,20 +558,13 @@ static uint32_t enqueue_lmhead(pb_context* ctx, const uint8_t* d_packed, size_t 
   const size_t actq_b = align((size_t)blocks * rows_pad * 32);
   const size_t acts_b = align((size_t)blocks * rows_pad * 4);
   const size_t tile_b = align((size_t)rows * (PB_VOCAB / 64) * 4);
-  const size_t logit_b = d_logits ? 0 : align((size_t)rows * PB_VOCAB * 4);
-  const size_t need = bitmap_b + meta_b + actq_b + acts_b + tile_b + logit_b;
-  DeviceGuard guard(ctx->device);
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  const size_t need = lm_workspace_bytes(rows, cols, d_logits == nullptr);
   if (need > ctx->lm_bytes) {
-    if (ctx->d_lm) {
-      hipError_t e = hipFree(ctx->d_lm);  // device-synchronising
-      ctx->d_lm = nullptr;
-      ctx->lm_bytes = 0;
-      if (e != hipSuccess) return device_error(err, e);
-    }
-    hipError_t e = hipMalloc(&ctx->d_lm, need);
-    if (e != hipSuccess) return device_error(err, e);
-    ctx->lm_bytes = need;
+    set_error(err, PB_CAPACITY, PB_DOMAIN_NONE, need, ctx->lm_bytes, PB_FIELD_BYTES, 6);
+    return PB_CAPACITY;
   }
+  DeviceGuard guard(ctx->device);
   char* base = static_cast<char*>(ctx->d_lm);
   pb::LmParams p;
   p.weights = d_packed;
@@ -524,26 +606,26 @@ static uint32_t enqueue_lmhead(pb_context* ctx, const uint8_t* d_packed, size_t 
 
 extern "C" {
 
-uint32_t pb_lmhead_sample_batch(pb_context* ctx, const uint8_t* d_packed, size_t vocab,
-                                size_t cols, const uint32_t* d_hidden, uint32_t rows,
+uint32_t pb_lmhead_sample_batch(pb_context* ctx, const uint8_t* d_packed, size_t packed_bytes,
+                                size_t vocab, size_t cols, const uint32_t* d_hidden, uint32_t rows,
                                 const uint32_t* d_hist, size_t hist_ld,
                                 const uint32_t* d_hist_len, const uint32_t* d_random_24,
                                 uint32_t* d_token, pb_sample_detail* d_detail,
                                 pb_inference_error* d_err, uint32_t* d_logits, void* stream,
                                 pb_inference_error* err) {
-  return enqueue_lmhead(ctx, d_packed, vocab, cols, d_hidden, rows, d_hist, hist_ld, d_hist_len,
+  return enqueue_lmhead(ctx, d_packed, packed_bytes, vocab, cols, d_hidden, rows, d_hist, hist_ld, d_hist_len,
                         d_random_24, d_token, d_detail, d_err, d_logits, stream, err, nullptr,
                         false);
 }
 
-uint32_t pb_lmhead_q8_sample_batch(pb_context* ctx, const uint8_t* d_packed, size_t vocab,
-                                   size_t cols, const uint32_t* d_hidden, uint32_t rows,
+uint32_t pb_lmhead_q8_sample_batch(pb_context* ctx, const uint8_t* d_packed,
+                                   size_t packed_bytes, size_t vocab, size_t cols, const uint32_t* d_hidden, uint32_t rows,
                                    const uint32_t* d_hist, size_t hist_ld,
                                    const uint32_t* d_hist_len, const uint32_t* d_random_24,
                                    uint32_t* d_token, pb_sample_detail* d_detail,
                                    pb_inference_error* d_err, uint32_t* d_logits, void* stream,
                                    pb_inference_error* err) {
-  return enqueue_lmhead(ctx, d_packed, vocab, cols, d_hidden, rows, d_hist, hist_ld, d_hist_len,
+  return enqueue_lmhead(ctx, d_packed, packed_bytes, vocab, cols, d_hidden, rows, d_hist, hist_ld, d_hist_len,
                         d_random_24, d_token, d_detail, d_err, d_logits, stream, err, nullptr,
                         true);
 }
@@ -564,8 +646,8 @@ uint32_t pb_decode_step(pb_context* ctx, const uint32_t* d_logits, size_t vocab,
                         &dec);
 }
 
-uint32_t pb_lmhead_decode_step(pb_context* ctx, const uint8_t* d_packed, size_t vocab,
-                               size_t cols, const uint32_t* d_hidden, uint32_t rows,
+uint32_t pb_lmhead_decode_step(pb_context* ctx, const uint8_t* d_packed, size_t packed_bytes,
+                               size_t vocab, size_t cols, const uint32_t* d_hidden, uint32_t rows,
                                uint32_t* d_hist, size_t hist_ld, uint32_t* d_hist_len,
                                const uint32_t* d_max_len, uint32_t* d_row_state,
                                const uint32_t* d_random_24, uint32_t* d_token,
@@ -574,12 +656,12 @@ uint32_t pb_lmhead_decode_step(pb_context* ctx, const uint8_t* d_packed, size_t 
   clear_error(err);
   const DecodeArgs dec{d_hist, d_hist_len, d_max_len, d_row_state};
   if (rows != 0 && !decode_args_ok(dec, err)) return PB_CAPACITY;
-  return enqueue_lmhead(ctx, d_packed, vocab, cols, d_hidden, rows, d_hist, hist_ld, d_hist_len,
+  return enqueue_lmhead(ctx, d_packed, packed_bytes, vocab, cols, d_hidden, rows, d_hist, hist_ld, d_hist_len,
                         d_random_24, d_token, d_detail, d_err, d_logits, stream, err, &dec, false);
 }
 
-uint32_t pb_lmhead_q8_decode_step(pb_context* ctx, const uint8_t* d_packed, size_t vocab,
-                                  size_t cols, const uint32_t* d_hidden, uint32_t rows,
+uint32_t pb_lmhead_q8_decode_step(pb_context* ctx, const uint8_t* d_packed,
+                                  size_t packed_bytes, size_t vocab, size_t cols, const uint32_t* d_hidden, uint32_t rows,
                                   uint32_t* d_hist, size_t hist_ld, uint32_t* d_hist_len,
                                   const uint32_t* d_max_len, uint32_t* d_row_state,
                                   const uint32_t* d_random_24, uint32_t* d_token,
@@ -588,7 +670,7 @@ uint32_t pb_lmhead_q8_decode_step(pb_context* ctx, const uint8_t* d_packed, size
   clear_error(err);
   const DecodeArgs dec{d_hist, d_hist_len, d_max_len, d_row_state};
   if (rows != 0 && !decode_args_ok(dec, err)) return PB_CAPACITY;
-  return enqueue_lmhead(ctx, d_packed, vocab, cols, d_hidden, rows, d_hist, hist_ld, d_hist_len,
+  return enqueue_lmhead(ctx, d_packed, packed_bytes, vocab, cols, d_hidden, rows, d_hist, hist_ld, d_hist_len,
                         d_random_24, d_token, d_detail, d_err, d_logits, stream, err, &dec, true);
 }
 
@@ -601,11 +683,10 @@ void pb_decode_draw(pb_sampling_state* states, const uint32_t* row_state, uint32
 }
 
 uint32_t pb_decode_settle(pb_sampling_state* states, const pb_sampling_state* saved,
-                          const uint32_t* state_before, const uint32_t* state_after,
-                          uint32_t rows) {
+                          const uint32_t* state_before, const uint32_t* tokens, uint32_t rows) {
   uint32_t restored = 0;
   for (uint32_t r = 0; r < rows; ++r) {
-    if (state_before[r] == PB_ROW_ACTIVE && state_after[r] == PB_ROW_ERROR) {
+    if (state_before[r] == PB_ROW_ACTIVE && tokens[r] == PB_NO_TOKEN) {
       states[r] = saved[r];
       ++restored;
     }
@@ -683,7 +764,8 @@ static uint32_t run_single_row(pb_context* ctx, const uint32_t* logits, const ui
   uint32_t st = enqueue_sample(ctx, ctx->d_row, PB_VOCAB, PB_VOCAB, 1,
                                with_hist ? ctx->d_hist : nullptr, ctx->hist_cap,
                                with_hist ? ctx->d_small : nullptr, ctx->d_small + 1, seen_dev,
-                               ctx->d_token, ctx->d_detail, ctx->d_err, s, &enqueue_err);
+                               ctx->d_token, ctx->d_detail, ctx->d_err, s, &enqueue_err, nullptr,
+                               true);
   if (st != PB_OK) {
     if (err) *err = enqueue_err;
     return st;

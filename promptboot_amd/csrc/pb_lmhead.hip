@@ -853,8 +853,8 @@ __global__ __launch_bounds__(64 * kSelectWaves) void lm_select_kernel(LmParams p
   const uint32_t wave = threadIdx.x >> 6;
   const uint32_t row = blockIdx.x * kSelectWaves + wave;
   if (row >= p.rows) return;
-  if (row_skipped(rp, row)) {  // decode loop: the row has ended
-    if (lane == 0) rp.token[row] = kNone;
+  if (row_skipped(rp, row)) {  // decode loop: the row has ended or has no room
+    if (lane == 0) skip_row(rp, row);
     return;
   }
   const uint32_t bad_logit = p.meta[row * 2 + 0];
@@ -973,6 +973,7 @@ __global__ __launch_bounds__(64) void mfma_selftest_kernel(int32_t* out) {
 
 hipError_t launch_lm_pack(const uint8_t* in, uint8_t* out, uint32_t vocab, uint32_t blocks,
                           hipStream_t stream) {
+  (void)hipGetLastError();  // report only this call's launch errors
   const size_t n = (size_t)vocab * blocks;
   // the tile flags start at zero: a fill kernel rather than a memset, which a
   // caller capturing the repack in a graph could not replay reliably
@@ -986,6 +987,7 @@ hipError_t launch_lm_pack(const uint8_t* in, uint8_t* out, uint32_t vocab, uint3
 
 hipError_t launch_lm_pack_q8(const uint8_t* in, uint8_t* out, uint32_t vocab, uint32_t blocks,
                              hipStream_t stream) {
+  (void)hipGetLastError();  // report only this call's launch errors
   const size_t n = (size_t)vocab * blocks;
   hipLaunchKernelGGL(lm_pack_q8_kernel, dim3((uint32_t)((n + kBlockThreads - 1) / kBlockThreads)),
                      dim3(kBlockThreads), 0, stream, in, out, vocab, blocks);
@@ -997,6 +999,7 @@ size_t gemm_lds_bytes(uint32_t cols) {
 }
 
 hipError_t launch_lm_sample(const LmParams& p, const RowParams& rp, hipStream_t stream) {
+  (void)hipGetLastError();  // report only this call's launch errors
   hipLaunchKernelGGL(lm_prep_kernel, dim3(p.rows_pad), dim3(kBlockThreads), 0, stream, p);
   if (p.rows <= kNarrowRows) {
     // Measured (Q4_0 step, us): one row tile with loads three blocks ahead
@@ -1041,6 +1044,7 @@ hipError_t launch_lm_sample(const LmParams& p, const RowParams& rp, hipStream_t 
 }
 
 hipError_t launch_mfma_selftest(int32_t* out, hipStream_t stream) {
+  (void)hipGetLastError();  // report only this call's launch errors
   hipLaunchKernelGGL(mfma_selftest_kernel, dim3(1), dim3(64), 0, stream, out);
   return hipGetLastError();
 }

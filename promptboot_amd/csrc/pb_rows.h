@@ -33,9 +33,30 @@ __device__ __forceinline__ uint32_t row_word(const uint32_t* ptr) {
   return *(const __attribute__((address_space(4))) uint32_t*)ptr;
 }
 
-// True when a launch in decode-loop mode must skip `row` (not active).
+// Context cap of a row in decode-loop mode: max_len[row], at most hist_ld.
+__device__ __forceinline__ uint32_t row_cap(const RowParams& p, uint32_t row) {
+  uint32_t cap = (uint32_t)p.hist_ld;
+  if (p.max_len != nullptr) {
+    const uint32_t m = row_word(p.max_len + row);
+    cap = m < cap ? m : cap;
+  }
+  return cap;
+}
+
+// True when a launch in decode-loop mode must skip `row`: the row has ended,
+// or its context is already at its cap (the REPL never samples without room).
 __device__ __forceinline__ bool row_skipped(const RowParams& p, uint32_t row) {
-  return p.row_state != nullptr && row_word(p.row_state + row) != PB_ROW_ACTIVE;
+  if (p.row_state == nullptr) return false;
+  if (row_word(p.row_state + row) != PB_ROW_ACTIVE) return true;
+  return row_word(p.hist_len_out + row) >= row_cap(p, row);
+}
+
+// Outputs of a skipped row (one lane): no token; a row that was still active
+// (its context is full) ends at its limit.  Its detail and error records are
+// not written.
+__device__ __forceinline__ void skip_row(const RowParams& p, uint32_t row) {
+  p.token[row] = kNone;
+  if (row_word(p.row_state + row) == PB_ROW_ACTIVE) p.row_state[row] = PB_ROW_LIMIT;
 }
 
 // Decode-loop bookkeeping after a row's sample (one lane): the working

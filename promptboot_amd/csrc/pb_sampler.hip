@@ -124,8 +124,8 @@ __global__ __launch_bounds__(kBlock) void segment_kernel(RowParams p) {
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = tid & 63u;
   const uint32_t wave = tid >> 6;
-  if (row_skipped(p, row)) {  // decode loop: the row has ended
-    if (seg == 0 && tid == 0) p.token[row] = kNone;
+  if (row_skipped(p, row)) {  // decode loop: the row has ended or has no room
+    if (seg == 0 && tid == 0) skip_row(p, row);
     return;
   }
 
@@ -497,7 +497,7 @@ __global__ __launch_bounds__(64 * kFinishWaves) void finish_kernel(RowParams p) 
   const uint32_t wave = threadIdx.x >> 6;
   const uint32_t row = blockIdx.x * kFinishWaves + wave;
   if (row >= p.rows) return;
-  if (row_skipped(p, row)) return;  // decode loop: the token is already PB_NO_TOKEN
+  if (row_skipped(p, row)) return;  // decode loop: segment_kernel wrote the skipped row
   // every load of the S lists and slice records is issued before the first wait
   constexpr uint32_t kStage = (kMaxSegments * kTopK + 63) / 64;
   uint64_t* st = staged[wave];
@@ -593,6 +593,7 @@ void plan_segments(uint32_t rows, uint32_t forced_segments, uint32_t* segs, uint
 }
 
 hipError_t launch_sample(const RowParams& p, hipStream_t stream) {
+  (void)hipGetLastError();  // report only this call's launch errors
   const uint32_t blocks = p.rows * p.segs;
   if (p.segs == 1) {
     hipLaunchKernelGGL((segment_kernel<kChunkF4, true>), dim3(blocks), dim3(kBlock), 0, stream, p);
@@ -629,6 +630,7 @@ __global__ __launch_bounds__(64) void wave_selftest_kernel(uint32_t* out) {
 }
 
 hipError_t launch_wave_selftest(uint32_t* out, hipStream_t stream) {
+  (void)hipGetLastError();  // report only this call's launch errors
   hipLaunchKernelGGL(wave_selftest_kernel, dim3(1), dim3(64), 0, stream, out);
   return hipGetLastError();
 }
@@ -644,6 +646,7 @@ __global__ __launch_bounds__(kBlock) void probe_kernel(int which, const uint32_t
 
 hipError_t launch_probe(int which, const uint32_t* in, uint32_t* out, size_t n,
                         hipStream_t stream) {
+  (void)hipGetLastError();  // report only this call's launch errors
   if (n == 0) return hipSuccess;
   const size_t blocks = (n + kBlock - 1) / kBlock;
   hipLaunchKernelGGL(probe_kernel, dim3((uint32_t)blocks), dim3(kBlock), 0, stream, which, in,
@@ -652,6 +655,7 @@ hipError_t launch_probe(int which, const uint32_t* in, uint32_t* out, size_t n,
 }
 
 hipError_t launch_writeback(const WritebackParams& p, hipStream_t stream) {
+  (void)hipGetLastError();  // report only this call's launch errors
   hipLaunchKernelGGL(writeback_kernel, dim3(p.rows), dim3(kBlock), 0, stream, p);
   return hipGetLastError();
 }

@@ -14,8 +14,12 @@ Rust's `Result<T, InferenceError>` becomes a return value or a raised
 (binary32 bit patterns) as in the reference; float32 arrays are accepted and
 viewed as words.
 
-`BatchSampler` drives the batched device entry points on torch device
-tensors (torch is used for device memory and streams only).
+`BatchSampler` and `DecodeBatch` drive the batched device entry points on
+device buffers: `promptboot_amd.hip.DeviceArray`, raw device pointers, or any
+array object with `data_ptr()` and a shape (tensors of another framework
+that shares this process's HIP runtime).  Streams are hipStream_t handles
+(`hip.Stream`, an int, or an object with `cuda_stream`); None is the null
+stream.
 
 All selection arithmetic runs in the HIP kernels; if the library is missing
 the import fails.
@@ -26,6 +30,8 @@ import ctypes
 import pathlib
 
 import numpy as np
+
+from . import hip
 
 VOCAB = 151_936
 TOP_K = 20
@@ -97,6 +103,7 @@ EXPORTS = {
     "pb_top_logits_8": (u32, [vp, size_t, vp, ctypes.POINTER(_Error)]),
     "pb_context_create": (u32, [ctypes.c_int, ctypes.POINTER(vp)]),
     "pb_context_destroy": (None, [vp]),
+    "pb_context_reserve": (u32, [vp, u32, size_t, ctypes.POINTER(_Error)]),
     "pb_sample_batch": (
         u32, [vp, vp, size_t, size_t, u32, vp, size_t, vp, vp, vp, vp, vp, vp,
               ctypes.POINTER(_Error)]),
@@ -112,22 +119,22 @@ EXPORTS = {
     "pb_lmhead_packed_bytes": (size_t, [size_t, size_t]),
     "pb_lmhead_pack_q4_0": (u32, [vp, size_t, size_t, vp, vp, ctypes.POINTER(_Error)]),
     "pb_lmhead_sample_batch": (
-        u32, [vp, vp, size_t, size_t, vp, u32, vp, size_t, vp, vp, vp, vp, vp, vp, vp,
+        u32, [vp, vp, size_t, size_t, size_t, vp, u32, vp, size_t, vp, vp, vp, vp, vp, vp, vp,
               ctypes.POINTER(_Error)]),
     "pb_decode_step": (
         u32, [vp, vp, size_t, size_t, u32, vp, size_t, vp, vp, vp, vp, vp, vp, vp, vp,
               ctypes.POINTER(_Error)]),
     "pb_lmhead_decode_step": (
-        u32, [vp, vp, size_t, size_t, vp, u32, vp, size_t, vp, vp, vp, vp, vp, vp, vp, vp,
-              vp, ctypes.POINTER(_Error)]),
+        u32, [vp, vp, size_t, size_t, size_t, vp, u32, vp, size_t, vp, vp, vp, vp, vp, vp, vp,
+              vp, vp, ctypes.POINTER(_Error)]),
     "pb_lmhead_q8_packed_bytes": (size_t, [size_t, size_t]),
     "pb_lmhead_pack_q8_0": (u32, [vp, size_t, size_t, vp, vp, ctypes.POINTER(_Error)]),
     "pb_lmhead_q8_sample_batch": (
-        u32, [vp, vp, size_t, size_t, vp, u32, vp, size_t, vp, vp, vp, vp, vp, vp, vp,
+        u32, [vp, vp, size_t, size_t, size_t, vp, u32, vp, size_t, vp, vp, vp, vp, vp, vp, vp,
               ctypes.POINTER(_Error)]),
     "pb_lmhead_q8_decode_step": (
-        u32, [vp, vp, size_t, size_t, vp, u32, vp, size_t, vp, vp, vp, vp, vp, vp, vp, vp,
-              vp, ctypes.POINTER(_Error)]),
+        u32, [vp, vp, size_t, size_t, size_t, vp, u32, vp, size_t, vp, vp, vp, vp, vp, vp, vp,
+              vp, vp, ctypes.POINTER(_Error)]),
     "pb_decode_draw": (None, [vp, vp, u32, vp, vp]),
     "pb_decode_settle": (u32, [vp, vp, vp, vp, u32]),
     "pb_version": (ctypes.c_char_p, []),
@@ -137,23 +144,15 @@ _lib = None
 
 
 def lib() -> ctypes.CDLL:
-    """Loads libpbsample.so; raises if it was not built (no fallback path)."""
+    """Loads libpbsample.so; raises if it was not built (no fallback path).
+
+    The library links the HIP runtime by SONAME (libamdhip64.so.7); when the
+    process already mapped a runtime of that name, the library shares it."""
     global _lib
     if _lib is None:
         if not LIB_PATH.exists():
             raise ImportError(f"{LIB_PATH} is missing: build it with "
                               "`make -C promptboot_amd/csrc` (hipcc, gfx950)")
-        # One HIP runtime per process: torch wheels bundle their own
-        # libamdhip64 (SONAME libamdhip64.so.7, but requested by torch as
-        # "libamdhip64.so").  Loaded first, it satisfies this library's
-        # libamdhip64.so.7 dependency as well; loaded after /opt/rocm's copy,
-        # torch would map a second runtime that finds no GPU.  So torch, when
-        # installed, is imported before the library is opened; torch stream
-        # handles are then valid for the sampler's launches.
-        try:
-            import torch  # noqa: F401
-        except ImportError:
-            pass
         L = ctypes.CDLL(str(LIB_PATH))
         for name, (res, args) in EXPORTS.items():
             fn = getattr(L, name)
@@ -282,24 +281,66 @@ def top_logits_8(logits, output: np.ndarray | None = None) -> np.ndarray:
 
 def fill_random_24(states: list[SamplingState]) -> np.ndarray:
     """One next_24 per row from the rows' own generators (host)."""
-    return np.array([s.next_24() for s in states], np.uint32)
+    return np.array([st.next_24() for st in states], np.uint32)
+
+
+# ---- device buffers handed to the batched entry points ----
+
+def _shape(x) -> tuple:
+    return tuple(int(d) for d in x.shape)
+
+
+def _itemsize(x) -> int:
+    return int(x.element_size()) if hasattr(x, "element_size") else int(x.dtype.itemsize)
+
+
+def _dev(x, name: str, *, itemsize: int = 4, rows: int | None = None,
+         row_elems: int | None = None, ndim: int | None = None):
+    """The device pointer of `x` (None stays None).  Array objects are checked:
+    C-contiguous, `itemsize`-byte elements, `ndim` dimensions when given, and
+    at least rows x row_elems elements.  A raw int pointer is taken as is."""
+    if x is None:
+        return None
+    if isinstance(x, int):
+        return vp(x)
+    if hasattr(x, "is_contiguous") and not x.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    if _itemsize(x) != itemsize:
+        raise ValueError(f"{name} must have {itemsize}-byte elements, not {_itemsize(x)}")
+    shape = _shape(x)
+    if ndim is not None and len(shape) != ndim:
+        raise ValueError(f"{name} must have {ndim} dimensions, has shape {shape}")
+    if rows is not None:
+        need = rows * (row_elems if row_elems is not None else 1)
+        have = int(np.prod(shape, dtype=np.int64))
+        if have < need:
+            raise ValueError(f"{name} holds {have} elements, {need} needed for {rows} rows")
+    return vp(x.data_ptr())
+
+
+def _nbytes(x) -> int:
+    return int(np.prod(_shape(x), dtype=np.int64)) * _itemsize(x)
 
 
 class BatchSampler:
     """Batched device sampling on one GPU (pb_context).
 
-    Tensors are torch CUDA tensors (int32/uint32-compatible words):
-    logits [B, ld] (float32 or int32 view), history [B, hist_ld] int32,
-    history lengths [B] int32, uniforms [B] int32."""
+    Device buffers hold 32-bit words: logits [B, ld] (binary32 bit patterns),
+    history [B, hist_ld], history lengths [B], uniforms [B]; outputs token
+    [B], detail [B, 84] (DETAIL_DTYPE), err [B, 12] (ERROR_DTYPE).  The
+    context's workspace is reserved (pb_context_reserve) before any call
+    that needs more, so the enqueue calls themselves never allocate."""
 
     def __init__(self, device: int = -1, segments: int = 0):
         self._ctx = vp()
         st = lib().pb_context_create(device, ctypes.byref(self._ctx))
         if st != OK:
             raise InferenceError(_Error(status=st))
-        self.segments = segments
+        self.segments = 0
+        self._rows = 0          # rows reserved under the current slice plan
+        self._lm = (0, 0)       # (rows, cols) reserved for the LM head
         if segments:
-            lib().pb_context_set_segments(self._ctx, segments)
+            self.set_segments(segments)
 
     def close(self):
         if self._ctx:
@@ -315,72 +356,95 @@ class BatchSampler:
     def set_segments(self, segments: int) -> None:
         self.segments = segments
         lib().pb_context_set_segments(self._ctx, segments)
+        self._rows = 0
+
+    def reserve(self, rows: int, cols: int = 0) -> None:
+        """Sizes the context for batches of up to `rows` rows (and the LM head
+        for up to `cols` columns); a set-up call, it may allocate."""
+        e = _Error()
+        _check(lib().pb_context_reserve(self._ctx, rows, cols, ctypes.byref(e)), e)
+        self._rows = max(self._rows, rows)
+        if cols:
+            self._lm = (max(self._lm[0], rows), max(self._lm[1], cols))
+
+    def _ensure(self, rows: int, cols: int = 0) -> None:
+        if self.segments and rows > self._rows:
+            self.reserve(rows)
+        if cols and (rows > self._lm[0] or cols > self._lm[1]):
+            self.reserve(max(rows, self._lm[0]), max(cols, self._lm[1]))
 
     def sample(self, logits, random_24, history=None, history_len=None, *, token=None,
                detail=None, err=None, inplace=False, seen=None, stream=None) -> None:
-        """Enqueues one batched sample; outputs are preallocated torch tensors:
-        token [B] int32, detail [B, 84] int32 (DETAIL_DTYPE), err [B, 12] int32."""
-        import torch
-
-        rows, ld = logits.shape
-        hist_ld = history.shape[1] if history is not None else 0
-        s = stream if stream is not None else torch.cuda.current_stream(logits.device)
+        """Enqueues one batched sample on `stream`."""
+        rows, ld = _shape(logits)
+        hist_ld = _shape(history)[1] if history is not None else 0
+        self._ensure(rows)
+        args = dict(rows=rows)
+        ptrs = [_dev(logits, "logits", ndim=2), _dev(history, "history", ndim=2, **args),
+                _dev(history_len, "history_len", **args), _dev(random_24, "random_24", **args)]
+        outs = [_dev(token, "token", **args), _dev(detail, "detail", row_elems=84, **args),
+                _dev(err, "err", row_elems=12, **args)]
         e = _Error()
-
-        def p(t):
-            return None if t is None else ctypes.c_void_p(t.data_ptr())
-
+        s = vp(hip.stream_handle(stream))
         if inplace:
             st = lib().pb_sample_batch_inplace(
-                self._ctx, p(logits), VOCAB, ld, rows, p(history), hist_ld, p(history_len),
-                p(random_24), p(seen), p(token), p(detail), p(err),
-                ctypes.c_void_p(s.cuda_stream), ctypes.byref(e))
-        else:
-            st = lib().pb_sample_batch(
-                self._ctx, p(logits), VOCAB, ld, rows, p(history), hist_ld, p(history_len),
-                p(random_24), p(token), p(detail), p(err), ctypes.c_void_p(s.cuda_stream),
+                self._ctx, ptrs[0], VOCAB, ld, rows, ptrs[1], hist_ld, ptrs[2], ptrs[3],
+                _dev(seen, "seen", itemsize=1, rows=rows, row_elems=SEEN_BYTES), *outs, s,
                 ctypes.byref(e))
+        else:
+            st = lib().pb_sample_batch(self._ctx, ptrs[0], VOCAB, ld, rows, ptrs[1], hist_ld,
+                                       ptrs[2], ptrs[3], *outs, s, ctypes.byref(e))
         _check(st, e)
 
     def pack_lmhead(self, weights, vocab: int = VOCAB, cols: int = 896, stream=None,
-                    q8: bool = False):
-        """Repacks a Q4_0 head (or, with q8, a Q8_0 head) given as a torch uint8
-        device tensor in promptboot's layout into the device layout; returns
-        the packed uint8 tensor."""
-        import torch
-
+                    q8: bool = False) -> hip.DeviceArray:
+        """Repacks a Q4_0 head (or, with q8, a Q8_0 head) held on the device in
+        promptboot's layout into the device layout; returns the packed bytes."""
+        src = vocab * (cols // 32) * (34 if q8 else 18)
+        if _nbytes(weights) != src:
+            raise ValueError(f"a {'Q8_0' if q8 else 'Q4_0'} head of {vocab} x {cols} is "
+                             f"{src} bytes, not {_nbytes(weights)}")
         nbytes = (lib().pb_lmhead_q8_packed_bytes if q8 else lib().pb_lmhead_packed_bytes)(
             vocab, cols)
-        packed = torch.empty(nbytes, dtype=torch.uint8, device=weights.device)
-        s = stream if stream is not None else torch.cuda.current_stream(weights.device)
+        packed = hip.DeviceArray(nbytes, np.uint8)
         e = _Error()
         pack = lib().pb_lmhead_pack_q8_0 if q8 else lib().pb_lmhead_pack_q4_0
-        st = pack(ctypes.c_void_p(weights.data_ptr()), vocab, cols,
-                  ctypes.c_void_p(packed.data_ptr()), ctypes.c_void_p(s.cuda_stream),
-                  ctypes.byref(e))
+        st = pack(_dev(weights, "weights", itemsize=_itemsize(weights)), vocab, cols,
+                  vp(packed.data_ptr()), vp(hip.stream_handle(stream)), ctypes.byref(e))
         _check(st, e)
         return packed
 
+    @staticmethod
+    def _head_args(packed, hidden, cols, q8):
+        rows, width = _shape(hidden)
+        if cols is not None and cols != width:
+            raise ValueError(f"cols={cols} but the hidden states have {width} columns")
+        nbytes = (lib().pb_lmhead_q8_packed_bytes if q8 else lib().pb_lmhead_packed_bytes)(
+            VOCAB, width)
+        if _nbytes(packed) != nbytes:
+            raise ValueError(f"the packed head holds {_nbytes(packed)} bytes; a "
+                             f"{'Q8_0' if q8 else 'Q4_0'} head of width {width} holds {nbytes}")
+        return rows, width, nbytes
+
     def lmhead_sample(self, packed, hidden, random_24, history=None, history_len=None, *,
-                      token, detail=None, err=None, logits=None, cols: int = 896,
+                      token, detail=None, err=None, logits=None, cols: int | None = None,
                       stream=None, q8: bool = False) -> None:
         """Enqueues the fused Q4_0 (or, with q8, Q8_0) LM head + sampler for
         hidden [B, cols]; `packed` comes from pack_lmhead with the same q8."""
-        import torch
-
-        rows = hidden.shape[0]
-        hist_ld = history.shape[1] if history is not None else 0
-        s = stream if stream is not None else torch.cuda.current_stream(hidden.device)
-        e = _Error()
-
-        def p(t):
-            return None if t is None else ctypes.c_void_p(t.data_ptr())
-
+        rows, width, nbytes = self._head_args(packed, hidden, cols, q8)
+        self._ensure(rows, width)
+        hist_ld = _shape(history)[1] if history is not None else 0
+        args = dict(rows=rows)
         fn = lib().pb_lmhead_q8_sample_batch if q8 else lib().pb_lmhead_sample_batch
-        st = fn(
-            self._ctx, p(packed), VOCAB, cols, p(hidden), rows, p(history), hist_ld,
-            p(history_len), p(random_24), p(token), p(detail), p(err), p(logits),
-            ctypes.c_void_p(s.cuda_stream), ctypes.byref(e))
+        e = _Error()
+        st = fn(self._ctx, _dev(packed, "packed", itemsize=1), nbytes, VOCAB, width,
+                _dev(hidden, "hidden", ndim=2), rows, _dev(history, "history", ndim=2, **args),
+                hist_ld, _dev(history_len, "history_len", **args),
+                _dev(random_24, "random_24", **args), _dev(token, "token", **args),
+                _dev(detail, "detail", row_elems=84, **args),
+                _dev(err, "err", row_elems=12, **args),
+                _dev(logits, "logits", row_elems=VOCAB, **args), vp(hip.stream_handle(stream)),
+                ctypes.byref(e))
         _check(st, e)
 
     def sample_rows(self, logits, history, history_len, states: list[SamplingState],
@@ -389,23 +453,23 @@ class BatchSampler:
         without the in-place write-back: one draw per row from that row's own
         state; failing rows keep their state (transactional).  Returns numpy
         (tokens, detail or None, errors)."""
-        import torch
-
-        rows = logits.shape[0]
-        before = [s.copy() for s in states]
-        r24 = torch.from_numpy(fill_random_24(states).view(np.int32)).to(logits.device)
-        token = torch.empty(rows, dtype=torch.int32, device=logits.device)
-        det = (torch.empty((rows, DETAIL_DTYPE.itemsize // 4), dtype=torch.int32,
-                           device=logits.device) if want_detail else None)
-        err = torch.empty((rows, ERROR_DTYPE.itemsize // 4), dtype=torch.int32,
-                          device=logits.device)
-        self.sample(logits, r24, history, history_len, token=token, detail=det, err=err)
-        torch.cuda.synchronize(logits.device)
-        tok = token.cpu().numpy().view(np.uint32)
-        errs = err.cpu().numpy().view(ERROR_DTYPE).reshape(rows)
+        rows = _shape(logits)[0]
+        before = [st.copy() for st in states]
+        r24 = hip.DeviceArray.from_numpy(fill_random_24(states))
+        token = hip.DeviceArray(rows, np.uint32)
+        det = hip.DeviceArray((rows, DETAIL_DTYPE.itemsize // 4), np.uint32) if want_detail else None
+        err = hip.DeviceArray((rows, ERROR_DTYPE.itemsize // 4), np.uint32)
+        try:
+            self.sample(logits, r24, history, history_len, token=token, detail=det, err=err)
+        except Exception:
+            for r in range(rows):
+                states[r]._s = before[r]._s
+            raise
+        tok = token.numpy()
+        errs = err.numpy().view(ERROR_DTYPE).reshape(rows)
         for r in np.flatnonzero(errs["status"] != OK):
             states[r]._s = before[r]._s
-        dets = det.cpu().numpy().view(DETAIL_DTYPE).reshape(rows) if want_detail else None
+        dets = det.numpy().view(DETAIL_DTYPE).reshape(rows) if want_detail else None
         return tok, dets, errs
 
 
@@ -416,16 +480,13 @@ class DecodeBatch:
     Each row owns a working context (prompt, then every generated token; an
     end-of-sequence piece is stored as IM_END), a length cap (prompt length +
     generation limit) and its own SamplingState, advanced once per sampled
-    token and never for a failed sample.  The contexts, lengths and row states
-    stay on the device; the host keeps the generators (pb_decode_draw /
-    pb_decode_settle)."""
+    token and never for a failed sample or a row already at its cap.  The
+    contexts, lengths and row states stay on the device; the host keeps the
+    generators (pb_decode_draw / pb_decode_settle)."""
 
     def __init__(self, prompts, seeds, limits, capacity: int | None = None, device: int = 0,
                  sampler: "BatchSampler | None" = None):
-        import torch
-
         self.rows = len(prompts)
-        self.dev = torch.device(f"cuda:{device}")
         cap = max(len(p) + int(g) for p, g in zip(prompts, limits))
         self.hist_ld = int(capacity) if capacity is not None else (cap + 3) // 4 * 4
         hist = np.zeros((self.rows, self.hist_ld), np.uint32)
@@ -433,10 +494,9 @@ class DecodeBatch:
             hist[r, :len(p)] = np.asarray(p, np.uint32)
         lens = np.array([len(p) for p in prompts], np.uint32)
         max_len = np.minimum(lens + np.asarray(limits, np.uint32), self.hist_ld).astype(np.uint32)
-
-        def dev(a):
-            return torch.from_numpy(np.ascontiguousarray(a).view(np.int32)).to(self.dev)
-
+        self._own = sampler is None
+        self.sampler = sampler if sampler is not None else BatchSampler(device)
+        dev = hip.DeviceArray.from_numpy
         self.hist, self.hist_len, self.max_len = dev(hist), dev(lens), dev(max_len)
         self.row_state_host = np.where(lens < max_len, ROW_ACTIVE, ROW_LIMIT).astype(np.uint32)
         self.row_state = dev(self.row_state_host)
@@ -444,11 +504,9 @@ class DecodeBatch:
         for r, seed in enumerate(seeds):
             lib().pb_sampling_state_new(ctypes.byref(self.states[r]), int(seed) & (2**64 - 1))
         self._saved = (_State * self.rows)()
-        self.token = torch.empty(self.rows, dtype=torch.int32, device=self.dev)
-        self.err = torch.empty((self.rows, ERROR_DTYPE.itemsize // 4), dtype=torch.int32,
-                               device=self.dev)
-        self._own = sampler is None
-        self.sampler = sampler if sampler is not None else BatchSampler(device)
+        self.r24 = hip.DeviceArray(self.rows, np.uint32)
+        self.token = hip.DeviceArray(self.rows, np.uint32)
+        self.err = hip.DeviceArray((self.rows, ERROR_DTYPE.itemsize // 4), np.uint32)
 
     def close(self):
         if self._own and self.sampler is not None:
@@ -459,93 +517,97 @@ class DecodeBatch:
         return bool((self.row_state_host == ROW_ACTIVE).any())
 
     def _draw(self):
-        import torch
-
         r24 = np.zeros(self.rows, np.uint32)
         before = self.row_state_host.copy()
         lib().pb_decode_draw(self.states, before.ctypes.data_as(vp), self.rows,
                              r24.ctypes.data_as(vp), self._saved)
-        return before, torch.from_numpy(r24.view(np.int32)).to(self.dev)
+        self.r24.upload(r24)
+        return before
+
+    def _undraw(self):
+        for r in range(self.rows):
+            self.states[r] = self._saved[r]
 
     def _settle(self, before):
-        import torch
-
-        torch.cuda.synchronize(self.dev)
-        after = self.row_state.cpu().numpy().view(np.uint32).copy()
+        after = self.row_state.numpy()
+        tokens = self.token.numpy()
         lib().pb_decode_settle(self.states, self._saved, before.ctypes.data_as(vp),
-                               after.ctypes.data_as(vp), self.rows)
+                               tokens.ctypes.data_as(vp), self.rows)
         self.row_state_host = after
-        return self.token.cpu().numpy().view(np.uint32).copy()
+        return tokens.copy()
+
+    def _ptrs(self):
+        return (vp(self.hist.data_ptr()), self.hist_ld, vp(self.hist_len.data_ptr()),
+                vp(self.max_len.data_ptr()), vp(self.row_state.data_ptr()),
+                vp(self.r24.data_ptr()), vp(self.token.data_ptr()), None,
+                vp(self.err.data_ptr()))
 
     def step(self, logits, stream=None) -> np.ndarray:
         """One step on logits [rows, ld] (rows that have ended are ignored).
-        Returns the tokens (NO_TOKEN for rows not sampled)."""
-        import torch
-
-        before, r24 = self._draw()
-        s = stream if stream is not None else torch.cuda.current_stream(self.dev)
+        Returns the tokens (NO_TOKEN for rows not sampled).  A refused step
+        leaves every SamplingState as it was."""
+        rows, ld = _shape(logits)
+        if rows != self.rows:
+            raise ValueError(f"logits have {rows} rows, the batch has {self.rows}")
+        lp = _dev(logits, "logits", ndim=2)
+        before = self._draw()
         e = _Error()
-        st = lib().pb_decode_step(
-            self.sampler._ctx, ctypes.c_void_p(logits.data_ptr()), VOCAB, logits.shape[1],
-            self.rows, ctypes.c_void_p(self.hist.data_ptr()), self.hist_ld,
-            ctypes.c_void_p(self.hist_len.data_ptr()), ctypes.c_void_p(self.max_len.data_ptr()),
-            ctypes.c_void_p(self.row_state.data_ptr()), ctypes.c_void_p(r24.data_ptr()),
-            ctypes.c_void_p(self.token.data_ptr()), None, ctypes.c_void_p(self.err.data_ptr()),
-            ctypes.c_void_p(s.cuda_stream), ctypes.byref(e))
-        _check(st, e)
+        try:
+            st = lib().pb_decode_step(self.sampler._ctx, lp, VOCAB, ld, self.rows, *self._ptrs(),
+                                      vp(hip.stream_handle(stream)), ctypes.byref(e))
+            _check(st, e)
+        except Exception:
+            self._undraw()
+            raise
         return self._settle(before)
 
-    def lmhead_step(self, packed, hidden, cols: int = 896, stream=None,
+    def lmhead_step(self, packed, hidden, cols: int | None = None, stream=None,
                     q8: bool = False) -> np.ndarray:
         """One step through the fused Q4_0 (or, with q8, Q8_0) LM head on
         hidden [rows, cols]."""
-        import torch
-
-        before, r24 = self._draw()
-        s = stream if stream is not None else torch.cuda.current_stream(self.dev)
-        e = _Error()
+        rows, width, nbytes = BatchSampler._head_args(packed, hidden, cols, q8)
+        if rows != self.rows:
+            raise ValueError(f"hidden has {rows} rows, the batch has {self.rows}")
+        self.sampler._ensure(rows, width)
+        pp, hp = _dev(packed, "packed", itemsize=1), _dev(hidden, "hidden", ndim=2)
+        before = self._draw()
         fn = lib().pb_lmhead_q8_decode_step if q8 else lib().pb_lmhead_decode_step
-        st = fn(
-            self.sampler._ctx, ctypes.c_void_p(packed.data_ptr()), VOCAB, cols,
-            ctypes.c_void_p(hidden.data_ptr()), self.rows,
-            ctypes.c_void_p(self.hist.data_ptr()), self.hist_ld,
-            ctypes.c_void_p(self.hist_len.data_ptr()), ctypes.c_void_p(self.max_len.data_ptr()),
-            ctypes.c_void_p(self.row_state.data_ptr()), ctypes.c_void_p(r24.data_ptr()),
-            ctypes.c_void_p(self.token.data_ptr()), None, ctypes.c_void_p(self.err.data_ptr()),
-            None, ctypes.c_void_p(s.cuda_stream), ctypes.byref(e))
-        _check(st, e)
+        e = _Error()
+        try:
+            p = self._ptrs()
+            st = fn(self.sampler._ctx, pp, nbytes, VOCAB, width, hp, self.rows, *p, None,
+                    vp(hip.stream_handle(stream)), ctypes.byref(e))
+            _check(st, e)
+        except Exception:
+            self._undraw()
+            raise
         return self._settle(before)
 
     def contexts(self) -> list[np.ndarray]:
-        h = self.hist.cpu().numpy().view(np.uint32)
-        n = self.hist_len.cpu().numpy().view(np.uint32)
+        h = self.hist.numpy()
+        n = self.hist_len.numpy()
         return [h[r, :n[r]].copy() for r in range(self.rows)]
 
     def errors(self) -> np.ndarray:
-        return self.err.cpu().numpy().view(ERROR_DTYPE).reshape(self.rows)
+        return self.err.numpy().view(ERROR_DTYPE).reshape(self.rows)
 
     def sampling_states(self) -> list[SamplingState]:
-        return [SamplingState.from_parts(s.state, s.draws) for s in self.states]
+        return [SamplingState.from_parts(st.state, st.draws) for st in self.states]
 
 
 def device_expf_bits(inp, out, stream=None) -> None:
-    """Runs the sampler's device expf on a torch CUDA int32 tensor (verification hook)."""
-    import torch
-
-    s = stream if stream is not None else torch.cuda.current_stream(inp.device)
-    st = lib().pb_device_expf_bits(ctypes.c_void_p(inp.data_ptr()), ctypes.c_void_p(out.data_ptr()),
-                                   inp.numel(), ctypes.c_void_p(s.cuda_stream))
+    """Runs the sampler's device expf on device words (verification hook)."""
+    n = int(np.prod(_shape(inp), dtype=np.int64))
+    st = lib().pb_device_expf_bits(_dev(inp, "inp"), _dev(out, "out", rows=n), n,
+                                   vp(hip.stream_handle(stream)))
     if st != OK:
         raise RuntimeError("pb_device_expf_bits failed")
 
 
 def device_penalize_bits(inp, out, stream=None) -> None:
     """Runs the sampler's device repetition penalty of single logits (verification hook)."""
-    import torch
-
-    s = stream if stream is not None else torch.cuda.current_stream(inp.device)
-    st = lib().pb_device_penalize_bits(ctypes.c_void_p(inp.data_ptr()),
-                                       ctypes.c_void_p(out.data_ptr()), inp.numel(),
-                                       ctypes.c_void_p(s.cuda_stream))
+    n = int(np.prod(_shape(inp), dtype=np.int64))
+    st = lib().pb_device_penalize_bits(_dev(inp, "inp"), _dev(out, "out", rows=n), n,
+                                       vp(hip.stream_handle(stream)))
     if st != OK:
         raise RuntimeError("pb_device_penalize_bits failed")

@@ -5,6 +5,14 @@ import sys
 import numpy as np
 import pytest
 
+# Some GPU tests build their inputs with torch.  torch bundles its own HIP
+# runtime, so it is imported before libpbsample.so opens one: the library and
+# promptboot_amd.hip then share torch's copy (one runtime per process).
+try:
+    import torch  # noqa: F401
+except ImportError:
+    pass
+
 ROOT = pathlib.Path(__file__).resolve().parents[1]
 GOLDEN = ROOT / "tests" / "golden"
 if str(ROOT) not in sys.path:

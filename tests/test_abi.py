@@ -119,9 +119,17 @@ def test_version_and_segment_plan():
     assert s.lib().pb_segments_for_rows(1) <= 64
 
 
+def _state_after_one(seed: int) -> int:
+    st = s.SamplingState(seed)
+    st.next_24()
+    return st.state()
+
+
 def test_decode_draw_and_settle_keep_one_draw_per_sampled_token():
     """Host side of the decode step: one next_24 per active row; a row that
-    failed gets its state back (inference.rs:954-963: no draw on error)."""
+    was active and got no token -- it failed, or its context was already
+    full -- gets its state back (inference.rs:954-963: no draw on error; the
+    REPL does not sample without room)."""
     import ctypes
 
     rows = 5
@@ -142,11 +150,13 @@ def test_decode_draw_and_settle_keep_one_draw_per_sampled_token():
             assert r24[r] == 0
         assert (states[r].state, states[r].draws) == (ref.state(), ref.draws())
         assert (saved[r].state, saved[r].draws) == (s.SamplingState(42 + r).state(), 0)
-    after = np.array([s.ROW_ERROR, s.ROW_EOS, s.ROW_ACTIVE, s.ROW_ERROR, s.ROW_EOS], np.uint32)
+    # row 0 failed, row 2 sampled, row 4 was full; rows 1 and 3 were not active
+    tokens = np.array([s.NO_TOKEN, s.NO_TOKEN, 123, s.NO_TOKEN, s.NO_TOKEN], np.uint32)
     n = s.lib().pb_decode_settle(states, saved, before.ctypes.data_as(ctypes.c_void_p),
-                                 after.ctypes.data_as(ctypes.c_void_p), rows)
-    assert n == 1  # row 3 was not active, so it drew nothing and has nothing to restore
-    assert [states[r].draws for r in range(rows)] == [0, 0, 1, 0, 1]
+                                 tokens.ctypes.data_as(ctypes.c_void_p), rows)
+    assert n == 2  # rows 1 and 3 drew nothing and have nothing to restore
+    assert [states[r].draws for r in range(rows)] == [0, 0, 1, 0, 0]
+    assert states[2].state == _state_after_one(44)
 
 
 def test_decode_step_argument_errors_need_no_device():
@@ -179,3 +189,29 @@ def test_lmhead_pack_argument_errors_need_no_device():
     # the source matrices, plus the Q4_0 layout's flag word per 64-id tile
     assert s.lib().pb_lmhead_packed_bytes(s.VOCAB, 896) == s.VOCAB * 28 * 18 + s.VOCAB // 64 * 4
     assert s.lib().pb_lmhead_q8_packed_bytes(s.VOCAB, 896) == s.VOCAB * 28 * 34
+
+
+def test_lmhead_and_reserve_argument_errors_need_no_device():
+    """A head packed for another width or format is refused by its size
+    before any device work (the C calls take the packed length), and so is a
+    reservation for a width the head cannot take."""
+    import ctypes
+
+    e = s._Error()
+    q4 = s.lib().pb_lmhead_packed_bytes(s.VOCAB, 896)
+    q8 = s.lib().pb_lmhead_q8_packed_bytes(s.VOCAB, 896)
+    cases = [(s.lib().pb_lmhead_sample_batch, q8, q4), (s.lib().pb_lmhead_q8_sample_batch, q4, q8),
+             (s.lib().pb_lmhead_sample_batch, s.lib().pb_lmhead_packed_bytes(s.VOCAB, 1024), q4)]
+    for fn, given, want in cases:
+        st = fn(None, None, given, s.VOCAB, 896, None, 4, None, 0, None, None, None, None, None,
+                None, None, ctypes.byref(e))
+        assert st == s.CAPACITY and (e.needed, e.available, e.detail) == (want, given, (4 << 32) | 7)
+    fake = ctypes.c_void_p(256)  # never dereferenced: the size check comes first
+    for fn, want in ((s.lib().pb_lmhead_decode_step, q4), (s.lib().pb_lmhead_q8_decode_step, q8)):
+        st = fn(None, None, want + 1, s.VOCAB, 896, None, 4, fake, 4, fake, None, fake, None,
+                None, None, None, None, None, ctypes.byref(e))
+        assert st == s.CAPACITY and (e.needed, e.available) == (want, want + 1)
+    st = s.lib().pb_context_reserve(None, 256, 900, ctypes.byref(e))
+    assert st == s.CAPACITY and (e.needed, e.available) == (32, 900)
+    st = s.lib().pb_context_reserve(None, 256, 4096, ctypes.byref(e))
+    assert st == s.CAPACITY and e.available == 4096

@@ -153,3 +153,37 @@ def test_lmhead_decode_steps_match_the_oracle_loop():
     finally:
         dec.close()
         smp.close()
+
+
+def test_active_row_at_its_cap_is_not_sampled():
+    """A row still marked active whose context is already at its cap is not
+    sampled (the REPL stops before sampling when there is no room): it ends
+    with ROW_LIMIT, no token, no draw, an unchanged context; its neighbour is
+    sampled as usual.  Both slice plans."""
+    from promptboot_amd import hip
+
+    rng = np.random.default_rng(5)
+    prompts = [workloads.zipf_ids(rng, 12), workloads.zipf_ids(rng, 40)]
+    seeds, limits = [3, 4], [0, 8]
+    logits = np.stack([stand_in_logits(r, 0, int(p[-1]), None) for r, p in enumerate(prompts)])
+    for segments in (0, 1):
+        oracle_rows = [o.DecodeRow(p, sd, lim) for p, sd, lim in zip(prompts, seeds, limits)]
+        want = [d.step(logits[r]) for r, d in enumerate(oracle_rows)]
+        assert want[0] is None and oracle_rows[0].reason == "LIMIT"
+        smp = s.BatchSampler(0, segments=segments)
+        dec = s.DecodeBatch(prompts, seeds, limits, sampler=smp)
+        try:
+            assert dec.row_state_host[0] == s.ROW_LIMIT
+            # mark the full row active on both sides, as a caller might
+            dec.row_state_host[0] = s.ROW_ACTIVE
+            dec.row_state.upload(dec.row_state_host)
+            got = dec.step(hip.DeviceArray.from_numpy(logits))
+            assert got[0] == s.NO_TOKEN and got[1] == want[1]
+            assert dec.row_state_host[0] == s.ROW_LIMIT
+            states = dec.sampling_states()
+            for r, d in enumerate(oracle_rows):
+                assert (states[r].state(), states[r].draws()) == (d.state.state(), d.state.draws())
+                assert dec.contexts()[r].tolist() == d.working
+        finally:
+            dec.close()
+            smp.close()

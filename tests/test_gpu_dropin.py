@@ -203,14 +203,14 @@ def test_preset_seen_bits_follow_the_reference_dedupe():
 
 
 def test_staging_grows_then_shorter_and_empty_histories():
-    """A 9,000-id history outgrows the drop-in's first staging buffers (4,096
-    ids); then a short history and an empty one follow on the regrown buffers.
-    Each call has preset scratch bits: with an empty history the scratch comes
-    back exactly as it went in."""
+    """A 40,000-id history outgrows the drop-in's staging (sized at context
+    creation for 32,768 ids, the context limit); then a short history and an
+    empty one follow on the regrown buffers.  Each call has preset scratch
+    bits: with an empty history the scratch comes back exactly as it went in."""
     rng = np.random.default_rng(17)
     base = rng.normal(0, 2.5, V).astype(np.float32).view(np.uint32)
     top = np.argsort(-base.view(np.float32))[:40].astype(np.uint32)
-    long_hist = np.concatenate([rng.integers(0, V, 8960).astype(np.uint32), top])
+    long_hist = np.concatenate([rng.integers(0, V, 39_960).astype(np.uint32), top])
     seen0 = np.zeros(s.SEEN_BYTES, np.uint8)
     for tok in list(top[::4]) + [9, 150_000]:
         seen0[tok // 8] |= 1 << (tok % 8)
