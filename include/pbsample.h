@@ -224,6 +224,24 @@ uint32_t pb_sample_batch(pb_context *ctx, const uint32_t *d_logits, size_t vocab
                          uint32_t *d_token, pb_sample_detail *d_detail,
                          pb_inference_error *d_err, void *stream, pb_inference_error *err);
 
+/* pb_sample_batch without any allocation, for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  No counterpart in the reference.  The slice workspace of the
+ * multi-slice plan lives in a static device array of 172,032 bytes (1,024
+ * row x slice records) per device, held until the process ends, instead of
+ * the context's workspace.  The automatic slice plan fits it for every batch
+ * size; a slice plan forced on the context (pb_context_set_segments) that
+ * needs more is refused with PB_CAPACITY (needed/available = bytes) before
+ * anything is enqueued.  Every call on one device shares that device's
+ * array: calls that overlap on the device race on it.  The context supplies
+ * the device and the slice plan; its own workspace is not used. */
+uint32_t pb_sample_batch_noalloc(pb_context *ctx, const uint32_t *d_logits, size_t vocab,
+                                 size_t ld, uint32_t rows, const uint32_t *d_hist,
+                                 size_t hist_ld, const uint32_t *d_hist_len,
+                                 const uint32_t *d_random_24, uint32_t *d_token,
+                                 pb_sample_detail *d_detail, pb_inference_error *d_err,
+                                 void *stream, pb_inference_error *err);
+
 /* As pb_sample_batch, then applies the repetition penalty in place to every
  * successful row (once per unique history id), as the reference mutates the
  * caller's logits (fp32_sse2.rs:1848-1876).  d_seen (optional, rows x

@@ -278,6 +278,9 @@ uint32_t pb_context_create(int device, pb_context** out) {
   if (e == hipSuccess) e = ensure_staging(ctx, PB_CONTEXT_IDS);
   if (e == hipSuccess)
     e = grow_device(&ctx->d_work, &ctx->list_bytes, slice_workspace_bytes(max_slots(255, 0)));
+  // the device address of pb_sample_batch_noalloc's static scratch, once per device
+  void* scratch = nullptr;
+  if (e == hipSuccess) e = pb::static_scratch_address(device, &scratch);
   if (e != hipSuccess) {
     release(ctx);
     return PB_DEVICE;
@@ -398,13 +401,19 @@ static uint32_t enqueue_sample_in(int device, uint32_t forced_segments, void* wo
 // enqueue_sample_in on the context's own workspace.  The arguments are
 // checked before the context is touched; then the context's lock is taken
 // unless the caller (a drop-in) already holds it.
+struct Workspace {
+  void* base;
+  size_t bytes;
+};
+
 static uint32_t enqueue_sample(pb_context* ctx, const uint32_t* d_logits, size_t vocab, size_t ld,
                                uint32_t rows, const uint32_t* d_hist, size_t hist_ld,
                                const uint32_t* d_hist_len, const uint32_t* d_random_24,
                                const uint8_t* d_excl, uint32_t* d_token,
                                pb_sample_detail* d_detail, pb_inference_error* d_err,
                                hipStream_t stream, pb_inference_error* err,
-                               const DecodeArgs* dec = nullptr, bool locked = false) {
+                               const DecodeArgs* dec = nullptr, bool locked = false,
+                               const Workspace* ws = nullptr) {
   uint32_t st = enqueue_sample_in(-1, 0, nullptr, 0, d_logits, vocab, ld, 0, d_hist, hist_ld,
                                   d_hist_len, d_random_24, d_excl, d_token, d_detail, d_err,
                                   stream, err, dec);
@@ -414,12 +423,36 @@ static uint32_t enqueue_sample(pb_context* ctx, const uint32_t* d_logits, size_t
     set_error(err, PB_CAPACITY, PB_DOMAIN_ARGMAX, 1, 0, PB_FIELD_BYTES, 3);
     return PB_CAPACITY;
   }
+  if (ctx == nullptr) {
+    set_error(err, PB_STATE, PB_DOMAIN_NONE, 1, 0, PB_FIELD_NONE, 0);
+    return PB_STATE;
+  }
   std::unique_lock<std::mutex> lock(ctx->mu, std::defer_lock);
   if (!locked) lock.lock();
-  return enqueue_sample_in(ctx->device, ctx->forced_segments, ctx->d_work, ctx->list_bytes,
-                           d_logits, vocab, ld, rows, d_hist, hist_ld, d_hist_len, d_random_24,
-                           d_excl, d_token, d_detail, d_err, stream, err, dec);
+  void* work = ws ? ws->base : ctx->d_work;
+  const size_t work_bytes = ws ? ws->bytes : ctx->list_bytes;
+  return enqueue_sample_in(ctx->device, ctx->forced_segments, work, work_bytes, d_logits, vocab,
+                           ld, rows, d_hist, hist_ld, d_hist_len, d_random_24, d_excl, d_token,
+                           d_detail, d_err, stream, err, dec);
 }
+
+namespace pb {
+
+int context_device(const pb_context* ctx) { return ctx->device; }
+
+uint32_t enqueue_sample_with_workspace(pb_context* ctx, void* work, size_t work_bytes,
+                                       const uint32_t* d_logits, size_t vocab, size_t ld,
+                                       uint32_t rows, const uint32_t* d_hist, size_t hist_ld,
+                                       const uint32_t* d_hist_len, const uint32_t* d_random_24,
+                                       uint32_t* d_token, pb_sample_detail* d_detail,
+                                       pb_inference_error* d_err, hipStream_t stream,
+                                       pb_inference_error* err) {
+  const Workspace ws{work, work_bytes};
+  return enqueue_sample(ctx, d_logits, vocab, ld, rows, d_hist, hist_ld, d_hist_len, d_random_24,
+                        nullptr, d_token, d_detail, d_err, stream, err, nullptr, false, &ws);
+}
+
+}  // namespace pb
 
 extern "C" {
 

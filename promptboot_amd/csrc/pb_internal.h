@@ -88,4 +88,19 @@ hipError_t launch_probe(int which, const uint32_t* in, uint32_t* out, size_t n,
                         hipStream_t stream);
 hipError_t launch_wave_selftest(uint32_t* out, hipStream_t stream);
 
+// The context's device (pb_api.cpp).
+int context_device(const pb_context* ctx);
+// pb_sample_batch with `work` (work_bytes) as the slice workspace in place of
+// the context's own; PB_CAPACITY when the slice plan needs more (pb_api.cpp).
+uint32_t enqueue_sample_with_workspace(pb_context* ctx, void* work, size_t work_bytes,
+                                       const uint32_t* d_logits, size_t vocab, size_t ld,
+                                       uint32_t rows, const uint32_t* d_hist, size_t hist_ld,
+                                       const uint32_t* d_hist_len, const uint32_t* d_random_24,
+                                       uint32_t* d_token, pb_sample_detail* d_detail,
+                                       pb_inference_error* d_err, hipStream_t stream,
+                                       pb_inference_error* err);
+// Device address of pb_sample_batch_noalloc's static scratch on `device`,
+// looked up once per device (pb_static.hip).
+hipError_t static_scratch_address(int device, void** out);
+
 }  // namespace pb

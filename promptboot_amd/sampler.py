@@ -107,6 +107,9 @@ EXPORTS = {
     "pb_sample_batch": (
         u32, [vp, vp, size_t, size_t, u32, vp, size_t, vp, vp, vp, vp, vp, vp,
               ctypes.POINTER(_Error)]),
+    "pb_sample_batch_noalloc": (
+        u32, [vp, vp, size_t, size_t, u32, vp, size_t, vp, vp, vp, vp, vp, vp,
+              ctypes.POINTER(_Error)]),
     "pb_sample_batch_inplace": (
         u32, [vp, vp, size_t, size_t, u32, vp, size_t, vp, vp, vp, vp, vp, vp, vp,
               ctypes.POINTER(_Error)]),
