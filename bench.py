@@ -6,36 +6,47 @@ One step = one pb_sample_batch call over a resident batch of synthetic rows
 penalty, top-20, temperature-0.7 softmax, top-p 0.8 and the draw for every
 row.  The headline workload is B=4096 rows with full-context histories
 (promptboot_amd.workloads "large"); B=1 and B=64 are timed the same way and
-reported under "by_batch".
+reported under "by_batch".  The process uses the library's own HIP binding
+(promptboot_amd.hip) for buffers, streams and events: no other framework is
+loaded, as a C or Rust caller of libpbsample.so would run it.
 
 The printed JSON line also carries:
-  roofline           the segment kernel's algorithmic HBM bytes per launch
-                     over its average launch time (HIP events on the launch
-                     stream) against the 8 TB/s MI355X peak, and the measured
-                     HBM traffic from the committed rocprofv3 counter summary
-                     when present;
-  cpu_baseline       the CPU oracle (a restatement of the reference sampler),
-                     single-threaded and pinned to one CPU, on the same 4096
-                     rows (3 repetitions, median);
-  parity             token agreement with the oracle over every row of the
-                     batch;
-  adversarial_B1024  the flat / ties / dominant / half-vocabulary-history
-                     sub-cases, each timed and checked against the oracle;
-  lmhead_fused       the fused Q4_0 LM head + sampler step (B=256);
-  lmhead_q8_fused    the same with the Q8_0 head (the model's output head);
-  lmhead_B1          one conversation's step (B=1) through each head;
-  host_buffers       PCIe-inclusive rates: the single-row drop-in on host
-                     buffers, and the B=4096 batch copied from pinned host
-                     memory every step (not the headline value).
+  roofline            the segment kernel's algorithmic HBM bytes per launch
+                      over its average launch time (HIP events on the launch
+                      stream) against the 8 TB/s MI355X peak; the read
+                      bandwidth the same load pattern reaches on this device
+                      (pb_device_read_probe over the same number of bytes);
+                      and the HBM traffic measured by rocprofv3 counters,
+                      taken from the committed summary only when that summary
+                      names this very build (pb_version);
+  cpu_baseline        the CPU oracle (a restatement of the reference sampler),
+                      single-threaded and pinned to one CPU, on the same 4096
+                      rows (3 repetitions, median);
+  production_sampling the reference's own timed case (the real Qwen "hello"
+                      row, its 30-id prompt, seed 0x0123456789abcdef; token
+                      9707): 3 timed calls of the GPU drop-in and of the
+                      pinned CPU oracle, min/median/max;
+  parity              token agreement with the oracle over every row;
+  adversarial_B1024   the flat / ties / dominant / half-vocabulary-history
+                      sub-cases, each timed and checked against the oracle;
+  lmhead_fused        the fused Q4_0 LM head + sampler step (B=256);
+  lmhead_q8_fused     the same with the Q8_0 head (the model's output head);
+  lmhead_B1           one conversation's step (B=1) through each head;
+  host_buffers        PCIe-inclusive rates: the single-row drop-in on host
+                      buffers, and the B=4096 batch copied from pinned host
+                      memory every step (not the headline value).
 
 Before the W warmup steps every batch size runs an untimed settle phase
 (the step repeated for 0.5 s) so the GPU is at its working clocks.
 
 Usage: python bench.py [--gpus 1] [--steps 200] [--warmup 5]
+       python bench.py --traffic-summary FETCH_DIR WRITE_DIR   (after two
+       rocprofv3 --pmc runs; writes the profiles/ traffic summary)
 """
 from __future__ import annotations
 
 import argparse
+import csv
 import json
 import os
 import pathlib
@@ -56,6 +67,10 @@ CPU_SAMPLE_ROWS = 4096
 SETTLE_S = 0.5
 PARITY_LMHEAD_ROWS = 64  # rows of the LM head step re-computed by the oracle (~9 G MACs)
 PMC_SUMMARY = ROOT / "profiles" / "segment_kernel_B4096_traffic.json"
+SEGMENT_KERNEL = "pb::segment_kernel<8, true>(pb::RowParams)"
+CALIBRATION_KERNEL = "__amd_rocclr_copyBuffer"
+PRODUCTION_SEED = 0x0123_4567_89AB_CDEF
+GOLDEN = ROOT / "tests" / "golden"
 
 
 def log(*a):
@@ -76,6 +91,8 @@ def host_cores() -> dict:
             "affinity": len(os.sched_getaffinity(0))}
 
 
+# ---- CPU legs (the oracle, pinned to one CPU in a child process) ----
+
 def cpu_worker(path: str) -> None:
     """Child process pinned to one CPU: times the oracle on the sample rows."""
     from oracle import oracle as o
@@ -94,81 +111,135 @@ def cpu_worker(path: str) -> None:
                       "tokens": tokens.tolist()}))
 
 
-def cpu_baseline(w: dict) -> dict:
+def production_worker() -> None:
+    """Child process pinned to one CPU: the reference's timed call
+    (validate_inference.rs:780-794; timer boundary :1303 -- after copying the
+    logits and allocating the scratch, from just before the call to its
+    return), three times with the oracle."""
+    from oracle import oracle as o
+
+    assert len(os.sched_getaffinity(0)) == 1, "CPU baseline must see exactly one CPU"
+    base = np.fromfile(GOLDEN / "qwen_hello_logits.f32le", dtype="<u4")
+    prompt = np.fromfile(GOLDEN / "qwen_hello_prompt.u32le", dtype="<u4")
+    runs = []
+    for _ in range(3):
+        logits = base.copy()
+        seen = np.zeros(o.SEEN_BYTES, np.uint8)
+        state = o.SamplingState(PRODUCTION_SEED)
+        t0 = time.perf_counter()
+        st, tok, _ = o.sample_token_with_repetition(logits, prompt, seen, state)
+        runs.append(time.perf_counter() - t0)
+        assert st == 0 and tok == 9707 and state.draws() == 1
+    print(json.dumps({"runs_s": runs}))
+
+
+def pinned_child(*args) -> dict:
     cpu = sorted(os.sched_getaffinity(0))[0]
+    out = subprocess.run(["taskset", "-c", str(cpu), sys.executable, str(ROOT / "bench.py"),
+                          *args], check=True, capture_output=True, text=True)
+    res = json.loads(out.stdout.strip().splitlines()[-1])
+    res["cpu"] = cpu
+    return res
+
+
+def cpu_baseline(w: dict) -> dict:
     n = min(CPU_SAMPLE_ROWS, w["logits"].shape[0])
     with tempfile.NamedTemporaryFile(suffix=".npz", dir="/dev/shm", delete=False) as f:
         path = f.name
     try:
         np.savez(path, logits=w["logits"][:n], hist=w["hist"][:n], hist_len=w["hist_len"][:n],
                  seeds=w["seeds"][:n])
-        out = subprocess.run(["taskset", "-c", str(cpu), sys.executable, str(ROOT / "bench.py"),
-                              "--cpu-worker", path], check=True, capture_output=True, text=True)
+        res = pinned_child("--cpu-worker", path)
     finally:
         os.unlink(path)
-    res = json.loads(out.stdout.strip().splitlines()[-1])
     runs = sorted(res["runs_s"])
     med = runs[1]
     return {"value": round(n / med, 2), "unit": "rows/s", "cores": 1, "kind": "port",
             "sample": f"first {n} rows of the B=4096 workload, sample_token_with_repetition "
-                      f"per row, 3 repetitions (median), pinned to CPU {cpu}",
+                      f"per row, 3 repetitions (median), pinned to CPU {res['cpu']}",
             "runs_s": [round(r, 4) for r in res["runs_s"]],
             "min_s": round(runs[0], 4), "median_s": round(med, 4), "max_s": round(runs[2], 4),
             "host_cores": host_cores(), "_tokens": np.array(res["tokens"], np.uint32)}
 
 
-def time_batch(smp, w: dict, steps: int, warmup: int) -> dict:
-    import torch
+def stats_us(secs) -> dict:
+    us = sorted(float(x) * 1e6 for x in secs)
+    return {"min_us": round(us[0], 1), "median_us": round(float(np.median(us)), 1),
+            "max_us": round(us[-1], 1), "calls": len(us)}
 
+
+# ---- GPU legs ----
+
+def dev(a):
+    from promptboot_amd import hip
+
+    return hip.DeviceArray.from_numpy(np.ascontiguousarray(a))
+
+
+def event_pass(step, steps: int, stream) -> float:
+    """Mean HIP-event time (ms) of `steps` calls of step(), events recorded on
+    the launch stream around each call."""
+    from promptboot_amd import hip
+
+    starts = [hip.Event() for _ in range(steps)]
+    ends = [hip.Event() for _ in range(steps)]
+    hip.synchronize()
+    for i in range(steps):
+        starts[i].record(stream)
+        step()
+        ends[i].record(stream)
+    hip.synchronize()
+    return float(np.mean([a.elapsed_ms(b) for a, b in zip(starts, ends)]))
+
+
+def wall_pass(step, steps: int) -> float:
+    """Wall time (s) of `steps` back-to-back calls, bracketed by device syncs."""
+    from promptboot_amd import hip
+
+    hip.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    hip.synchronize()
+    return time.perf_counter() - t0
+
+
+def settle(step, per_round: int = 8) -> None:
+    """Untimed: repeat the step for SETTLE_S seconds so the GPU leaves its
+    idle clocks (a cold MI355X runs the first tens of launches ~10 % slower)."""
+    from promptboot_amd import hip
+
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < SETTLE_S:
+        for _ in range(per_round):
+            step()
+        hip.synchronize()
+
+
+def time_batch(smp, w: dict, steps: int, warmup: int, stream) -> dict:
+    from promptboot_amd import hip
     from promptboot_amd import sampler as s
     from promptboot_amd import workloads
 
-    dev = torch.device("cuda:0")
-
-    def t(a):
-        return torch.from_numpy(np.ascontiguousarray(a).view(np.int32)).to(dev)
-
     B = w["logits"].shape[0]
-    logits, hist, hl, r24 = t(w["logits"]), t(w["hist"]), t(w["hist_len"]), t(w["random_24"])
-    token = torch.empty(B, dtype=torch.int32, device=dev)
-    det = torch.empty((B, s.DETAIL_DTYPE.itemsize // 4), dtype=torch.int32, device=dev)
-    stream = torch.cuda.current_stream(dev)
+    logits, hist, hl, r24 = dev(w["logits"]), dev(w["hist"]), dev(w["hist_len"]), dev(w["random_24"])
+    token = hip.DeviceArray(B, np.uint32)
+    det = hip.DeviceArray((B, s.DETAIL_DTYPE.itemsize // 4), np.uint32)
 
-    def step(with_detail=False):
-        smp.sample(logits, r24, hist, hl, token=token, detail=det if with_detail else None,
-                   stream=stream)
-
-    step(with_detail=True)
-    torch.cuda.synchronize()
-    tokens = token.cpu().numpy().view(np.uint32).copy()
-    detail = det.cpu().numpy().view(s.DETAIL_DTYPE).reshape(B).copy()
-    # Untimed settle: repeat the step for SETTLE_S seconds so the GPU leaves
-    # its idle clocks (a cold MI355X runs the first tens of launches ~10 %
-    # slower), then the W warmup steps, then exactly K timed steps.
-    t_settle = time.perf_counter()
-    while time.perf_counter() - t_settle < SETTLE_S:
-        for _ in range(8):
-            step()
-        torch.cuda.synchronize()
+    # one call with the detail kept for the parity check; the timed steps are
+    # one bound foreign call each, as a C caller makes them
+    smp.sample(logits, r24, hist, hl, token=token, detail=det, stream=stream)
+    step = smp.bind_sample(logits, r24, hist, hl, token=token, stream=stream)
+    tokens = token.numpy()
+    detail = det.numpy().view(s.DETAIL_DTYPE).reshape(B).copy()
+    settle(step)
     for _ in range(warmup):
         step()
     # Two timed passes of the same K steps: HIP events around each launch give
     # the kernel time (the roofline); a pass with no events in it gives the
     # wall time per step (the rows/s value), free of the events' own markers.
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    torch.cuda.synchronize()
-    for i in range(steps):
-        starts[i].record(stream)
-        step()
-        ends[i].record(stream)
-    torch.cuda.synchronize()
-    kernel_ms = float(np.mean([a.elapsed_time(b) for a, b in zip(starts, ends)]))
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        step()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
+    kernel_ms = event_pass(step, steps, stream)
+    wall = wall_pass(step, steps)
     ms_per_step = wall / steps * 1e3
     alg = workloads.algorithmic_bytes(w["hist_len"])
     return {"rows": B, "ms_per_step": ms_per_step, "rows_per_s": B / (ms_per_step / 1e3),
@@ -178,7 +249,77 @@ def time_batch(smp, w: dict, steps: int, warmup: int) -> dict:
             "_tokens": tokens, "_detail": detail}
 
 
-def time_host_buffers(smp, w1: dict, w: dict, calls: int = 200, steps: int = 5) -> dict:
+def read_ceiling(nbytes: int, stream, steps: int = 20) -> dict:
+    """Read bandwidth of the sampler's load pattern (pb_device_read_probe)
+    over a buffer of `nbytes`, 4096 workgroups as in the B=4096 launch."""
+    import ctypes
+
+    from promptboot_amd import hip
+    from promptboot_amd import sampler as s
+
+    words = nbytes // 16 * 4
+    buf = hip.DeviceArray(words, np.uint32)
+    out = hip.DeviceArray.zeros(4096, np.uint32)
+    h = ctypes.c_void_p(hip.stream_handle(stream))
+
+    def step():
+        st = s.lib().pb_device_read_probe(ctypes.c_void_p(buf.data_ptr()), words,
+                                          ctypes.c_void_p(out.data_ptr()), 4096, h)
+        assert st == s.OK
+
+    settle(step)
+    ms = event_pass(step, steps, stream)
+    buf.free()
+    return {"read_gbs": round(words * 4 / (ms / 1e3) / 1e9, 1), "bytes": words * 4,
+            "launch_ms": round(ms, 4), "kernel": "pb::read_probe_kernel (pb_device_read_probe)"}
+
+
+def time_production(stream) -> dict:
+    """The reference's timed case: the hello row, its 30-id prompt, seed
+    0x0123456789abcdef, one sample_token_with_repetition call, token 9707.
+    Three timed calls of the GPU drop-in on host buffers (the reference's
+    call shape; timer around the call only) beside the pinned CPU oracle;
+    the same row resident in HBM through pb_sample_batch is reported too."""
+    from promptboot_amd import hip
+    from promptboot_amd import sampler as s
+
+    base = np.fromfile(GOLDEN / "qwen_hello_logits.f32le", dtype="<u4")
+    prompt = np.fromfile(GOLDEN / "qwen_hello_prompt.u32le", dtype="<u4")
+    # one untimed call brings up the default context and its staging
+    s.sample_token_with_repetition(base.copy(), prompt, np.zeros(s.SEEN_BYTES, np.uint8),
+                                   s.SamplingState(PRODUCTION_SEED))
+    runs = []
+    for _ in range(3):
+        logits = base.copy()
+        seen = np.zeros(s.SEEN_BYTES, np.uint8)
+        state = s.SamplingState(PRODUCTION_SEED)
+        t0 = time.perf_counter()
+        tok = s.sample_token_with_repetition(logits, prompt, seen, state)
+        runs.append(time.perf_counter() - t0)
+        assert tok == 9707 and state.draws() == 1
+    smp = s.BatchSampler(0)
+    hist = np.zeros((1, 32), np.uint32)
+    hist[0, :prompt.size] = prompt
+    r24 = np.array([s.SamplingState(PRODUCTION_SEED).next_24()], np.uint32)
+    d_logits, d_hist = dev(base[None, :]), dev(hist)
+    d_len, d_r24 = dev(np.array([prompt.size], np.uint32)), dev(r24)
+    token = hip.DeviceArray(1, np.uint32)
+    step = smp.bind_sample(d_logits, d_r24, d_hist, d_len, token=token, stream=stream)
+    step()
+    assert int(token.numpy()[0]) == 9707
+    settle(step)
+    resident_ms = event_pass(step, 50, stream)
+    smp.close()
+    cpu = pinned_child("--production-worker")
+    return {"case": "hello row (tests/golden/qwen_hello_logits.f32le), 30-id prompt, seed "
+                    "0x0123456789abcdef, one sample_token_with_repetition: token 9707 each call",
+            "gpu_dropin": stats_us(runs),
+            "gpu_resident_pb_sample_batch_us": round(resident_ms * 1e3, 1),
+            "cpu_port": {**stats_us(cpu["runs_s"]), "cores": 1, "cpu": cpu["cpu"]},
+            "token": 9707}
+
+
+def time_host_buffers(smp, w1: dict, w: dict, stream, calls: int = 200, steps: int = 5) -> dict:
     """Rates with the inputs in host memory, so PCIe is included (never the
     headline value, which is timed with the inputs resident in HBM):
 
@@ -189,8 +330,7 @@ def time_host_buffers(smp, w1: dict, w: dict, calls: int = 200, steps: int = 5) 
                 (logits, the padded history matrix, lengths, uniforms), then
                 pb_sample_batch, then the tokens copied back.
     """
-    import torch
-
+    from promptboot_amd import hip
     from promptboot_amd import sampler as s
 
     row0 = np.ascontiguousarray(w1["logits"][0]).view(np.uint32)
@@ -206,30 +346,29 @@ def time_host_buffers(smp, w1: dict, w: dict, calls: int = 200, steps: int = 5) 
             times.append(time.perf_counter() - t0)
     times = np.array(times) * 1e6
 
-    dev = torch.device("cuda:0")
-    stream = torch.cuda.current_stream(dev)
     B = w["logits"].shape[0]
-    host = [torch.from_numpy(np.ascontiguousarray(w[k]).view(np.int32)).pin_memory()
-            for k in ("logits", "hist", "hist_len", "random_24")]
-    devs = [torch.empty_like(h, device=dev) for h in host]
-    token = torch.empty(B, dtype=torch.int32, device=dev)
-    h_token = torch.empty(B, dtype=torch.int32).pin_memory()
-    h2d = sum(h.numel() * 4 for h in host)
+    names = ("logits", "hist", "hist_len", "random_24")
+    host = []
+    for k in names:
+        a = np.ascontiguousarray(w[k])
+        h = hip.PinnedArray(a.shape, a.dtype)
+        h.array[...] = a
+        host.append(h)
+    devs = [hip.DeviceArray(h.array.shape, h.dtype) for h in host]
+    token = hip.DeviceArray(B, np.uint32)
+    h_token = hip.PinnedArray(B, np.uint32)
+    h2d = sum(h.nbytes for h in host)
 
     def step():
         for d, h in zip(devs, host):
-            d.copy_(h, non_blocking=True)
+            hip.copy_async(d, h, h.nbytes, hip.H2D, stream)
         smp.sample(devs[0], devs[3], devs[1], devs[2], token=token, stream=stream)
-        h_token.copy_(token, non_blocking=True)
+        hip.copy_async(h_token, token, token.nbytes, hip.D2H, stream)
 
     step()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        step()
-    torch.cuda.synchronize()
-    sec = (time.perf_counter() - t0) / steps
-    del host, devs
+    sec = wall_pass(step, steps) / steps
+    for a in host + devs + [h_token]:
+        a.free()
     return {"dropin_us_per_call": {"median": round(float(np.median(times)), 1),
                                    "p10": round(float(np.percentile(times, 10)), 1),
                                    "p90": round(float(np.percentile(times, 90)), 1),
@@ -246,63 +385,42 @@ MFMA_INT8_PEAK_TOPS = 5000.0     # dense int8 MFMA, MI355X
 VALU_LANE_OPS_PEAK = 256 * 4 * 16 * 2.4e9  # 32-bit VALU lane-ops/s, MI355X
 
 
-def time_lmhead(smp, steps: int, warmup: int, q8: bool = False, rows: int = 256) -> dict:
+def time_lmhead(smp, steps: int, warmup: int, stream, q8: bool = False, rows: int = 256) -> dict:
     """Fused Q4_0 (or, with q8, Q8_0) LM head + sampler, `rows` hidden states of
     width 896 (256 by default; 1 is one conversation's decode step)."""
-    import torch
-
+    from promptboot_amd import hip
     from promptboot_amd import sampler as s
     from promptboot_amd import workloads
 
     w = workloads.make_lmhead(rows=rows)
     head = workloads.make_q8_head() if q8 else w["q4"]
-    dev = torch.device("cuda:0")
-
-    def t(a):
-        return torch.from_numpy(np.ascontiguousarray(a).view(np.int32)).to(dev)
-
-    packed = smp.pack_lmhead(torch.from_numpy(head).to(dev), q8=q8)
-    hidden, hist, hl, r24 = t(w["hidden"]), t(w["hist"]), t(w["hist_len"]), t(w["random_24"])
-    B = hidden.shape[0]
-    token = torch.empty(B, dtype=torch.int32, device=dev)
-    stream = torch.cuda.current_stream(dev)
-
-    def step():
-        smp.lmhead_sample(packed, hidden, r24, hist, hl, token=token, stream=stream, q8=q8)
+    d_head = dev(head)
+    packed = smp.pack_lmhead(d_head, q8=q8, stream=stream)
+    hip.synchronize()
+    d_head.free()
+    hidden, hist, hl, r24 = dev(w["hidden"]), dev(w["hist"]), dev(w["hist_len"]), dev(w["random_24"])
+    B = rows
+    token = hip.DeviceArray(B, np.uint32)
+    smp.reserve(B, workloads.HIDDEN)
+    step = smp.bind_lmhead(packed, hidden, r24, hist, hl, token=token, stream=stream, q8=q8)
 
     # one step with the logits and detail kept, for the parity check below
-    logits = torch.empty((B, s.VOCAB), dtype=torch.int32, device=dev)
-    det = torch.empty((B, s.DETAIL_DTYPE.itemsize // 4), dtype=torch.int32, device=dev)
+    logits = hip.DeviceArray((B, s.VOCAB), np.uint32)
+    det = hip.DeviceArray((B, s.DETAIL_DTYPE.itemsize // 4), np.uint32)
     smp.lmhead_sample(packed, hidden, r24, hist, hl, token=token, detail=det, logits=logits,
                       stream=stream, q8=q8)
-    torch.cuda.synchronize()
     n_check = min(PARITY_LMHEAD_ROWS, B)
-    g_logits = logits[:n_check].cpu().numpy().view(np.uint32)
-    g_tokens = token.cpu().numpy().view(np.uint32)[:n_check].copy()
-    g_flags = det.cpu().numpy().view(s.DETAIL_DTYPE).reshape(B)["flags"][:n_check].copy()
-    del logits, det
-    t_settle = time.perf_counter()
-    while time.perf_counter() - t_settle < SETTLE_S:
-        for _ in range(4):
-            step()
-        torch.cuda.synchronize()
+    g_logits = logits.numpy()[:n_check].copy()
+    g_tokens = token.numpy()[:n_check].copy()
+    g_flags = det.numpy().view(s.DETAIL_DTYPE).reshape(B)["flags"][:n_check].copy()
+    logits.free()
+    settle(step, 4)
     for _ in range(warmup):
         step()
     # events around each step for its time; a pass without events for rows/s
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    torch.cuda.synchronize()
-    for i in range(steps):
-        starts[i].record(stream)
-        step()
-        ends[i].record(stream)
-    torch.cuda.synchronize()
-    step_ms = float(np.mean([a.elapsed_time(b) for a, b in zip(starts, ends)]))
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        step()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
+    step_ms = event_pass(step, steps, stream)
+    wall = wall_pass(step, steps)
+    packed.free()
     # parity on a bounded sample: the oracle's head and sampler on the first
     # rows (bit-exact logits; token agreement on non-boundary rows)
     from oracle import oracle as o
@@ -334,6 +452,7 @@ def time_lmhead(smp, steps: int, warmup: int, q8: bool = False, rows: int = 256)
             "int8_tops": round(ops / (step_ms / 1e3) / 1e12, 1),
             "int8_mfma_frac": round(ops / (step_ms / 1e3) / 1e12 / MFMA_INT8_PEAK_TOPS, 4),
             "epilogue_valu_frac": round(epilogue / (step_ms / 1e3) / VALU_LANE_OPS_PEAK, 4),
+            "alg_bytes": alg,
             "hbm_gbs": round(alg / (step_ms / 1e3) / 1e9, 1),
             "hbm_frac": round(alg / (step_ms / 1e3) / 1e9 / PEAK_HBM_GBS, 4),
             "parity": parity,
@@ -348,7 +467,7 @@ def time_lmhead(smp, steps: int, warmup: int, q8: bool = False, rows: int = 256)
 ADVERSARIAL = ("flat", "ties", "dominant", "half")
 
 
-def time_adversarial(smp, steps: int, warmup: int, threads: int) -> dict:
+def time_adversarial(smp, steps: int, warmup: int, threads: int, stream) -> dict:
     """The adversarial B=1024 sub-cases (flat logits, ties at the rank-20
     boundary, one dominant token, a history over half the vocabulary), each
     timed and checked row by row against the oracle."""
@@ -359,7 +478,7 @@ def time_adversarial(smp, steps: int, warmup: int, threads: int) -> dict:
     for name in ADVERSARIAL:
         log(f"adversarial {name}: generating, timing, checking")
         w = workloads.make(name)
-        r = time_batch(smp, w, steps, warmup)
+        r = time_batch(smp, w, steps, warmup, stream)
         rtok, rdet, _, _ = o.sample_batch(w["logits"], w["hist"], w["hist_len"],
                                           w["random_24"], threads=threads)
         boundary = r["_detail"]["flags"] != 0
@@ -377,6 +496,89 @@ def time_adversarial(smp, steps: int, warmup: int, threads: int) -> dict:
     return out
 
 
+def measured_traffic(version: str) -> dict:
+    """HBM bytes per launch of the segment kernel from the committed counter
+    summary -- only if it was measured on this very build."""
+    if not PMC_SUMMARY.exists():
+        return {"traffic": None, "traffic_source": "no counter summary"}
+    d = json.loads(PMC_SUMMARY.read_text())
+    if d.get("library") != version:
+        return {"traffic": None,
+                "traffic_source": f"stale: the summary was measured on {d.get('library')!r}, "
+                                  f"this run uses {version!r}"}
+    return {"traffic": d.get("hbm_bytes_per_launch"),
+            "traffic_source": f"{PMC_SUMMARY.relative_to(ROOT)} (same build)"}
+
+
+# ---- rocprofv3 counter summary ----
+
+def _pmc_rows(folder: str, counter: str):
+    rows = []
+    for f in pathlib.Path(folder).rglob("*counter_collection.csv"):
+        with open(f) as fh:
+            for r in csv.DictReader(fh):
+                if r.get("Counter_Name") == counter:
+                    rows.append(r)
+    return rows
+
+
+def traffic_summary(fetch_dir: str, write_dir: str) -> None:
+    """Writes profiles/segment_kernel_B4096_traffic.json from a FETCH_SIZE and
+    a WRITE_SIZE rocprofv3 run of this bench (see the commands it records):
+    the per-dispatch KiB of the B=4096 segment kernel, each scaled by what the
+    same counter reads for the calibration copy of known size."""
+    from promptboot_amd import sampler as s
+    from promptboot_amd import workloads
+
+    def per_kernel(folder, counter, name_prefix):
+        vals = [float(r["Counter_Value"]) for r in _pmc_rows(folder, counter)
+                if r["Kernel_Name"].startswith(name_prefix)]
+        return (float(np.mean(vals)) if vals else None), len(vals)
+
+    cal_bytes = 1024 << 20
+    f_cal, _ = per_kernel(fetch_dir, "FETCH_SIZE", CALIBRATION_KERNEL)
+    w_cal, _ = per_kernel(write_dir, "WRITE_SIZE", CALIBRATION_KERNEL)
+    # the B=4096 launch is the one with 4096 workgroups; B=1 and B=64 use the
+    # same kernel name only with one slice per row from 256 rows on
+    def big(folder, counter):
+        vals = [float(r["Counter_Value"]) for r in _pmc_rows(folder, counter)
+                if r["Kernel_Name"].startswith(SEGMENT_KERNEL.split("(")[0])
+                and int(r.get("Grid_Size", r.get("Grid_Size_X", 0)) or 0) == 4096 * 256]
+        return float(np.mean(vals)), len(vals)
+
+    f_k, nf = big(fetch_dir, "FETCH_SIZE")
+    w_k, nw = big(write_dir, "WRITE_SIZE")
+    f_scale = cal_bytes / 1024 / f_cal
+    w_scale = cal_bytes / 1024 / w_cal
+    hbm = (f_k * f_scale + w_k * w_scale) * 1024
+    w = workloads.make("large")
+    alg = workloads.algorithmic_bytes(w["hist_len"])
+    repo = "$REPO"
+    cmd = ("cd /tmp && export TMPDIR=/tmp && timeout -s KILL 300 rocprofv3 --pmc {c} -f csv -d "
+           f"{repo}/gpurun_out/pmc_{{c}} -o run -- python3 {repo}/bench.py --no-cpu-baseline "
+           "--no-adversarial --no-lmhead --no-host-buffers --no-production --batches 4096 "
+           "--steps 2 --warmup 0 --calibration-copy-mib 1024")
+    out = {"kernel": SEGMENT_KERNEL,
+           "library": s.lib().pb_version().decode(),
+           "workload": "B=4096 rows x 151936 fp32 logits, history lengths U[16,32768] "
+                       "(promptboot_amd.workloads large)",
+           "commands": [cmd.format(c="FETCH_SIZE"), cmd.format(c="WRITE_SIZE"),
+                        f"python3 {repo}/bench.py --traffic-summary {repo}/gpurun_out/pmc_FETCH_SIZE "
+                        f"{repo}/gpurun_out/pmc_WRITE_SIZE"],
+           "calibration": {"kernel": f"{CALIBRATION_KERNEL} (hipMemcpyAsync device to device, "
+                                     "1024 MiB read + 1024 MiB written)",
+                           "fetch_size_kib": round(f_cal, 2), "write_size_kib": round(w_cal, 2),
+                           "fetch_scale": round(f_scale, 4), "write_scale": round(w_scale, 4)},
+           "segment_kernel_per_dispatch": {"dispatches": [nf, nw],
+                                           "fetch_size_kib": round(f_k, 2),
+                                           "write_size_kib": round(w_k, 2)},
+           "hbm_bytes_per_launch": int(round(hbm)),
+           "algorithmic_bytes_per_launch": alg,
+           "traffic_over_algorithmic": round(hbm / alg, 4)}
+    PMC_SUMMARY.write_text(json.dumps(out, indent=1) + "\n")
+    print(json.dumps(out, indent=1))
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -386,20 +588,31 @@ def main() -> int:
     ap.add_argument("--no-adversarial", action="store_true",
                     help="skip the adversarial B=1024 sub-cases")
     ap.add_argument("--no-lmhead", action="store_true",
-                    help="skip the fused Q4_0 LM head + sampler timing")
+                    help="skip the fused LM head + sampler timings")
     ap.add_argument("--no-host-buffers", action="store_true",
                     help="skip the PCIe-inclusive timings (drop-in on host buffers, "
                          "B=4096 copied from pinned host memory)")
+    ap.add_argument("--no-production", action="store_true",
+                    help="skip the reference's own timed case (hello row, seed 0x0123456789abcdef)")
     ap.add_argument("--batches", default="1,64,4096")
     ap.add_argument("--segments", type=int, default=0,
                     help="force the slices per row (0 = the library's choice)")
     ap.add_argument("--calibration-copy-mib", type=int, default=0,
                     help="first run one device-to-device copy of this many MiB, so a "
                          "rocprofv3 --pmc run can scale FETCH_SIZE/WRITE_SIZE to bytes")
+    ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="write the counter summary of two rocprofv3 --pmc runs and exit")
     ap.add_argument("--cpu-worker", default=None, help=argparse.SUPPRESS)
+    ap.add_argument("--production-worker", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.cpu_worker:
         cpu_worker(args.cpu_worker)
+        return 0
+    if args.production_worker:
+        production_worker()
+        return 0
+    if args.traffic_summary:
+        traffic_summary(*args.traffic_summary)
         return 0
     if args.gpus != 1:
         print("bench.py measures one GPU only: the sampler shards rows across GPUs with no "
@@ -422,45 +635,53 @@ def main() -> int:
         log("timing the CPU baseline (oracle, one pinned CPU)")
         cpu = cpu_baseline(work[head])
 
-    import torch
-
     from oracle import oracle as o
+    from promptboot_amd import hip
     from promptboot_amd import sampler as s
 
-    torch.cuda.set_device(0)
+    hip.set_device(0)
+    version = s.lib().pb_version().decode()
+    stream = hip.Stream()
     if args.calibration_copy_mib:
-        n = args.calibration_copy_mib << 18  # float32 words
-        src = torch.ones(n, dtype=torch.float32, device="cuda:0")
-        dst = torch.empty_like(src)
-        dst.copy_(src)
-        torch.cuda.synchronize()
-        del src, dst
+        n = args.calibration_copy_mib << 18  # 32-bit words
+        src = hip.DeviceArray.zeros(n, np.uint32)
+        dst = hip.DeviceArray(n, np.uint32)
+        dst.copy_from(src, stream)
+        hip.synchronize()
+        src.free()
+        dst.free()
     smp = s.BatchSampler(0, segments=args.segments)
     results = {}
     for B in batches:
         log(f"timing B={B}")
-        results[B] = time_batch(smp, work[B], args.steps, args.warmup)
+        results[B] = time_batch(smp, work[B], args.steps, args.warmup, stream)
+    main_res = results[head]
+    log("timing the read ceiling of the sampler's load pattern")
+    ceiling = read_ceiling(main_res["alg_bytes"], stream)
     threads = min(16, len(os.sched_getaffinity(0)))
     adversarial = None
     if not args.no_adversarial:
-        adversarial = time_adversarial(smp, min(args.steps, 50), args.warmup, threads)
+        adversarial = time_adversarial(smp, min(args.steps, 50), args.warmup, threads, stream)
     lmhead = lmhead_q8 = lmhead_b1 = None
     if not args.no_lmhead:
         log("timing the fused Q4_0 LM head + sampler (B=256)")
-        lmhead = time_lmhead(smp, min(args.steps, 50), args.warmup)
+        lmhead = time_lmhead(smp, min(args.steps, 50), args.warmup, stream)
         log("timing the fused Q8_0 LM head + sampler (B=256)")
-        lmhead_q8 = time_lmhead(smp, min(args.steps, 50), args.warmup, q8=True)
+        lmhead_q8 = time_lmhead(smp, min(args.steps, 50), args.warmup, stream, q8=True)
         log("timing one conversation's step through each head (B=1)")
-        lmhead_b1 = {"q4_0": time_lmhead(smp, min(args.steps, 100), args.warmup, rows=1),
-                     "q8_0": time_lmhead(smp, min(args.steps, 100), args.warmup, q8=True,
+        lmhead_b1 = {"q4_0": time_lmhead(smp, min(args.steps, 100), args.warmup, stream, rows=1),
+                     "q8_0": time_lmhead(smp, min(args.steps, 100), args.warmup, stream, q8=True,
                                          rows=1)}
+    production = None
+    if not args.no_production:
+        log("timing the reference's own case (hello row)")
+        production = time_production(stream)
     host_buffers = None
     if not args.no_host_buffers and 1 in work and 4096 in work:
         log("timing with the inputs in host memory (PCIe included)")
-        host_buffers = time_host_buffers(smp, work[1], work[4096])
+        host_buffers = time_host_buffers(smp, work[1], work[4096], stream)
     smp.close()
 
-    main_res = results[head]
     w = work[head]
     log("checking tokens against the oracle")
     rtok, rdet, _, _ = o.sample_batch(w["logits"], w["hist"], w["hist_len"], w["random_24"],
@@ -477,14 +698,15 @@ def main() -> int:
         parity["cpu_baseline_tokens_agree"] = bool((cpu["_tokens"] == main_res["_tokens"][:n]).all())
         cpu.pop("_tokens")
 
-    traffic = None
-    if PMC_SUMMARY.exists():
-        traffic = json.loads(PMC_SUMMARY.read_text()).get("hbm_bytes_per_launch")
+    traffic = measured_traffic(version)
     roof = {"bound": "hbm", "achieved": round(main_res["achieved_gbs"], 1), "peak": PEAK_HBM_GBS,
             "unit": "GB/s", "frac": round(main_res["achieved_gbs"] / PEAK_HBM_GBS, 4),
-            "traffic": traffic, "kernel": "pb::segment_kernel<8, true>",
+            "traffic": traffic["traffic"], "traffic_source": traffic["traffic_source"],
+            "kernel": "pb::segment_kernel<8, true>",
             "alg_bytes_per_launch": main_res["alg_bytes"],
-            "launch_ms": round(main_res["launch_ms"], 4)}
+            "launch_ms": round(main_res["launch_ms"], 4),
+            "read_ceiling": ceiling,
+            "frac_of_read_ceiling": round(main_res["achieved_gbs"] / ceiling["read_gbs"], 4)}
     by_batch = {}
     for B, r in results.items():
         by_batch[str(B)] = {"rows_per_s": round(r["rows_per_s"], 1),
@@ -513,11 +735,14 @@ def main() -> int:
                                "repetition penalty 1.1",
                    "rows": head, "vocab": 151936, "hist_ld": int(w["hist"].shape[1])},
         "tokens_per_s": round(main_res["rows_per_s"], 1),
+        "library": version,
+        "torch_loaded": "torch" in sys.modules,
         "by_batch": by_batch,
         "adversarial_B1024": adversarial,
         "lmhead_fused": lmhead,
         "lmhead_q8_fused": lmhead_q8,
         "lmhead_B1": lmhead_b1,
+        "production_sampling": production,
         "host_buffers": host_buffers,
         "roofline": roof,
         "cpu_baseline": cpu,

@@ -422,7 +422,15 @@ uint32_t pb_device_wave_selftest(uint32_t *d_out, void *stream);
  * B[k][j] = (5k + 11j) % 15 - 7 (k < 32) to d_out[32 i + j]. */
 uint32_t pb_device_mfma_selftest(int32_t *d_out, void *stream);
 
-/* Library version string and build target ("gfx950"). */
+/* Read-only stream probe (diagnostic, no reference counterpart): `blocks`
+ * workgroups read the n_words words at d_in (16-byte aligned) with the
+ * sampler's load pattern and XOR what they read into d_out[0 .. blocks).
+ * Timing it gives the read bandwidth the sampler's stream can reach. */
+uint32_t pb_device_read_probe(const uint32_t *d_in, size_t n_words, uint32_t *d_out,
+                              uint32_t blocks, void *stream);
+
+/* Library version string: "pbsample <version> src:<hash of the sources it was
+ * built from> gfx950". */
 const char *pb_version(void);
 
 #ifdef __cplusplus

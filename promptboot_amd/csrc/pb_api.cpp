@@ -233,7 +233,13 @@ void pb_fill_random_24(pb_sampling_state* states, uint32_t rows, uint32_t* out) 
   for (uint32_t r = 0; r < rows; ++r) out[r] = pb_next_24(&states[r]);
 }
 
-const char* pb_version(void) { return "pbsample 0.1 gfx950"; }
+// PB_SOURCE_HASH (set by the Makefile) identifies the sources the library was
+// built from, so a measurement recorded against one build can be told apart
+// from another build's.
+#ifndef PB_SOURCE_HASH
+#define PB_SOURCE_HASH "unknown"
+#endif
+const char* pb_version(void) { return "pbsample 0.2 src:" PB_SOURCE_HASH " gfx950"; }
 
 uint32_t pb_segments_for_rows(uint32_t rows) {
   uint32_t segs = 0, seg_f4 = 0;
@@ -259,6 +265,15 @@ uint32_t pb_device_penalize_bits(const uint32_t* d_in, uint32_t* d_out, size_t n
 
 uint32_t pb_device_wave_selftest(uint32_t* d_out, void* stream) {
   return pb::launch_wave_selftest(d_out, static_cast<hipStream_t>(stream)) == hipSuccess
+             ? PB_OK
+             : PB_DEVICE;
+}
+
+uint32_t pb_device_read_probe(const uint32_t* d_in, size_t n_words, uint32_t* d_out,
+                              uint32_t blocks, void* stream) {
+  if (((uintptr_t)d_in & 15u) != 0) return PB_ALIGNMENT;
+  return pb::launch_read_probe(d_in, n_words, d_out, blocks, static_cast<hipStream_t>(stream)) ==
+                 hipSuccess
              ? PB_OK
              : PB_DEVICE;
 }

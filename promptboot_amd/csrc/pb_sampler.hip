@@ -654,6 +654,43 @@ hipError_t launch_probe(int which, const uint32_t* in, uint32_t* out, size_t n,
   return hipGetLastError();
 }
 
+// Read-only stream probe: each workgroup reads a contiguous run of float4
+// with the sampler's access pattern (256 threads, kChunkF4 float4 per thread
+// in flight, non-temporal loads) and writes one word, the XOR of what it read,
+// so the loads cannot be dropped.  Its rate is the read bandwidth the
+// sampler's own stream can reach on this device: the ceiling the segment
+// kernel is measured against besides the datasheet peak.
+__global__ __launch_bounds__(kBlock) void read_probe_kernel(const v4u* __restrict__ in,
+                                                            size_t n4, size_t per_block,
+                                                            uint32_t* out) {
+  const size_t lo = (size_t)blockIdx.x * per_block;
+  const size_t hi = lo + per_block < n4 ? lo + per_block : n4;
+  uint32_t acc = 0;
+  for (size_t base = lo; base < hi; base += (size_t)kBlock * kChunkF4) {
+    v4u x[kChunkF4];
+#pragma unroll
+    for (int j = 0; j < kChunkF4; ++j) {
+      const size_t f = base + (size_t)j * kBlock + threadIdx.x;
+      x[j] = f < hi ? __builtin_nontemporal_load(in + f) : v4u{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int j = 0; j < kChunkF4; ++j) acc ^= x[j].x ^ x[j].y ^ x[j].z ^ x[j].w;
+  }
+  acc = wave_min_u32(acc) ^ acc;  // every lane's value reaches the store
+  if ((threadIdx.x & 63u) == 0) atomicXor(out + blockIdx.x, acc);
+}
+
+hipError_t launch_read_probe(const uint32_t* in, size_t n_words, uint32_t* out, uint32_t blocks,
+                             hipStream_t stream) {
+  (void)hipGetLastError();  // report only this call's launch errors
+  const size_t n4 = n_words / 4;
+  if (n4 == 0 || blocks == 0) return hipSuccess;
+  const size_t per_block = (n4 + blocks - 1) / blocks;
+  hipLaunchKernelGGL(read_probe_kernel, dim3(blocks), dim3(kBlock), 0, stream,
+                     reinterpret_cast<const v4u*>(in), n4, per_block, out);
+  return hipGetLastError();
+}
+
 hipError_t launch_writeback(const WritebackParams& p, hipStream_t stream) {
   (void)hipGetLastError();  // report only this call's launch errors
   hipLaunchKernelGGL(writeback_kernel, dim3(p.rows), dim3(kBlock), 0, stream, p);

@@ -118,6 +118,7 @@ EXPORTS = {
     "pb_device_expf_bits": (u32, [vp, vp, size_t, vp]),
     "pb_device_penalize_bits": (u32, [vp, vp, size_t, vp]),
     "pb_device_wave_selftest": (u32, [vp, vp]),
+    "pb_device_read_probe": (u32, [vp, size_t, vp, u32, vp]),
     "pb_device_mfma_selftest": (u32, [vp, vp]),
     "pb_lmhead_packed_bytes": (size_t, [size_t, size_t]),
     "pb_lmhead_pack_q4_0": (u32, [vp, size_t, size_t, vp, vp, ctypes.POINTER(_Error)]),
@@ -398,6 +399,54 @@ class BatchSampler:
             st = lib().pb_sample_batch(self._ctx, ptrs[0], VOCAB, ld, rows, ptrs[1], hist_ld,
                                        ptrs[2], ptrs[3], *outs, s, ctypes.byref(e))
         _check(st, e)
+
+    def bind_sample(self, logits, random_24, history=None, history_len=None, *, token=None,
+                    detail=None, err=None, stream=None):
+        """A zero-argument callable that enqueues this exact pb_sample_batch
+        call: the arguments are checked and converted once, so each call
+        costs one foreign call, as it does a C caller (for timing loops)."""
+        rows, ld = _shape(logits)
+        hist_ld = _shape(history)[1] if history is not None else 0
+        self._ensure(rows)
+        args = dict(rows=rows)
+        argv = (self._ctx, _dev(logits, "logits", ndim=2), VOCAB, ld, rows,
+                _dev(history, "history", ndim=2, **args), hist_ld,
+                _dev(history_len, "history_len", **args), _dev(random_24, "random_24", **args),
+                _dev(token, "token", **args), _dev(detail, "detail", row_elems=84, **args),
+                _dev(err, "err", row_elems=12, **args), vp(hip.stream_handle(stream)))
+        fn = lib().pb_sample_batch
+
+        def call():
+            e = _Error()
+            st = fn(*argv, ctypes.byref(e))
+            if st != OK:
+                raise InferenceError(e)
+
+        return call
+
+    def bind_lmhead(self, packed, hidden, random_24, history=None, history_len=None, *,
+                    token, detail=None, err=None, logits=None, stream=None, q8: bool = False):
+        """bind_sample for the fused LM head + sampler (lmhead_sample)."""
+        rows, width, nbytes = self._head_args(packed, hidden, None, q8)
+        self._ensure(rows, width)
+        hist_ld = _shape(history)[1] if history is not None else 0
+        args = dict(rows=rows)
+        argv = (self._ctx, _dev(packed, "packed", itemsize=1), nbytes, VOCAB, width,
+                _dev(hidden, "hidden", ndim=2), rows, _dev(history, "history", ndim=2, **args),
+                hist_ld, _dev(history_len, "history_len", **args),
+                _dev(random_24, "random_24", **args), _dev(token, "token", **args),
+                _dev(detail, "detail", row_elems=84, **args),
+                _dev(err, "err", row_elems=12, **args),
+                _dev(logits, "logits", row_elems=VOCAB, **args), vp(hip.stream_handle(stream)))
+        fn = lib().pb_lmhead_q8_sample_batch if q8 else lib().pb_lmhead_sample_batch
+
+        def call():
+            e = _Error()
+            st = fn(*argv, ctypes.byref(e))
+            if st != OK:
+                raise InferenceError(e)
+
+        return call
 
     def pack_lmhead(self, weights, vocab: int = VOCAB, cols: int = 896, stream=None,
                     q8: bool = False) -> hip.DeviceArray:
