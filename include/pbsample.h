@@ -277,7 +277,7 @@ uint32_t pb_lmhead_pack_q4_0(const uint8_t *d_q4, size_t vocab, size_t cols, uin
                              void *stream, pb_inference_error *err);
 
 /* One decode step for `rows` sequences: hidden states (rows x cols binary32
- * words) through the packed head, then the sampler exactly as pb_sample_batch
+ * words, 16-byte aligned) through the packed head, then the sampler exactly as pb_sample_batch
  * on the resulting logits (repetition penalty, top-k 20, temperature 0.7,
  * top-p 0.8, draw).  vocab must be PB_VOCAB, cols a multiple of 32 up to 2048
  * (896 for Qwen2.5-0.5B).  packed_bytes is the size of d_packed and must be

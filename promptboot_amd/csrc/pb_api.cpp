@@ -141,16 +141,26 @@ static size_t max_slots(uint32_t rows, uint32_t forced_segments) {
   return best;
 }
 
-// Fused LM head workspace for `rows` rows of `cols` columns (either format),
-// logits included.
-static size_t lm_workspace_bytes(uint32_t rows, size_t cols, bool with_logits) {
+// Fused LM head workspace for `rows` rows of `cols` columns (either format):
+// the Q8_0 activations and their scales, the tile maxima and, unless the
+// caller keeps them, the logits.
+struct LmLayout {
+  size_t act_q, act_s, tilemax, logits, total;
+};
+static LmLayout lm_layout(uint32_t rows, size_t cols, bool with_logits) {
   auto align = [](size_t x) { return (x + 255) & ~(size_t)255; };
   const size_t rows_pad = ((size_t)rows + 63u) & ~(size_t)63u;
   const size_t blocks = cols / 32;
-  return align((size_t)rows * (PB_VOCAB / 32) * 4) + align((size_t)rows * 8) +
-         align(blocks * rows_pad * 32) + align(blocks * rows_pad * 4) +
-         align((size_t)rows * (PB_VOCAB / 64) * 4) +
-         (with_logits ? align((size_t)rows * PB_VOCAB * 4) : 0);
+  LmLayout l;
+  l.act_q = 0;
+  l.act_s = l.act_q + align(blocks * rows_pad * 32);
+  l.tilemax = l.act_s + align(blocks * rows_pad * 4);
+  l.logits = l.tilemax + align((size_t)rows * (PB_VOCAB / 64) * 4);
+  l.total = l.logits + (with_logits ? align((size_t)rows * PB_VOCAB * 4) : 0);
+  return l;
+}
+static size_t lm_workspace_bytes(uint32_t rows, size_t cols, bool with_logits) {
+  return lm_layout(rows, cols, with_logits).total;
 }
 
 static void free_staging(pb_context* ctx) {
@@ -588,7 +598,8 @@ static uint32_t enqueue_lmhead(pb_context* ctx, const uint8_t* d_packed, size_t 
     set_error(err, PB_CAPACITY, PB_DOMAIN_NONE, want, packed_bytes, PB_FIELD_BYTES, 7);
     return PB_CAPACITY;
   }
-  if (((uintptr_t)d_packed & 15u) != 0 || ((uintptr_t)d_logits & 15u) != 0) {
+  if (((uintptr_t)d_packed & 15u) != 0 || ((uintptr_t)d_logits & 15u) != 0 ||
+      ((uintptr_t)d_hidden & 15u) != 0) {
     set_error(err, PB_ALIGNMENT, PB_DOMAIN_NONE, 16, 0, PB_FIELD_ALIGNMENT, 2);
     return PB_ALIGNMENT;
   }
@@ -599,15 +610,9 @@ static uint32_t enqueue_lmhead(pb_context* ctx, const uint8_t* d_packed, size_t 
     return PB_CAPACITY;
   }
   const uint32_t rows_pad = (rows + 63u) & ~63u;
-  const uint32_t blocks = (uint32_t)(cols / 32);
-  auto align = [](size_t x) { return (x + 255) & ~(size_t)255; };
-  const size_t bitmap_b = align((size_t)rows * (PB_VOCAB / 32) * 4);
-  const size_t meta_b = align((size_t)rows * 8);
-  const size_t actq_b = align((size_t)blocks * rows_pad * 32);
-  const size_t acts_b = align((size_t)blocks * rows_pad * 4);
-  const size_t tile_b = align((size_t)rows * (PB_VOCAB / 64) * 4);
   std::lock_guard<std::mutex> lock(ctx->mu);
-  const size_t need = lm_workspace_bytes(rows, cols, d_logits == nullptr);
+  const LmLayout lay = lm_layout(rows, cols, d_logits == nullptr);
+  const size_t need = lay.total;
   if (need > ctx->lm_bytes) {
     set_error(err, PB_CAPACITY, PB_DOMAIN_NONE, need, ctx->lm_bytes, PB_FIELD_BYTES, 6);
     return PB_CAPACITY;
@@ -621,17 +626,11 @@ static uint32_t enqueue_lmhead(pb_context* ctx, const uint8_t* d_packed, size_t 
   p.rows = rows;
   p.rows_pad = rows_pad;
   p.cols = (uint32_t)cols;
-  p.hist = d_hist_len ? d_hist : nullptr;
-  p.hist_ld = hist_ld;
-  p.hist_len = d_hist_len;
-  p.bitmap = reinterpret_cast<uint32_t*>(base);
-  p.meta = reinterpret_cast<uint32_t*>(base + bitmap_b);
-  p.act_q = reinterpret_cast<int8_t*>(base + bitmap_b + meta_b);
-  p.act_s = reinterpret_cast<float*>(base + bitmap_b + meta_b + actq_b);
-  p.tilemax = reinterpret_cast<uint32_t*>(base + bitmap_b + meta_b + actq_b + acts_b);
-  p.logits = d_logits ? d_logits
-                      : reinterpret_cast<uint32_t*>(base + bitmap_b + meta_b + actq_b + acts_b +
-                                                    tile_b);
+  p.fused_quant = rows <= pb::kFusedQuantRows;
+  p.act_q = reinterpret_cast<int8_t*>(base + lay.act_q);
+  p.act_s = reinterpret_cast<float*>(base + lay.act_s);
+  p.tilemax = reinterpret_cast<uint32_t*>(base + lay.tilemax);
+  p.logits = d_logits ? d_logits : reinterpret_cast<uint32_t*>(base + lay.logits);
   p.logits_ld = PB_VOCAB;
 
   pb::RowParams rp;
@@ -639,9 +638,11 @@ static uint32_t enqueue_lmhead(pb_context* ctx, const uint8_t* d_packed, size_t 
   rp.logits = p.logits;
   rp.ld = PB_VOCAB;
   rp.rows = rows;
-  rp.hist = p.hist;
+  rp.hist = d_hist_len ? d_hist : nullptr;
   rp.hist_ld = hist_ld;
   rp.hist_len = d_hist_len;
+  rp.hist_vec4 = (rp.hist != nullptr && hist_ld >= 4u && (hist_ld & 3u) == 0 &&
+                  ((uintptr_t)d_hist & 15u) == 0);
   rp.random_24 = d_random_24;
   rp.token = d_token;
   rp.detail = d_detail;

@@ -51,26 +51,26 @@ struct WritebackParams {
   uint32_t* gather;        // rows x hist_ld final values at the history ids, or null
 };
 
-// Fused Q4_0 LM head + sampler (pb_lmhead.hip).
+// Fused Q4_0 / Q8_0 LM head + sampler (pb_lmhead.hip).
 struct LmParams {
   const uint8_t* weights;   // packed head: [blocks][vocab][16] nibbles (Q4_0) or [32] int8
                             // (Q8_0), then [blocks][vocab] fp16 scales
   bool q8;                  // the head is Q8_0 (else Q4_0)
+  bool fused_quant;         // the GEMM quantises the activations itself (few rows)
   const uint32_t* hidden;   // rows x cols binary32 words
   uint32_t rows;
   uint32_t rows_pad;        // rows rounded up to 64
   uint32_t cols;            // hidden width, multiple of 32
-  const uint32_t* hist;
-  size_t hist_ld;
-  const uint32_t* hist_len;
-  uint32_t* bitmap;         // rows x 4,748 history bitmap words
-  uint32_t* meta;           // rows x {first non-finite logit, first bad history position}
   int8_t* act_q;            // [blocks][rows_pad][32] Q8_0 quants
-  float* act_s;             // [blocks][rows_pad] activation scales
+  float* act_s;             // [blocks][rows_pad] activation scales / 16
   uint32_t* logits;         // rows x logits_ld raw logits (binary32 words)
   size_t logits_ld;
-  uint32_t* tilemax;        // rows x 2,374 order word of the largest penalised value per 64-id tile
+  uint32_t* tilemax;        // rows x 2,374 order word of the largest raw logit per 64-id
+                            // tile, 0xffffffff when the tile holds a non-finite logit
 };
+
+// Rows up to which the narrow GEMM quantises the activations itself.
+constexpr uint32_t kFusedQuantRows = 4;
 
 hipError_t launch_lm_pack(const uint8_t* in, uint8_t* out, uint32_t vocab, uint32_t blocks,
                           hipStream_t stream);

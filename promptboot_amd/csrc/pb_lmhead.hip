@@ -8,23 +8,24 @@
 // followed by the sampler of pb_sampler.hip on the resulting logits rows.
 //
 // Kernels, in launch order:
-//   lm_prep_kernel     one workgroup per row (rows padded to 64): the Q8_0
-//                      activations (in the head's contraction order) and the
-//                      fp32 activation scales divided by 16, zeros for pad
-//                      rows; the row's history as a 151,936-bit bitmap
-//                      (global) and its first bad history position.
+//   lm_quant_kernel    (more than kFusedQuantRows rows) one thread per (row,
+//                      block): the Q8_0 activations in the head's contraction
+//                      order and the fp32 activation scales divided by 16,
+//                      zeros for padding rows.
 //   lm_gemm_kernel     one workgroup per (64-id vocabulary tile, 256 rows):
 //                      v_mfma_i32_16x16x32_i8 gives each block's exact int32
 //                      dot; the reference's per-block binary32 epilogue runs on
 //                      the VALU.  Writes the raw logits and, per (row, tile),
-//                      the order word of the largest penalised value.
-//   lm_select_kernel   one wave per row: the row's top-20 lies inside the 20
-//                      tiles with the largest maxima (each of the 20 best tile
-//                      maxima is a distinct element at least as good as the
-//                      20th best of them, so every top-20 element sits in one
-//                      of those tiles); it re-reads those 1,280 logits,
-//                      selects exactly, and finishes the row (softmax, top-p,
-//                      draw) with the sampler's finalize_row.
+//                      the order word of the largest raw logit.
+//   lm_gemm_narrow_kernel  the same for up to 64 rows, one wave per tile;
+//                      with up to kFusedQuantRows rows each workgroup
+//                      quantises the activations itself (no lm_quant_kernel).
+//   lm_select_kernel   one workgroup per row: the history bitmap in LDS, then
+//                      the exact top-20 of the penalised logits best-first
+//                      over the tiles (the penalty never raises a value, so a
+//                      tile's raw maximum bounds its penalised elements), and
+//                      the row's finish (softmax, top-p, draw) with the
+//                      sampler's finalize_row.
 //
 // Weight nibbles are stored XOR 8 and expanded to int8 by masking them into
 // the high half of a byte: (n ^ 8) << 4 = 16 * (n - 8) as a signed byte.  The
@@ -60,7 +61,6 @@ constexpr uint32_t kRowsPerGroup = 256;
 constexpr uint32_t kNarrowRows = 64;
 constexpr uint32_t kWordsPerRow = kVocab / 32;
 constexpr uint32_t kTilesPerRow = kVocab / kTileIds;  // 2,374
-constexpr uint32_t kCandCap = 800;       // >= 20 lanes x 38 tile keys
 constexpr uint32_t kTileBytes = kTileIds * 16;    // packed Q4_0 nibbles of one (block, tile)
 constexpr uint32_t kTileBytesQ8 = kTileIds * 32;  // packed Q8_0 weights of one (block, tile)
 // M = 1.5 * 2^23: its binade has unit spacing, so M + i is exact for |i| < 2^22.
@@ -195,16 +195,17 @@ __global__ __launch_bounds__(kBlockThreads) void lm_pack_q8_kernel(const uint8_t
   scales[(size_t)b * vocab + v] = (uint16_t)(src[0] | (src[1] << 8));
 }
 
-// ---- Q8_0 activations of one (row, block) (inference_prepare_q8) ----
-// act_q: [blocks][rows_pad][32] int8 in the head's contraction order: bytes
-// 8q .. 8q+7 hold elements 4q .. 4q+3 and 16+4q .. 16+4q+3 (q = 0..3).
-// act_s: [blocks][rows_pad] the fp32 scale the dot uses (half_to_f32 of the
-// stored fp16) times 2^-4, which is exact.  Pad rows are zero.
-__device__ __forceinline__ void quantize_block(const LmParams& p, uint32_t row, uint32_t b,
-                                               const uint32_t (&x)[32]) {
-  uint32_t packed[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
+// ---- Q8_0 activations of one block (inference_prepare_q8) ----
+// The 32 quants of one block of 32 activations in the head's contraction
+// order (bytes 8q .. 8q+7 hold elements 4q .. 4q+3 and 16+4q .. 16+4q+3,
+// q = 0..3), and the fp32 scale the dot uses (half_to_f32 of the stored fp16)
+// times 2^-4, which is exact.  A padding row (live == false) gives zeros.
+__device__ __forceinline__ void quantize_block(const uint32_t (&x)[32], bool live,
+                                               uint32_t (&packed)[8], float& scale16) {
+#pragma unroll
+  for (int k = 0; k < 8; ++k) packed[k] = 0u;
   float act_scale = 0.0f;
-  if (row < p.rows) {
+  if (live) {
     uint32_t maximum = 0u;
 #pragma unroll
     for (int e = 0; e < 32; ++e) {
@@ -223,160 +224,94 @@ __device__ __forceinline__ void quantize_block(const LmParams& p, uint32_t row, 
       packed[2 * ((e & 15) >> 2) + (e >> 4)] |= q << (8 * (e & 3));
     }
   }
+  scale16 = act_scale * 0.0625f;
+}
+
+// The 32 activations of (row, block b) as binary32 words, 16-byte loads.
+__device__ __forceinline__ void load_block(const LmParams& p, uint32_t row, uint32_t b,
+                                           uint32_t (&x)[32]) {
+  const v4u* src = reinterpret_cast<const v4u*>(p.hidden + (size_t)row * p.cols + b * 32u);
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const v4u v = src[k];
+    x[4 * k + 0] = v.x;
+    x[4 * k + 1] = v.y;
+    x[4 * k + 2] = v.z;
+    x[4 * k + 3] = v.w;
+  }
+}
+
+// ---- Q8_0 activations of every (row, block), batches above kFusedQuantRows ----
+// act_q: [blocks][rows_pad][32] int8 in the contraction order; act_s:
+// [blocks][rows_pad] scales / 16.  Padding rows are zero.  One thread per
+// (row, block).
+__global__ __launch_bounds__(kBlockThreads) void lm_quant_kernel(LmParams p) {
+  const uint32_t blocks = p.cols / 32u;
+  const uint32_t g = blockIdx.x * kBlockThreads + threadIdx.x;
+  if (g >= p.rows_pad * blocks) return;
+  const uint32_t row = g / blocks;
+  const uint32_t b = g - row * blocks;
+  const bool live = row < p.rows;
+  uint32_t x[32];
+  if (live) {
+    load_block(p, row, b, x);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 32; ++e) x[e] = 0u;
+  }
+  uint32_t packed[8];
+  float scale16;
+  quantize_block(x, live, packed, scale16);
   v4u* dst = reinterpret_cast<v4u*>(p.act_q + ((size_t)b * p.rows_pad + row) * 32);
   dst[0] = v4u{packed[0], packed[1], packed[2], packed[3]};
   dst[1] = v4u{packed[4], packed[5], packed[6], packed[7]};
-  p.act_s[(size_t)b * p.rows_pad + row] = act_scale * 0.0625f;
+  p.act_s[(size_t)b * p.rows_pad + row] = scale16;
 }
 
-// ---- per row: Q8_0 activations, history bitmap, first bad history position ----
-// One workgroup per padded row: threads 0 .. blocks-1 quantise the row's
-// blocks (pad rows get zeros) while the workgroup builds the row's 151,936-bit
-// history bitmap in LDS and writes it out.  Every load is requested first --
-// the quantisers' inputs, the history length and the first 1,024 ids of the
-// padded history row (ids past the length are ignored) -- so the bitmap is
-// built while the quantisers' inputs arrive.
-__global__ __launch_bounds__(kBlockThreads) void lm_prep_kernel(LmParams p) {
-  constexpr uint32_t kEarlyIds = 4;  // history ids per thread requested up front
-  __shared__ uint32_t bm[kWordsPerRow];
-  __shared__ uint32_t bad;
-  const uint32_t row = blockIdx.x;
-  const uint32_t tid = threadIdx.x;
-  const bool live = row < p.rows;
-  const bool quantiser = tid < p.cols / 32u;
-  uint32_t x[32];
-#pragma unroll
-  for (int e = 0; e < 32; ++e)
-    x[e] = quantiser && live ? p.hidden[(size_t)row * p.cols + tid * 32u + (uint32_t)e] : 0u;
-  const bool has_hist = live && p.hist != nullptr && p.hist_len != nullptr;
-  const uint32_t* hrow = p.hist + (size_t)row * p.hist_ld;
-  uint32_t early[kEarlyIds];
-#pragma unroll
-  for (uint32_t u = 0; u < kEarlyIds; ++u) {
-    const uint32_t q = tid + u * kBlockThreads;
-    early[u] = has_hist && q < p.hist_ld ? hrow[q] : 0u;
-  }
-  uint32_t len = has_hist ? p.hist_len[row] : 0u;
-  if ((size_t)len > p.hist_ld) len = (uint32_t)p.hist_ld;
-  if (!live) {  // pad row: zero activations only (the whole workgroup leaves here)
-    if (quantiser) quantize_block(p, row, tid, x);
-    return;
-  }
-  for (uint32_t i = tid; i < kWordsPerRow; i += kBlockThreads) bm[i] = 0u;
-  if (tid == 0) bad = kNone;
-  __syncthreads();
-  uint32_t my_bad = kNone;
-  auto add = [&](uint32_t q, uint32_t id) {
-    if (id >= kVocab) {
-      my_bad = q < my_bad ? q : my_bad;
-    } else {
-      uint32_t* word = &bm[id >> 5];
-      const uint32_t bit = 1u << (id & 31u);
-      if ((__hip_atomic_load(word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) & bit) == 0u)
-        atomicOr(word, bit);
-    }
-  };
-#pragma unroll
-  for (uint32_t u = 0; u < kEarlyIds; ++u) {
-    const uint32_t q = tid + u * kBlockThreads;
-    if (q < len) add(q, early[u]);
-  }
-  for (uint32_t q = tid + kEarlyIds * kBlockThreads; q < len; q += kBlockThreads) add(q, hrow[q]);
-  if (quantiser) quantize_block(p, row, tid, x);
-  if (my_bad != kNone) atomicMin(&bad, my_bad);
-  __syncthreads();
-  uint32_t* out = p.bitmap + (size_t)row * kWordsPerRow;
-  for (uint32_t i = tid; i < kWordsPerRow; i += kBlockThreads) out[i] = bm[i];
-  if (tid == 0) {
-    p.meta[row * 2 + 0] = kNone;  // first non-finite logit, lowered by the GEMM
-    p.meta[row * 2 + 1] = bad;
-  }
-}
+// Tile word of a row whose 64 logits in the tile include an infinite or NaN
+// one (above every finite order word, which is at most 0xff7fffff).
+constexpr uint32_t kNonFiniteTile = 0xffffffffu;
 
 // ---- a wave's results for one 64-id tile ----
 // total[rt][c][i] is row first_row + 16 rt + i, id 64 tile + 4n + c, where
 // first_row is the lane's row of step 0 (lanes 16q .. 16q+15 hold rows 4q + i
-// of each row tile, four consecutive ids per lane).  hb_all holds four
-// history bits per step s = 4 rt + i.  Writes the raw logits, lowers each
-// row's first non-finite index, and writes per row the order word of the
-// tile's largest penalised value.  The steps run in passes (stores and raw
-// maxima, then the penalty, then the row maxima) so that the DPP chains
-// interleave; the penalty sits behind one wave-uniform branch, since a wave's
-// rows rarely hold a history id in a 64-id tile.
-template <int kRT>
+// of each row tile, four consecutive ids per lane).  For the real rows among
+// result registers i < kI: stores the raw logits and the order word of the
+// tile's largest raw logit (kNonFiniteTile when one of them is infinite or
+// NaN).  The repetition penalty is not applied here: the selection applies it
+// to the few tiles it reads (it never raises a value, so the raw maximum
+// bounds the penalised ones).
+template <int kRT, int kI>
 __device__ __forceinline__ void write_tile(const LmParams& p, const float (&total)[kRT][4][4],
-                                           uint32_t hb_all, uint32_t first_row, uint32_t tile,
-                                           uint32_t n) {
-  constexpr int kSteps = 4 * kRT;
+                                           uint32_t first_row, uint32_t tile, uint32_t n) {
+  constexpr int kSteps = kRT * kI;
   const uint32_t v0 = tile * kTileIds;
-  float probe = 0.0f;
-  float m[kSteps];
   const size_t ld = p.logits_ld;
   uint32_t* lbase = p.logits + (size_t)first_row * ld + v0 + 4u * n;
-#pragma unroll
-  for (int s = 0; s < kSteps; ++s) {
-    const int rt = s >> 2, i = s & 3;
-    const float y[4] = {total[rt][0][i], total[rt][1][i], total[rt][2][i], total[rt][3][i]};
-    if (first_row + 16u * (uint32_t)rt + (uint32_t)i < p.rows)
-      *reinterpret_cast<v4f*>(lbase + (size_t)(16 * rt + i) * ld) = v4f{y[0], y[1], y[2], y[3]};
-#pragma unroll
-    for (int c = 0; c < 4; ++c) probe = __builtin_fmaf(y[c], 0.0f, probe);
-    m[s] = fmaxf(fmaxf(y[0], y[1]), fmaxf(y[2], y[3]));
-  }
-  // The penalty is monotone (x <= y gives pen(x) <= pen(y)), so the largest
-  // penalised history value is the penalty of the largest history value: one
-  // penalty per lane and step.  NaN is the identity of fmaxf, so a side with
-  // no element stays NaN and drops out, and pen(NaN) is NaN.  (A lane whose
-  // four values are all NaN may give another NaN than the per-element form;
-  // such a row is an error row, whose tile maxima are not used.)
-  if (__ballot(hb_all != 0u)) {
-    const float kNaN = __builtin_nanf("");
-#pragma unroll
-    for (int s = 0; s < kSteps; ++s) {
-      const int rt = s >> 2, i = s & 3;
-      const uint32_t hb = (hb_all >> (4 * s)) & 0xfu;
-      if (hb != 0u) {
-        float h[4], u[4];
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const bool hit = ((hb >> c) & 1u) != 0u;
-          h[c] = hit ? total[rt][c][i] : kNaN;
-          u[c] = hit ? kNaN : total[rt][c][i];
-        }
-        const float mh = fmaxf(fmaxf(h[0], h[1]), fmaxf(h[2], h[3]));
-        const float mu = fmaxf(fmaxf(u[0], u[1]), fmaxf(u[2], u[3]));
-        m[s] = fmaxf(mu, f_of(penalize_bits(b_of(mh))));
-      }
-    }
-  }
-  // order word of each row's largest value in the tile (ord_of: adding +0
-  // turns -0 into +0, then negative values are inverted)
   uint32_t o[kSteps];
 #pragma unroll
   for (int s = 0; s < kSteps; ++s) {
-    o[s] = b_of(m[s] + 0.0f);
-    o[s] ^= (uint32_t)((int32_t)o[s] >> 31) | 0x80000000u;
+    const int rt = s / kI, i = s % kI;
+    const float y[4] = {total[rt][0][i], total[rt][1][i], total[rt][2][i], total[rt][3][i]};
+    if (first_row + 16u * (uint32_t)rt + (uint32_t)i < p.rows)
+      *reinterpret_cast<v4f*>(lbase + (size_t)(16 * rt + i) * ld) = v4f{y[0], y[1], y[2], y[3]};
+    // y * 0 is NaN exactly when y is infinite or NaN
+    const float probe = __builtin_fmaf(
+        y[0], 0.0f, __builtin_fmaf(y[1], 0.0f, __builtin_fmaf(y[2], 0.0f, y[3] * 0.0f)));
+    const float m = fmaxf(fmaxf(y[0], y[1]), fmaxf(y[2], y[3]));
+    // order word of the maximum: adding +0 turns -0 into +0, then negative
+    // values are inverted
+    uint32_t w = b_of(m + 0.0f);
+    w ^= (uint32_t)((int32_t)w >> 31) | 0x80000000u;
+    o[s] = probe != probe ? kNonFiniteTile : w;
   }
 #pragma unroll
   for (int s = 0; s < kSteps; ++s) o[s] = row16_max_u32(o[s]);
   if (n == 0u) {
 #pragma unroll
     for (int s = 0; s < kSteps; ++s) {
-      const uint32_t row = first_row + 16u * (uint32_t)(s >> 2) + (uint32_t)(s & 3);
+      const uint32_t row = first_row + 16u * (uint32_t)(s / kI) + (uint32_t)(s % kI);
       if (row < p.rows) p.tilemax[(size_t)row * kTilesPerRow + tile] = o[s];
-    }
-  }
-  if (__ballot(probe != probe)) {
-    // a non-finite raw logit in this wave's rows: lower each row's first index
-#pragma unroll
-    for (int s = 0; s < kSteps; ++s) {
-      const int rt = s >> 2, i = s & 3;
-      const uint32_t row = first_row + 16u * (uint32_t)rt + (uint32_t)i;
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        if (row < p.rows && (b_of(total[rt][c][i]) & 0x7f800000u) == 0x7f800000u)
-          atomicMin(&p.meta[row * 2], v0 + 4u * n + (uint32_t)c);
-      }
     }
   }
 }
@@ -397,7 +332,7 @@ __device__ __forceinline__ void write_tile(const LmParams& p, const float (&tota
 // exactly M + 16 dot (|16 dot| < 2^19).  fma(M + 16 dot, ws, -M ws) is then
 // 16 dot ws rounded once (M ws is exact: ws has at most 11 significant bits),
 // which is 16 times the reference's mul(f32(dot), ws); its product with
-// a_scale / 16 (from lm_prep_kernel) is the reference's
+// a_scale / 16 (from quantize_block) is the reference's
 // mul(mul(f32(dot), ws), a_scale) bit for bit.  Scaling by powers of two is
 // exact here: |16 dot ws| is 0 or lies in [2^-20, 2^36), far from the
 // subnormal and overflow ranges.  A tile with an infinite or NaN fp16 weight
@@ -416,7 +351,6 @@ __global__ __launch_bounds__(kGemmThreads) void lm_gemm_kernel(LmParams p) {
   // Dynamic LDS: the activation scales / 16 of every block for the group's
   // 256 rows, then this tile's weight scales and -M * weight scales by block.
   extern __shared__ __align__(16) float lds[];
-  __shared__ uint32_t hist_words[kRowsPerGroup][2];
   const uint32_t blocks = p.cols / 32u;
   float* act_scale = lds;
   float* w_scale = lds + blocks * kRowsPerGroup;
@@ -443,14 +377,10 @@ __global__ __launch_bounds__(kGemmThreads) void lm_gemm_kernel(LmParams p) {
       odd |= (b_of(ws) & 0x7f800000u) == 0x7f800000u ? 1u : 0u;
     }
   }
-  for (uint32_t i = tid; i < kRowsPerGroup * 2; i += kGemmThreads) {
-    const uint32_t r = group0 + i / 2;
-    (&hist_words[0][0])[i] = r < p.rows ? p.bitmap[(size_t)r * kWordsPerRow + v0 / 32 + i % 2] : 0u;
-  }
   for (uint32_t i = tid; i < blocks * kRowsPerGroup; i += kGemmThreads) {
     const uint32_t b = i / kRowsPerGroup;
     const uint32_t r = group0 + (i - b * kRowsPerGroup);
-    // lm_prep_kernel stores a_scale / 16 (exact); the Q8_0 epilogue needs a_scale
+    // lm_quant_kernel stores a_scale / 16 (exact); the Q8_0 epilogue needs a_scale
     const float as16 = r < p.rows_pad ? p.act_s[(size_t)b * p.rows_pad + r] : 0.0f;
     act_scale[i] = kQ8 ? as16 * 16.0f : as16;
   }
@@ -608,15 +538,7 @@ __global__ __launch_bounds__(kGemmThreads) void lm_gemm_kernel(LmParams p) {
     gemm(std::false_type{});
   }
 
-  // history bits of the lane's four ids for each step s = 4 rt + i (row
-  // lrow0 + 16 rt + 4q + i); bitmap words of rows past p.rows are zero
-  uint32_t hb_all = 0;
-#pragma unroll
-  for (int s = 0; s < 8; ++s) {
-    const uint32_t lr = lrow0 + 16u * (uint32_t)(s >> 2) + 4u * q + (uint32_t)(s & 3);
-    hb_all |= ((hist_words[lr][n >> 3] >> (4u * (n & 7u))) & 0xfu) << (4 * s);
-  }
-  write_tile<2>(p, total, hb_all, group0 + lrow0 + 4u * q, tile, n);
+  write_tile<2, 4>(p, total, group0 + lrow0 + 4u * q, tile, n);
 }
 
 // ---- the head for narrow batches (up to 64 rows) ----
@@ -624,43 +546,48 @@ __global__ __launch_bounds__(kGemmThreads) void lm_gemm_kernel(LmParams p) {
 // 32 rows of one 64-id tile; with few rows most of that work is padding.
 // Here one wave takes one 64-id tile and 16 kRT rows (one MFMA row tile up
 // to 32 rows, two above), four waves per workgroup over consecutive tiles,
-// the grid's y over the row groups.  Each block's weight and activation scales are loaded with
-// its operands (four fp16 weight scales and 4 kRT activation scales per
-// lane), and the loads run kSets - 1 blocks ahead in rotating operand sets:
-// with one wave per tile, the memory in flight per wave is what keeps the
-// weights streaming.  The epilogue is the wide kernel's, for both formats; a
-// Q4_0 tile flagged at pack time for an infinite or NaN weight scale takes the
-// subtract-then-multiply form for all its blocks.  The loop body has no branch:
-// at a branch's join the compiler waits for every load in flight, which would
-// undo the loads issued ahead.  With at most four rows every real row is
-// result register i < kI of lanes 0 .. 15, so the epilogue of the other
-// registers (padding rows) is left out: kI = 1 for one conversation.
-template <bool kQ8, int kRT, int kSets, int kI>
+// the grid's y over the row groups.  Each block's weight and activation
+// scales are loaded with its operands (four fp16 weight scales and 4 kRT
+// activation scales per lane), and the loads run kSets - 1 blocks ahead in
+// rotating operand sets: with one wave per tile, the memory in flight per
+// wave is what keeps the weights streaming.  The epilogue is the wide
+// kernel's, for both formats; a Q4_0 tile flagged at pack time for an
+// infinite or NaN weight scale takes the subtract-then-multiply form for all
+// its blocks.  The loop body has no branch: at a branch's join the compiler
+// waits for every load in flight, which would undo the loads issued ahead.
+// With at most four rows every real row is result register i < kI of lanes
+// 0 .. 15, so the epilogue of the other registers (padding rows) is left
+// out: kI = 1 for one conversation.
+//
+// kFused (at most kFusedQuantRows rows): each workgroup quantises the rows'
+// activations itself, into LDS, instead of reading them from lm_quant_kernel
+// -- one launch less per step.  The first blocks' weights are requested
+// before the quantisation, so it overlaps their latency.
+constexpr uint32_t kMaxBlocks = 2048 / 32;
+template <bool kQ8, int kRT, int kSets, int kI, bool kFused>
 __global__ __launch_bounds__(256) void lm_gemm_narrow_kernel(LmParams p) {
   static_assert(kI == 4 || kRT == 1, "partial rows only with one row tile");
+  static_assert(!kFused || (kRT == 1 && kI <= (int)kFusedQuantRows), "fused rows fit one row tile");
+  // kFused: [block][row] quants (8 words) and scales / 16 of the real rows
+  __shared__ __align__(16) uint32_t aq_lds[kFused ? kMaxBlocks : 1][kFused ? kFusedQuantRows : 1][8];
+  __shared__ __align__(16) float as_lds[kFused ? kMaxBlocks : 1][kFused ? kFusedQuantRows : 1];
   const uint32_t lane = threadIdx.x & 63u;
   // the tile is wave-uniform: held in scalar registers, so every load below
   // is a scalar base plus a 32-bit lane offset, with no 64-bit address
   // arithmetic per lane
-  const uint32_t tile = blockIdx.x * 4u + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  if (tile >= kTilesPerRow) return;  // whole wave, no barrier follows
+  const uint32_t tile_raw = blockIdx.x * 4u + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const bool live_wave = tile_raw < kTilesPerRow;
+  // waves past the last tile work on the last one (and store nothing), so
+  // that every wave reaches the workgroup barrier of the fused quantisation
+  const uint32_t tile = live_wave ? tile_raw : kTilesPerRow - 1u;
+  if (!kFused && !live_wave) return;  // whole wave, no barrier follows
   const uint32_t n = lane & 15u;
   const uint32_t q = lane >> 4;
   const uint32_t row0 = blockIdx.y * (16u * kRT);  // first row of the wave's group
-  const uint32_t v0 = tile * kTileIds;
   const uint32_t blocks = p.cols / 32u;
   const uint32_t last = blocks - 1u;
   constexpr uint32_t kWords = kQ8 ? 2u : 1u;  // uint4 of packed weights per lane and block
   constexpr uint32_t kTile = kQ8 ? kTileBytesQ8 : kTileBytes;
-
-  // history words of the lane's rows, requested before the loop
-  constexpr int kSteps = 4 * kRT;
-  uint32_t hw[kSteps];
-#pragma unroll
-  for (int s = 0; s < kSteps; ++s) {
-    const uint32_t row = row0 + 16u * (uint32_t)(s >> 2) + 4u * q + (uint32_t)(s & 3);
-    hw[s] = row < p.rows ? p.bitmap[(size_t)row * kWordsPerRow + (v0 >> 5) + (n >> 3)] : 0u;
-  }
 
   // Each load is a wave-uniform base plus one 32-bit byte offset (the block's
   // uniform part + the lane's part).  The widths of at most 2048 keep the
@@ -672,7 +599,7 @@ __global__ __launch_bounds__(256) void lm_gemm_narrow_kernel(LmParams p) {
   const uint32_t w_stride = kTilesPerRow * kTile;  // bytes per block
   const uint32_t w_off = tile * kTile + 16u * kWords * lane;
   const uint8_t* ws_base = p.weights;
-  const uint32_t ws_off = blocks * kVocab * (kQ8 ? 32u : 16u) + 2u * v0 + 8u * n;
+  const uint32_t ws_off = blocks * kVocab * (kQ8 ? 32u : 16u) + 2u * tile * kTileIds + 8u * n;
   const uint8_t* as_base = reinterpret_cast<const uint8_t*>(p.act_s);
   const uint32_t as_stride = p.rows_pad * 4u;
   const uint32_t as_off = (row0 + 4u * q) * 4u;
@@ -687,20 +614,32 @@ __global__ __launch_bounds__(256) void lm_gemm_narrow_kernel(LmParams p) {
     uint64_t ws;    // four fp16 weight scales, ids 4n .. 4n+3
     vIf as[kRT];    // activation scales / 16 of rows 16 rt + 4q .. 4q + kI - 1
   };
-  auto load = [&](uint32_t b, Operands& o) {
-    const uint32_t ao = b * a_stride + a_off;
-#pragma unroll
-    for (int rt = 0; rt < kRT; ++rt)
-      o.a[rt] = *reinterpret_cast<const uint64_t*>(a_base + (ao + 16u * 32u * (uint32_t)rt));
+  auto load_w = [&](uint32_t b, Operands& o) {
     const uint32_t wo = b * w_stride + w_off;
 #pragma unroll
     for (uint32_t k = 0; k < kWords; ++k)
       o.raw[k] = *reinterpret_cast<const v4u*>(w_base + (wo + 16u * k));
     o.ws = *reinterpret_cast<const uint64_t*>(ws_base + (b * (kVocab * 2u) + ws_off));
-    const uint32_t so = b * as_stride + as_off;
+  };
+  auto load_a = [&](uint32_t b, Operands& o) {
+    if constexpr (kFused) {
+      // real rows only: lanes n < rows (A) and the q == 0 result registers
+      const uint64_t a = *reinterpret_cast<const uint64_t*>(&aq_lds[b][n & (kFusedQuantRows - 1u)][2u * q]);
+      o.a[0] = n < p.rows ? a : 0ull;
+      vIf v;
 #pragma unroll
-    for (int rt = 0; rt < kRT; ++rt)
-      o.as[rt] = *reinterpret_cast<const vIf*>(as_base + (so + 64u * (uint32_t)rt));
+      for (int i = 0; i < kI; ++i) v[i] = q == 0u ? as_lds[b][i] : 0.0f;
+      o.as[0] = v;
+    } else {
+      const uint32_t ao = b * a_stride + a_off;
+#pragma unroll
+      for (int rt = 0; rt < kRT; ++rt)
+        o.a[rt] = *reinterpret_cast<const uint64_t*>(a_base + (ao + 16u * 32u * (uint32_t)rt));
+      const uint32_t so = b * as_stride + as_off;
+#pragma unroll
+      for (int rt = 0; rt < kRT; ++rt)
+        o.as[rt] = *reinterpret_cast<const vIf*>(as_base + (so + 64u * (uint32_t)rt));
+    }
   };
 
   float total[kRT][4][4];
@@ -789,17 +728,39 @@ __global__ __launch_bounds__(256) void lm_gemm_narrow_kernel(LmParams p) {
 
   // Block t sits in set t % kSets.  Loads are unconditional (clamped to the
   // last block).  Whole rounds of kSets blocks run in the loop; the last
-  // blocks (fewer than kSets, already loaded) run after it.
-  auto gemm = [&](auto odd_tag) {
-    Operands ops[kSets];
+  // blocks (fewer than kSets, already loaded) run after it.  The first
+  // kSets - 1 blocks are requested before anything else (and, with kFused,
+  // before the quantisation and its barrier, which every wave reaches on the
+  // same path).
+  Operands ops[kSets];
 #pragma unroll
-    for (int k = 0; k < kSets - 1; ++k) load(min((uint32_t)k, last), ops[k]);
+  for (int k = 0; k < kSets - 1; ++k) load_w(min((uint32_t)k, last), ops[k]);
+  if constexpr (kFused) {
+    // the rows' activations, quantised into LDS while those loads fly
+    for (uint32_t pair = threadIdx.x; pair < p.rows * blocks; pair += 256u) {
+      const uint32_t r = pair / blocks;
+      const uint32_t b = pair - r * blocks;
+      uint32_t x[32], packed[8];
+      float scale16;
+      load_block(p, r, b, x);
+      quantize_block(x, true, packed, scale16);
+      *reinterpret_cast<v4u*>(&aq_lds[b][r][0]) = v4u{packed[0], packed[1], packed[2], packed[3]};
+      *reinterpret_cast<v4u*>(&aq_lds[b][r][4]) = v4u{packed[4], packed[5], packed[6], packed[7]};
+      as_lds[b][r] = scale16;
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int k = 0; k < kSets - 1; ++k) load_a(min((uint32_t)k, last), ops[k]);
+  auto gemm = [&](auto odd_tag) {
     const uint32_t whole = blocks / kSets * kSets;
 #pragma unroll 1
     for (uint32_t b = 0; b < whole; b += kSets) {
 #pragma unroll
       for (int k = 0; k < kSets; ++k) {
-        load(min(b + (uint32_t)(k + kSets - 1), last), ops[(k + kSets - 1) % kSets]);
+        const uint32_t ahead = min(b + (uint32_t)(k + kSets - 1), last);
+        load_w(ahead, ops[(k + kSets - 1) % kSets]);
+        load_a(ahead, ops[(k + kSets - 1) % kSets]);
         __builtin_amdgcn_sched_barrier(0);
         run(ops[k], odd_tag);
         __builtin_amdgcn_sched_barrier(0);
@@ -820,123 +781,368 @@ __global__ __launch_bounds__(256) void lm_gemm_narrow_kernel(LmParams p) {
       gemm(std::false_type{});
     }
   }
-
-  uint32_t hb_all = 0;
-#pragma unroll
-  for (int s = 0; s < kSteps; ++s) hb_all |= ((hw[s] >> (4u * (n & 7u))) & 0xfu) << (4 * s);
-  write_tile<kRT>(p, total, hb_all, row0 + 4u * q, tile, n);
+  if (live_wave) write_tile<kRT, kI>(p, total, row0 + 4u * q, tile, n);
 }
 
-// Collects into `cand` every key of this lane (keys[0..N)) that reaches thr.
+// A value every lane holds alike, moved to a scalar register so that the
+// compiler branches and selects on it as a wave-uniform value.
+__device__ __forceinline__ uint32_t uniform(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_readfirstlane((int)v);
+}
+
+// Collects into `cand` every key of this lane (keys[0..N)) in [lo, hi);
+// `below` receives the lane's largest key under lo.
 template <int N>
-__device__ __forceinline__ uint32_t collect_at_least(uint64_t* cand, const uint64_t (&keys)[N],
-                                                     uint64_t thr, uint32_t count) {
+__device__ __forceinline__ uint32_t collect_range(uint64_t* cand, const uint64_t (&keys)[N],
+                                                  uint64_t lo, uint64_t hi, uint64_t& below) {
+  uint32_t count = 0;
+  below = 0;
 #pragma unroll
   for (int j = 0; j < N; ++j) {
-    const bool take = keys[j] != 0 && keys[j] >= thr;
+    const bool take = keys[j] != 0 && keys[j] >= lo && keys[j] < hi;
     const uint64_t mask = __ballot(take);
     if (take) cand[count + lanes_below(mask)] = keys[j];
     count += (uint32_t)__popcll((unsigned long long)mask);
+    below = (keys[j] < lo && keys[j] > below) ? keys[j] : below;
   }
-  return count;
+  return uniform(count);
 }
 
-// ---- selection: one wave per row ----
-// One row per workgroup: the 256 rows of a step then spread over 256 CUs
-// instead of 64 (measured 9.9 against 10.5 us per launch with four rows per
-// workgroup; two rows per workgroup gave 10.6).
-constexpr uint32_t kSelectWaves = 1;
-__global__ __launch_bounds__(64 * kSelectWaves) void lm_select_kernel(LmParams p, RowParams rp) {
-  __shared__ uint64_t cand[kSelectWaves][kCandCap];
-  __shared__ uint64_t top[kSelectWaves][kTopK];
-  const uint32_t lane = threadIdx.x & 63u;
-  const uint32_t wave = threadIdx.x >> 6;
-  const uint32_t row = blockIdx.x * kSelectWaves + wave;
-  if (row >= p.rows) return;
+// ---- selection: one workgroup per row ----
+// A tile's key is its order word with 0xffff - tile below it: tiles hold
+// consecutive ids, so among tiles with equal maxima the lower tile holds the
+// lower id, and the keys order the tiles as the keys of their best elements
+// would.  No element of a tile can reach a key above its word with the
+// lowest low bits any element can have (word_bound): the penalty never
+// raises a value, so the raw maximum bounds the penalised ones.
+constexpr uint32_t kSelectThreads = 256;
+constexpr int kTileKeys = (kTilesPerRow + 63) / 64;    // 38 tile words per lane
+constexpr uint32_t kTileCap = 20 * kTileKeys;          // tiles collected per round, at most
+constexpr int kChunkTiles = 32;                        // tiles read per pass
+constexpr uint32_t kElemCap = 20 * kChunkTiles;        // element keys collected per pass
+
+__device__ __forceinline__ uint64_t tile_key(uint32_t word, uint32_t tile) {
+  return ((uint64_t)word << 32) | (0xffffu - tile);
+}
+__device__ __forceinline__ uint64_t word_bound(uint32_t word) {
+  return ((uint64_t)word << 32) | (uint64_t)((0x3ffffu << 1) | 1u);
+}
+// The same bound knowing the tile: its lowest id is 64 tile.
+__device__ __forceinline__ uint64_t tile_bound(uint64_t key) {
+  const uint32_t tile = 0xffffu - (uint32_t)(key & 0xffffu);
+  return (key & 0xffffffff00000000ull) | (uint64_t)(((0x3ffffu - tile * kTileIds) << 1) | 1u);
+}
+
+// Waves 1-3 build the row's history bitmap in LDS (once per unique id, the
+// first bad position) while wave 0 reads the row's 2,374 tile words and
+// picks candidate tiles.  Then wave 0 alone selects the exact top-20 of the
+// penalised logits best-first: each round takes the tiles whose keys reach
+// the 20th best of the lanes' best remaining tile keys (at least 20 tiles),
+// reads their logits, penalises them through the bitmap and merges them into
+// the row's top-20; it stops once the 20th best key beats word_bound of the
+// best tile not read yet -- usually after one round.  The row is finished
+// with finalize_row.  Error rows: the lowest tile flagged kNonFiniteTile
+// holds the first non-finite logit (NONFINITE_OUTPUT, which takes precedence),
+// else the first history id >= vocab (TOKEN_ID).
+//
+// The first round works on the 32-bit words (the tile is implicit in the
+// lane and slot): its threshold is the 20th best of the lanes' best words,
+// and it takes every tile at or above it (a superset of the 64-bit rule's
+// tiles; when ties at that word overflow the list, the exact 64-bit rule
+// runs instead).  Its first pass needs one sort of elements: when at least 20
+// of its tiles hold no history id, their raw maxima are elements, all at or
+// above the threshold word, so every top-20 element reaches that word raw as
+// well as penalised; the elements whose raw value reaches it (usually a few
+// more than 20, at most 64 here) are keyed one per lane and sorted once.
+__global__ __launch_bounds__(kSelectThreads) void lm_select_kernel(LmParams p, RowParams rp) {
+  __shared__ __align__(16) uint32_t bm[kWordsPerRow];
+  __shared__ uint32_t tcand[kTileCap];
+  __shared__ uint64_t ecand[kElemCap];
+  __shared__ uint64_t top[kTopK];
+  __shared__ uint32_t bad_hist;
+  const uint32_t row = blockIdx.x;
+  const uint32_t tid = threadIdx.x;
+  const uint32_t lane = tid & 63u;
+  const uint32_t wave = tid >> 6;
   if (row_skipped(rp, row)) {  // decode loop: the row has ended or has no room
-    if (lane == 0) skip_row(rp, row);
+    if (tid == 0) skip_row(rp, row);
     return;
   }
-  const uint32_t bad_logit = p.meta[row * 2 + 0];
-  const uint32_t bad_hist = p.meta[row * 2 + 1];
-  const uint32_t r24 = rp.random_24[row];  // requested before the selection
-  if (bad_logit != kNone || bad_hist != kNone) {
-    // error row: the GEMM lowered meta[0] to the first non-finite logit
-    finalize_row(rp, row, 0, bad_logit, bad_hist, lane, r24);
-    return;
+  uint32_t len = 0;
+  if (rp.hist != nullptr && rp.hist_len != nullptr) {
+    len = row_word(rp.hist_len + row);
+    if ((size_t)len > rp.hist_ld) len = (uint32_t)rp.hist_ld;
   }
-  uint64_t* my_cand = cand[wave];
-  uint64_t* my_top = top[wave];
-
-  // 1. the 20 tiles with the largest maxima.  A tile's key is its order word
-  // with 0xffff - tile below it: tiles hold consecutive ids, so among tiles
-  // with equal maxima the lower tile holds the lower id, and these keys order
-  // the tiles exactly as the 64-bit keys of their best elements would.
-  constexpr int kPerLane = (kTilesPerRow + 63) / 64;  // 38
-  const uint32_t* tm = p.tilemax + (size_t)row * kTilesPerRow;
-  // The threshold is the 20th best lane maximum as a full key: keys are
-  // distinct, so exactly 20 lanes reach it and at most 20 x 38 keys are
-  // collected (kCandCap).  A threshold on the order word alone would let
-  // every lane through when values tie.
-  uint64_t keys[kPerLane];
-  uint64_t lane_best = 0;
-#pragma unroll
-  for (int j = 0; j < kPerLane; ++j) {
-    const uint32_t i = lane + 64u * j;
-    keys[j] = i < kTilesPerRow ? ((uint64_t)tm[i] << 32) | (0xffffu - i) : 0;
-    lane_best = keys[j] > lane_best ? keys[j] : lane_best;
-  }
-  uint64_t thr = shfl64(wave_sort_desc(lane_best, lane), kTopK - 1);
-  uint32_t count = collect_at_least(my_cand, keys, thr, 0);
-  if (lane < (uint32_t)kTopK) my_top[lane] = 0;
-  __builtin_amdgcn_wave_barrier();
-  merge_all(my_top, my_cand, count, lane);
-  const uint64_t tile_key = lane < (uint32_t)kTopK ? my_top[lane] : 0;
-
-  // 2. exact top-20 over those tiles' 1,280 logits
   const uint32_t* lrow = p.logits + (size_t)row * p.logits_ld;
-  const uint32_t* brow = p.bitmap + (size_t)row * kWordsPerRow;
-  // Every load is issued before the first is used: with the penalty's branch
-  // between them the compiler would otherwise wait for each tile in turn.
-  uint32_t xb[kTopK], hw[kTopK];
+
+  // wave 0: the uniform and the tile words (tile lane + 64 j in words[j],
+  // 0 past the last tile), requested first
+  uint32_t r24 = 0;
+  uint32_t words[kTileKeys];
+  if (wave == 0) {
+    r24 = rp.random_24[row];
+    const uint32_t* tm = p.tilemax + (size_t)row * kTilesPerRow;
 #pragma unroll
-  for (int i = 0; i < kTopK; ++i) {
-    const uint32_t v = (0xffffu - (uint32_t)shfl64(tile_key, (uint32_t)i)) * kTileIds + lane;
-    xb[i] = lrow[v];
-    hw[i] = brow[v >> 5];
+    for (int j = 0; j < kTileKeys; ++j) {
+      const uint32_t t = lane + 64u * (uint32_t)j;
+      words[j] = t < kTilesPerRow ? tm[t] : 0u;
+    }
   }
-  __builtin_amdgcn_sched_barrier(0);
-  uint64_t ek[kTopK];
-  lane_best = 0;
-  // The 20 tiles' maxima are 20 distinct elements whose penalised values
-  // reach the 20th best tile's order word, so the row's 20th best key is at
-  // least (that word << 32): usually only a few more than 20 elements do.
-  const uint64_t tile_floor = shfl64(tile_key, kTopK - 1) & 0xffffffff00000000ull;
-  uint32_t at_floor = 0;
+  static_assert(kWordsPerRow % 4 == 0, "the bitmap is cleared 16 bytes at a time");
+  for (uint32_t i = tid; i < kWordsPerRow / 4; i += kSelectThreads)
+    reinterpret_cast<v4u*>(bm)[i] = v4u{0u, 0u, 0u, 0u};
+  if (tid == 0) bad_hist = kNone;
+  if (tid < (uint32_t)kTopK) top[tid] = 0;
+  __syncthreads();
+
+  // Collects the tiles with keys in [lo, hi) into tcand, in lane order per
+  // slot; `below` receives the lane's best key under lo.
+  auto collect_tiles = [&](uint64_t lo, uint64_t hi, uint64_t& below) -> uint32_t {
+    uint32_t count = 0;
+    below = 0;
 #pragma unroll
-  for (int i = 0; i < kTopK; ++i) {
-    const uint32_t v = (0xffffu - (uint32_t)shfl64(tile_key, (uint32_t)i)) * kTileIds + lane;
-    const uint32_t yb = ((hw[i] >> (v & 31u)) & 1u) ? penalize_bits(xb[i]) : xb[i];
-    ek[i] = make_key(yb, v);
-    lane_best = ek[i] > lane_best ? ek[i] : lane_best;
-    at_floor += (uint32_t)__popcll((unsigned long long)__ballot(ek[i] >= tile_floor));
-  }
-  uint64_t key;
-  if (at_floor <= 64u) {
-    // one sort of the elements at or above the floor
-    count = collect_at_least(my_cand, ek, tile_floor, 0);
-    __builtin_amdgcn_wave_barrier();
-    key = wave_sort_desc(lane < count ? my_cand[lane] : 0, lane);
+    for (int j = 0; j < kTileKeys; ++j) {
+      const uint32_t t = lane + 64u * (uint32_t)j;
+      const uint64_t k = words[j] != 0u ? tile_key(words[j], t) : 0ull;
+      const bool take = k != 0 && k >= lo && k < hi;
+      const uint64_t mask = __ballot(take);
+      if (mask) {
+        if (take) tcand[count + lanes_below(mask)] = t;
+        count += (uint32_t)__popcll((unsigned long long)mask);
+      }
+      below = (k < lo && k > below) ? k : below;
+    }
+    return uniform(count);
+  };
+
+  uint32_t nf_tile = kNone;   // wave 0: lowest tile holding a non-finite logit
+  uint64_t thr = 0;           // wave 0: this round's lowest tile key
+  uint32_t ntiles = 0;        // wave 0: tiles collected this round
+  uint64_t rem = 0;           // wave 0: a bound of every element key of the lane's tiles not read yet
+  uint32_t tl = 0;            // wave 0: lane i < kChunkTiles holds the pass's tile i
+  uint32_t xb[kChunkTiles];   // wave 0: the first pass's logits, requested before the barrier
+  // The pass's tiles, one per lane (the first tile again past the end), and
+  // their logits: tile i is wave-uniform (readlane), so each load is a scalar
+  // base plus the lane's offset.
+  auto fetch_pass = [&](uint32_t base, uint32_t nt) {
+    tl = tcand[base + (lane < nt ? lane : 0u)];
+#pragma unroll
+    for (int i = 0; i < kChunkTiles; ++i) xb[i] = lrow[bcast32(tl, (uint32_t)i) * kTileIds + lane];
+  };
+  if (wave != 0) {
+    // ---- the history bitmap and the first bad position (waves 1-3) ----
+    const uint32_t t = tid - 64u;
+    constexpr uint32_t kHistThreads = kSelectThreads - 64u;
+    const uint32_t* hrow = len != 0 ? rp.hist + (size_t)row * rp.hist_ld : nullptr;
+    uint32_t my_bad = kNone;
+    auto add = [&](uint32_t pos, uint32_t id) {
+      if (pos >= len) return;
+      if (id >= kVocab) {
+        my_bad = pos < my_bad ? pos : my_bad;
+      } else {
+        uint32_t* word = &bm[id >> 5];
+        const uint32_t bit = 1u << (id & 31u);
+        if ((__hip_atomic_load(word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) & bit) == 0u)
+          atomicOr(word, bit);
+      }
+    };
+    if (rp.hist_vec4) {
+      // four uint4 (16 ids) per thread in flight; the last uint4 of a row
+      // stays inside it (hist_ld is a multiple of 4)
+      const v4u* h4 = reinterpret_cast<const v4u*>(hrow);
+      const uint32_t n4 = (len + 3u) / 4u;
+      for (uint32_t k0 = t; k0 < n4; k0 += 4u * kHistThreads) {
+        v4u v[4];
+#pragma unroll
+        for (uint32_t u = 0; u < 4; ++u) v[u] = h4[min(k0 + u * kHistThreads, n4 - 1u)];
+#pragma unroll
+        for (uint32_t u = 0; u < 4; ++u) {
+          const uint32_t k = k0 + u * kHistThreads;
+          if (k < n4) {
+            add(4u * k + 0u, v[u].x);
+            add(4u * k + 1u, v[u].y);
+            add(4u * k + 2u, v[u].z);
+            add(4u * k + 3u, v[u].w);
+          }
+        }
+      }
+    } else {
+      for (uint32_t q0 = t; q0 < len; q0 += 8u * kHistThreads) {
+        uint32_t v[8];
+#pragma unroll
+        for (uint32_t u = 0; u < 8; ++u) v[u] = hrow[min(q0 + u * kHistThreads, len - 1u)];
+#pragma unroll
+        for (uint32_t u = 0; u < 8; ++u) add(q0 + u * kHistThreads, v[u]);
+      }
+    }
+    my_bad = wave_min_u32(my_bad);
+    if (lane == 0 && my_bad != kNone) atomicMin(&bad_hist, my_bad);
   } else {
-    // many ties at the floor: threshold from the lanes' best keys, then merge
-    thr = shfl64(wave_sort_desc(lane_best, lane), kTopK - 1);
-    __builtin_amdgcn_wave_barrier();
-    count = collect_at_least(my_cand, ek, thr, 0);
-    if (lane < (uint32_t)kTopK) my_top[lane] = 0;
-    __builtin_amdgcn_wave_barrier();
-    merge_all(my_top, my_cand, count, lane);
-    key = my_top[lane < (uint32_t)kTopK ? lane : 0];
+    // ---- wave 0: non-finite tiles, then the first round's candidate tiles ----
+    uint32_t lbw = 0;
+#pragma unroll
+    for (int j = 0; j < kTileKeys; ++j) lbw = max(lbw, words[j]);
+    if (__ballot(lbw == kNonFiniteTile)) {
+#pragma unroll
+      for (int j = 0; j < kTileKeys; ++j) {
+        const uint32_t t = lane + 64u * (uint32_t)j;
+        if (words[j] == kNonFiniteTile && t < nf_tile) nf_tile = t;
+      }
+      nf_tile = uniform(wave_min_u32(nf_tile));
+    } else {
+      const uint32_t thr_word = bcast32(wave_sort_desc_u32(lbw, lane), kTopK - 1);
+      // tiles whose word reaches it, and the lane's best word below it
+      uint32_t count = 0, below = 0;
+#pragma unroll
+      for (int j = 0; j < kTileKeys; ++j) {
+        const bool take = words[j] >= thr_word;
+        const uint64_t mask = __ballot(take);
+        if (mask) {
+          // past the list's end nothing is stored; the count then exceeds it
+          const uint32_t slot = count + lanes_below(mask);
+          if (take && slot < kTileCap) tcand[slot] = lane + 64u * (uint32_t)j;
+          count += (uint32_t)__popcll((unsigned long long)mask);
+        }
+        below = max(below, take ? 0u : words[j]);
+      }
+      count = uniform(count);
+      if (count <= kTileCap) {
+        thr = (uint64_t)thr_word << 32;
+        ntiles = count;
+        rem = below != 0 ? word_bound(below) : 0ull;
+      } else {
+        // ties at the threshold word overflow the list: the exact 64-bit rule
+        uint64_t lb = 0;
+#pragma unroll
+        for (int j = 0; j < kTileKeys; ++j) {
+          const uint64_t k = words[j] != 0u ? tile_key(words[j], lane + 64u * (uint32_t)j) : 0ull;
+          lb = k > lb ? k : lb;
+        }
+        thr = shfl64(wave_sort_desc(lb, lane), kTopK - 1);
+        uint64_t below64;
+        ntiles = collect_tiles(thr, ~0ull, below64);
+        rem = below64 != 0 ? tile_bound(below64) : 0ull;
+      }
+      __builtin_amdgcn_wave_barrier();
+      // the first pass's logits are requested now and used after the barrier
+      fetch_pass(0, min(ntiles, (uint32_t)kChunkTiles));
+    }
   }
+  __syncthreads();
+  if (wave != 0) return;
+
+  // ---- wave 0: errors, then the best-first selection ----
+  const uint32_t first_bad_hist = bad_hist;
+  if (nf_tile != kNone) {
+    const uint32_t id = nf_tile * kTileIds + lane;
+    const uint32_t first = (lrow[id] & 0x7f800000u) == 0x7f800000u ? id : kNone;
+    finalize_row(rp, row, 0, wave_min_u32(first), first_bad_hist, lane, r24);
+    return;
+  }
+  if (first_bad_hist != kNone) {
+    finalize_row(rp, row, 0, kNone, first_bad_hist, lane, r24);
+    return;
+  }
+  uint64_t k20 = 0;  // the row's 20th best key so far
+  bool first_round = true;
+  for (;;) {
+    // every tile in tcand[0 .. ntiles) is read, kChunkTiles at a time; the
+    // first pass's logits are already in xb
+    for (uint32_t base = 0; base < ntiles; base += (uint32_t)kChunkTiles) {
+      const uint32_t nt = uniform(min(ntiles - base, (uint32_t)kChunkTiles));
+      if (base != 0) fetch_pass(base, nt);
+      if (first_round && ntiles <= (uint32_t)kChunkTiles) {
+        // a tile's 64 history bits are bitmap words 2t and 2t + 1: lane i < nt
+        // reads those of tile i
+        const uint64_t hbits =
+            *reinterpret_cast<const uint64_t*>(&bm[2u * (lane < nt ? tl : bcast32(tl, 0))]);
+        const uint32_t clean = uniform((uint32_t)__popcll((unsigned long long)(
+            __ballot(hbits == 0) & ((nt >= 64u ? 0ull : (1ull << nt)) - 1ull))));
+        if (clean >= (uint32_t)kTopK) {
+          // elements whose raw value reaches the threshold word move, one per
+          // lane, through LDS (id and raw bits)
+          const float floor_value = f_of(key_value_bits(thr));
+          uint32_t count = 0;
+#pragma unroll
+          for (int i = 0; i < kChunkTiles; ++i) {
+            const bool take = f_of(xb[i]) >= floor_value;
+            const uint64_t mask = (uint32_t)i < nt ? __ballot(take) : 0ull;
+            if (mask) {
+              const uint32_t id = bcast32(tl, (uint32_t)i) * kTileIds + lane;
+              const uint32_t slot = count + lanes_below(mask);
+              if (take && slot < kElemCap) ecand[slot] = ((uint64_t)id << 32) | xb[i];
+              count += (uint32_t)__popcll((unsigned long long)mask);
+            }
+          }
+          count = uniform(count);
+          if (count <= 64u) {
+            __builtin_amdgcn_wave_barrier();
+            uint64_t k = 0;
+            if (lane < count) {
+              const uint64_t e = ecand[lane];
+              const uint32_t id = (uint32_t)(e >> 32);
+              const uint32_t xbits = (uint32_t)e;
+              const bool hit = ((bm[id >> 5] >> (id & 31u)) & 1u) != 0u;
+              k = make_key(hit ? penalize_bits(xbits) : xbits, id);
+            }
+            __builtin_amdgcn_wave_barrier();
+            const uint64_t sorted = wave_sort_desc(k, lane);
+            if (lane < (uint32_t)kTopK) top[lane] = sorted;
+            __builtin_amdgcn_wave_barrier();
+            k20 = shfl64(sorted, kTopK - 1);
+            continue;
+          }
+        }
+      }
+      // history bits of the lane's element of each tile, all requested first
+      // (element 64 t + lane sits in bitmap word 2 t + lane / 32, bit lane % 32)
+      uint32_t hw[kChunkTiles];
+#pragma unroll
+      for (int i = 0; i < kChunkTiles; ++i) hw[i] = bm[2u * bcast32(tl, (uint32_t)i) + (lane >> 5)];
+      uint64_t ek[kChunkTiles];
+#pragma unroll
+      for (int i = 0; i < kChunkTiles; ++i) {
+        const uint32_t v = bcast32(tl, (uint32_t)i) * kTileIds + lane;
+        const bool hit = ((hw[i] >> (lane & 31u)) & 1u) != 0u;
+        uint32_t yb = xb[i];
+        // a tile rarely holds a history id: the penalty behind a wave-uniform branch
+        if (__ballot(hit)) yb = hit ? penalize_bits(yb) : yb;
+        ek[i] = (uint32_t)i < nt ? make_key(yb, v) : 0;
+      }
+      // Keys below the 20th best of the lanes' best (64 distinct elements)
+      // or below the row's 20th best so far cannot enter the top-20.
+      uint64_t lbe = 0;
+#pragma unroll
+      for (int i = 0; i < kChunkTiles; ++i) lbe = ek[i] > lbe ? ek[i] : lbe;
+      uint64_t floor = shfl64(wave_sort_desc(lbe, lane), kTopK - 1);
+      floor = floor > k20 ? floor : k20;
+      uint64_t unused;
+      const uint32_t ne = collect_range(ecand, ek, floor, ~0ull, unused);
+      __builtin_amdgcn_wave_barrier();
+      const uint64_t t20 = merge_all(top, ecand, ne, lane);
+      k20 = t20 > k20 ? t20 : k20;
+    }
+    // stop once no tile left can reach the top-20
+    const uint64_t best = wave_max64(rem);
+    if (best == 0 || k20 > best) break;
+    // another round, on the 64-bit keys: the next tiles best-first
+    const uint64_t hi = thr;
+    uint64_t lb = 0;
+#pragma unroll
+    for (int j = 0; j < kTileKeys; ++j) {
+      const uint64_t k = words[j] != 0u ? tile_key(words[j], lane + 64u * (uint32_t)j) : 0ull;
+      lb = (k < hi && k > lb) ? k : lb;
+    }
+    thr = shfl64(wave_sort_desc(lb, lane), kTopK - 1);
+    if (thr == 0) thr = 1;  // fewer than 20 lanes hold a tile: take them all
+    uint64_t below64;
+    ntiles = collect_tiles(thr, hi, below64);
+    rem = below64 != 0 ? tile_bound(below64) : 0ull;
+    __builtin_amdgcn_wave_barrier();
+    fetch_pass(0, min(ntiles, (uint32_t)kChunkTiles));
+    first_round = false;
+  }
+  const uint64_t key = top[lane < (uint32_t)kTopK ? lane : 0];
   finalize_row(rp, row, lane < (uint32_t)kTopK ? key : 0, kNone, kNone, lane, r24);
 }
 
@@ -1000,7 +1206,11 @@ size_t gemm_lds_bytes(uint32_t cols) {
 
 hipError_t launch_lm_sample(const LmParams& p, const RowParams& rp, hipStream_t stream) {
   (void)hipGetLastError();  // report only this call's launch errors
-  hipLaunchKernelGGL(lm_prep_kernel, dim3(p.rows_pad), dim3(kBlockThreads), 0, stream, p);
+  if (!p.fused_quant) {
+    const uint32_t pairs = p.rows_pad * (p.cols / 32u);
+    hipLaunchKernelGGL(lm_quant_kernel, dim3((pairs + kBlockThreads - 1) / kBlockThreads),
+                       dim3(kBlockThreads), 0, stream, p);
+  }
   if (p.rows <= kNarrowRows) {
     // Measured (Q4_0 step, us): one row tile with loads three blocks ahead
     // gives B = 1 37.0, B = 8 39.7, B = 32 51.2 (five ahead: 38.5, 41.0, 53.4;
@@ -1011,22 +1221,26 @@ hipError_t launch_lm_sample(const LmParams& p, const RowParams& rp, hipStream_t 
     const dim3 block(256);
     if (p.q8) {
       if (p.rows == 1)
-        hipLaunchKernelGGL((lm_gemm_narrow_kernel<true, 1, 4, 1>), grid, block, 0, stream, p);
+        hipLaunchKernelGGL((lm_gemm_narrow_kernel<true, 1, 4, 1, true>), grid, block, 0, stream, p);
       else if (p.rows == 2)
-        hipLaunchKernelGGL((lm_gemm_narrow_kernel<true, 1, 4, 2>), grid, block, 0, stream, p);
+        hipLaunchKernelGGL((lm_gemm_narrow_kernel<true, 1, 4, 2, true>), grid, block, 0, stream, p);
+      else if (p.fused_quant)
+        hipLaunchKernelGGL((lm_gemm_narrow_kernel<true, 1, 4, 4, true>), grid, block, 0, stream, p);
       else if (rt == 1)
-        hipLaunchKernelGGL((lm_gemm_narrow_kernel<true, 1, 4, 4>), grid, block, 0, stream, p);
+        hipLaunchKernelGGL((lm_gemm_narrow_kernel<true, 1, 4, 4, false>), grid, block, 0, stream, p);
       else
-        hipLaunchKernelGGL((lm_gemm_narrow_kernel<true, 2, 2, 4>), grid, block, 0, stream, p);
+        hipLaunchKernelGGL((lm_gemm_narrow_kernel<true, 2, 2, 4, false>), grid, block, 0, stream, p);
     } else {
       if (p.rows == 1)
-        hipLaunchKernelGGL((lm_gemm_narrow_kernel<false, 1, 4, 1>), grid, block, 0, stream, p);
+        hipLaunchKernelGGL((lm_gemm_narrow_kernel<false, 1, 4, 1, true>), grid, block, 0, stream, p);
       else if (p.rows == 2)
-        hipLaunchKernelGGL((lm_gemm_narrow_kernel<false, 1, 4, 2>), grid, block, 0, stream, p);
+        hipLaunchKernelGGL((lm_gemm_narrow_kernel<false, 1, 4, 2, true>), grid, block, 0, stream, p);
+      else if (p.fused_quant)
+        hipLaunchKernelGGL((lm_gemm_narrow_kernel<false, 1, 4, 4, true>), grid, block, 0, stream, p);
       else if (rt == 1)
-        hipLaunchKernelGGL((lm_gemm_narrow_kernel<false, 1, 4, 4>), grid, block, 0, stream, p);
+        hipLaunchKernelGGL((lm_gemm_narrow_kernel<false, 1, 4, 4, false>), grid, block, 0, stream, p);
       else
-        hipLaunchKernelGGL((lm_gemm_narrow_kernel<false, 2, 2, 4>), grid, block, 0, stream, p);
+        hipLaunchKernelGGL((lm_gemm_narrow_kernel<false, 2, 2, 4, false>), grid, block, 0, stream, p);
     }
   } else {
     const dim3 gemm_grid(kTilesPerRow, (p.rows_pad + kRowsPerGroup - 1) / kRowsPerGroup);
@@ -1037,9 +1251,7 @@ hipError_t launch_lm_sample(const LmParams& p, const RowParams& rp, hipStream_t 
       hipLaunchKernelGGL(lm_gemm_kernel<false>, gemm_grid, dim3(kGemmThreads),
                          gemm_lds_bytes(p.cols), stream, p);
   }
-  hipLaunchKernelGGL(lm_select_kernel, dim3((p.rows + kSelectWaves - 1) / kSelectWaves),
-                     dim3(64 * kSelectWaves), 0, stream,
-                     p, rp);
+  hipLaunchKernelGGL(lm_select_kernel, dim3(p.rows), dim3(kSelectThreads), 0, stream, p, rp);
   return hipGetLastError();
 }
 
