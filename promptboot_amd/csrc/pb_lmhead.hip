@@ -1212,33 +1212,35 @@ hipError_t launch_lm_sample(const LmParams& p, const RowParams& rp, hipStream_t 
                        dim3(kBlockThreads), 0, stream, p);
   }
   if (p.rows <= kNarrowRows) {
-    // Measured (Q4_0 step, us): one row tile with loads three blocks ahead
-    // gives B = 1 37.0, B = 8 39.7, B = 32 51.2 (five ahead: 38.5, 41.0, 53.4;
-    // seven: 42.5, 44.8); two row tiles with one block ahead give B = 64 70.8
-    // (two ahead: 73.8; one tile: 75.3).
+    // Measured (whole step, HIP events, us), loads one / two / three blocks
+    // ahead with one row tile: Q4_0 B = 1 23.3 / 24.0 / 24.7, B = 2 27.2 /
+    // 28.6 / 32.4, B = 4 29.8 / 30.8 / 33.9, B = 32 44.0 / 44.5 / 46.1; Q8_0
+    // B = 1 32.8 / 33.2 / 33.5, B = 4 36.1 / 37.5 / 41.2 (five, seven or ten
+    // ahead were slower still).  Two row tiles with one block ahead give
+    // B = 64 70.8 us (two ahead: 73.8; one tile: 75.3).
     const uint32_t rt = p.rows <= 32u ? 1u : 2u;
     const dim3 grid((kTilesPerRow + 3) / 4, (p.rows + 16u * rt - 1) / (16u * rt));
     const dim3 block(256);
     if (p.q8) {
       if (p.rows == 1)
-        hipLaunchKernelGGL((lm_gemm_narrow_kernel<true, 1, 4, 1, true>), grid, block, 0, stream, p);
+        hipLaunchKernelGGL((lm_gemm_narrow_kernel<true, 1, 2, 1, true>), grid, block, 0, stream, p);
       else if (p.rows == 2)
-        hipLaunchKernelGGL((lm_gemm_narrow_kernel<true, 1, 4, 2, true>), grid, block, 0, stream, p);
+        hipLaunchKernelGGL((lm_gemm_narrow_kernel<true, 1, 2, 2, true>), grid, block, 0, stream, p);
       else if (p.fused_quant)
-        hipLaunchKernelGGL((lm_gemm_narrow_kernel<true, 1, 4, 4, true>), grid, block, 0, stream, p);
+        hipLaunchKernelGGL((lm_gemm_narrow_kernel<true, 1, 2, 4, true>), grid, block, 0, stream, p);
       else if (rt == 1)
-        hipLaunchKernelGGL((lm_gemm_narrow_kernel<true, 1, 4, 4, false>), grid, block, 0, stream, p);
+        hipLaunchKernelGGL((lm_gemm_narrow_kernel<true, 1, 2, 4, false>), grid, block, 0, stream, p);
       else
         hipLaunchKernelGGL((lm_gemm_narrow_kernel<true, 2, 2, 4, false>), grid, block, 0, stream, p);
     } else {
       if (p.rows == 1)
-        hipLaunchKernelGGL((lm_gemm_narrow_kernel<false, 1, 4, 1, true>), grid, block, 0, stream, p);
+        hipLaunchKernelGGL((lm_gemm_narrow_kernel<false, 1, 2, 1, true>), grid, block, 0, stream, p);
       else if (p.rows == 2)
-        hipLaunchKernelGGL((lm_gemm_narrow_kernel<false, 1, 4, 2, true>), grid, block, 0, stream, p);
+        hipLaunchKernelGGL((lm_gemm_narrow_kernel<false, 1, 2, 2, true>), grid, block, 0, stream, p);
       else if (p.fused_quant)
-        hipLaunchKernelGGL((lm_gemm_narrow_kernel<false, 1, 4, 4, true>), grid, block, 0, stream, p);
+        hipLaunchKernelGGL((lm_gemm_narrow_kernel<false, 1, 2, 4, true>), grid, block, 0, stream, p);
       else if (rt == 1)
-        hipLaunchKernelGGL((lm_gemm_narrow_kernel<false, 1, 4, 4, false>), grid, block, 0, stream, p);
+        hipLaunchKernelGGL((lm_gemm_narrow_kernel<false, 1, 2, 4, false>), grid, block, 0, stream, p);
       else
         hipLaunchKernelGGL((lm_gemm_narrow_kernel<false, 2, 2, 4, false>), grid, block, 0, stream, p);
     }
