@@ -32,6 +32,9 @@ The printed JSON line also carries:
   lmhead_fused        the fused Q4_0 LM head + sampler step (B=256);
   lmhead_q8_fused     the same with the Q8_0 head (the model's output head);
   lmhead_B1           one conversation's step (B=1) through each head;
+                      each LM-head leg also gives its step's HBM traffic
+                      (the per-kernel counter figures of the committed
+                      summary, same-build only) over its algorithmic bytes;
   host_buffers        PCIe-inclusive rates: the single-row drop-in on host
                       buffers, and the B=4096 batch copied from pinned host
                       memory every step (not the headline value).
@@ -507,7 +510,41 @@ def measured_traffic(version: str) -> dict:
                 "traffic_source": f"stale: the summary was measured on {d.get('library')!r}, "
                                   f"this run uses {version!r}"}
     return {"traffic": d.get("hbm_bytes_per_launch"),
-            "traffic_source": f"{PMC_SUMMARY.relative_to(ROOT)} (same build)"}
+            "traffic_source": f"{_shown(PMC_SUMMARY)} (same build)"}
+
+
+# The kernels of one LM-head step, as (name prefix, grid threads), by leg.
+LM_STEP_KERNELS = {
+    ("q4_0", 256): [("pb::lm_quant_kernel", 7168), ("pb::lm_gemm_kernel<false>", 1215488),
+                    ("pb::lm_select_kernel", 65536)],
+    ("q8_0", 256): [("pb::lm_quant_kernel", 7168), ("pb::lm_gemm_kernel<true>", 1215488),
+                    ("pb::lm_select_kernel", 65536)],
+    ("q4_0", 1): [("pb::lm_gemm_narrow_kernel<false", 152064), ("pb::lm_select_kernel", 256)],
+    ("q8_0", 1): [("pb::lm_gemm_narrow_kernel<true", 152064), ("pb::lm_select_kernel", 256)],
+}
+
+
+def lm_step_traffic(version: str, head: str, rows: int, alg: int) -> dict:
+    """HBM bytes of one LM-head step from the committed counter summary (its
+    per-kernel figures), only if it was measured on this very build."""
+    if not PMC_SUMMARY.exists():
+        return {"traffic": None, "traffic_source": "no counter summary"}
+    d = json.loads(PMC_SUMMARY.read_text())
+    if d.get("library") != version:
+        return {"traffic": None, "traffic_source": "stale counter summary"}
+    total = 0
+    for prefix, grid in LM_STEP_KERNELS[(head, rows)]:
+        hits = [k for k in d.get("lm_head_kernels_per_dispatch", [])
+                if k["kernel"].startswith(prefix) and k["grid_threads"] == grid]
+        if len(hits) != 1:
+            return {"traffic": None, "traffic_source": f"no counter figure for {prefix}"}
+        total += hits[0]["fetch_bytes"] + hits[0]["write_bytes"]
+    return {"traffic": total, "traffic_over_alg": round(total / alg, 3),
+            "traffic_source": f"{_shown(PMC_SUMMARY)} (same build)"}
+
+
+def _shown(path: pathlib.Path) -> str:
+    return str(path.relative_to(ROOT) if path.is_relative_to(ROOT) else path)
 
 
 # ---- rocprofv3 counter summary ----
@@ -526,24 +563,32 @@ def traffic_summary(fetch_dir: str, write_dir: str) -> None:
     """Writes profiles/segment_kernel_B4096_traffic.json from a FETCH_SIZE and
     a WRITE_SIZE rocprofv3 run of this bench (see the commands it records):
     the per-dispatch KiB of the B=4096 segment kernel, each scaled by what the
-    same counter reads for the calibration copy of known size."""
+    same counter reads for the calibration copy of known size, and the same
+    scaled bytes per dispatch of each LM-head kernel (by grid) of the run."""
     from promptboot_amd import sampler as s
     from promptboot_amd import workloads
 
-    def per_kernel(folder, counter, name_prefix):
-        vals = [float(r["Counter_Value"]) for r in _pmc_rows(folder, counter)
-                if r["Kernel_Name"].startswith(name_prefix)]
-        return (float(np.mean(vals)) if vals else None), len(vals)
+    def name(r):  # rocprofv3 may list a kernel with its return type
+        return r["Kernel_Name"].removeprefix("void ")
+
+    def grid(r):
+        return int(r.get("Grid_Size", r.get("Grid_Size_X", 0)) or 0)
+
+    # the calibration copy is the copy kernel's largest dispatch (the bench's
+    # own small copies use the same kernel)
+    def calibration(folder, counter):
+        rows = [r for r in _pmc_rows(folder, counter) if name(r).startswith(CALIBRATION_KERNEL)]
+        top = max(grid(r) for r in rows)
+        return float(np.mean([float(r["Counter_Value"]) for r in rows if grid(r) == top]))
 
     cal_bytes = 1024 << 20
-    f_cal, _ = per_kernel(fetch_dir, "FETCH_SIZE", CALIBRATION_KERNEL)
-    w_cal, _ = per_kernel(write_dir, "WRITE_SIZE", CALIBRATION_KERNEL)
+    f_cal = calibration(fetch_dir, "FETCH_SIZE")
+    w_cal = calibration(write_dir, "WRITE_SIZE")
     # the B=4096 launch is the one with 4096 workgroups; B=1 and B=64 use the
     # same kernel name only with one slice per row from 256 rows on
     def big(folder, counter):
         vals = [float(r["Counter_Value"]) for r in _pmc_rows(folder, counter)
-                if r["Kernel_Name"].startswith(SEGMENT_KERNEL.split("(")[0])
-                and int(r.get("Grid_Size", r.get("Grid_Size_X", 0)) or 0) == 4096 * 256]
+                if name(r).startswith(SEGMENT_KERNEL.split("(")[0]) and grid(r) == 4096 * 256]
         return float(np.mean(vals)), len(vals)
 
     f_k, nf = big(fetch_dir, "FETCH_SIZE")
@@ -551,12 +596,34 @@ def traffic_summary(fetch_dir: str, write_dir: str) -> None:
     f_scale = cal_bytes / 1024 / f_cal
     w_scale = cal_bytes / 1024 / w_cal
     hbm = (f_k * f_scale + w_k * w_scale) * 1024
+
+    # the LM head legs' kernels, per (kernel, grid): the B=256 steps use the
+    # wide GEMM, the B=1 steps the narrow one; lm_select_kernel's grid is
+    # 256 threads per row
+    def lm_kernels(folder, counter):
+        g = {}
+        for r in _pmc_rows(folder, counter):
+            k = name(r)
+            if not k.startswith("pb::lm_") or "pack" in k:
+                continue
+            key = (k.split("(")[0], grid(r))
+            g.setdefault(key, []).append(float(r["Counter_Value"]))
+        return g
+
+    lf, lw = lm_kernels(fetch_dir, "FETCH_SIZE"), lm_kernels(write_dir, "WRITE_SIZE")
+    lm = []
+    for key in sorted(set(lf) & set(lw)):
+        fb = float(np.mean(lf[key])) * f_scale * 1024
+        wb = float(np.mean(lw[key])) * w_scale * 1024
+        lm.append({"kernel": key[0], "grid_threads": key[1],
+                   "dispatches": [len(lf[key]), len(lw[key])],
+                   "fetch_bytes": int(round(fb)), "write_bytes": int(round(wb))})
     w = workloads.make("large")
     alg = workloads.algorithmic_bytes(w["hist_len"])
     repo = "$REPO"
     cmd = ("cd /tmp && export TMPDIR=/tmp && timeout -s KILL 300 rocprofv3 --pmc {c} -f csv -d "
            f"{repo}/gpurun_out/pmc_{{c}} -o run -- python3 {repo}/bench.py --no-cpu-baseline "
-           "--no-adversarial --no-lmhead --no-host-buffers --no-production --batches 4096 "
+           "--no-adversarial --no-host-buffers --no-production --batches 4096 "
            "--steps 2 --warmup 0 --calibration-copy-mib 1024")
     out = {"kernel": SEGMENT_KERNEL,
            "library": s.lib().pb_version().decode(),
@@ -574,7 +641,8 @@ def traffic_summary(fetch_dir: str, write_dir: str) -> None:
                                            "write_size_kib": round(w_k, 2)},
            "hbm_bytes_per_launch": int(round(hbm)),
            "algorithmic_bytes_per_launch": alg,
-           "traffic_over_algorithmic": round(hbm / alg, 4)}
+           "traffic_over_algorithmic": round(hbm / alg, 4),
+           "lm_head_kernels_per_dispatch": lm}
     PMC_SUMMARY.write_text(json.dumps(out, indent=1) + "\n")
     print(json.dumps(out, indent=1))
 
@@ -699,6 +767,11 @@ def main() -> int:
         cpu.pop("_tokens")
 
     traffic = measured_traffic(version)
+    for res, head_fmt in ((lmhead, "q4_0"), (lmhead_q8, "q8_0")):
+        if res is not None:
+            res.update(lm_step_traffic(version, head_fmt, 256, res["alg_bytes"]))
+    for head_fmt, res in (lmhead_b1 or {}).items():
+        res.update(lm_step_traffic(version, head_fmt, 1, res["alg_bytes"]))
     roof = {"bound": "hbm", "achieved": round(main_res["achieved_gbs"], 1), "peak": PEAK_HBM_GBS,
             "unit": "GB/s", "frac": round(main_res["achieved_gbs"] / PEAK_HBM_GBS, 4),
             "traffic": traffic["traffic"], "traffic_source": traffic["traffic_source"],
