@@ -212,10 +212,13 @@ __device__ __forceinline__ double bcast_f64(double v, uint32_t src) {
   return __builtin_bit_cast(double, shfl64(__builtin_bit_cast(uint64_t, v), src));
 }
 
-// Bitonic sort of one key per lane, descending (lane 0 holds the maximum).
+// Bitonic sort of one key per lane, descending (lane 0 holds the maximum),
+// over groups of kLanes lanes (32 or 64; with 32 each half of the wave is
+// sorted on its own).
+template <uint32_t kLanes = 64>
 __device__ __forceinline__ uint64_t wave_sort_desc(uint64_t key, uint32_t lane) {
 #pragma unroll
-  for (uint32_t k = 2; k <= 64; k <<= 1) {
+  for (uint32_t k = 2; k <= kLanes; k <<= 1) {
 #pragma unroll
     for (uint32_t j = k >> 1; j > 0; j >>= 1) {
       const uint64_t other = shfl_xor64(key, (int)j);

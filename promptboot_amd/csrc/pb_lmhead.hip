@@ -813,19 +813,24 @@ __device__ __forceinline__ uint32_t collect_range(uint64_t* cand, const uint64_t
 // consecutive ids, so among tiles with equal maxima the lower tile holds the
 // lower id, and the keys order the tiles as the keys of their best elements
 // would.  No element of a tile can reach a key above its word with the
-// lowest low bits any element can have (word_bound): the penalty never
-// raises a value, so the raw maximum bounds the penalised ones.
-constexpr uint32_t kSelectThreads = 256;
+// lowest low bits any element can have with the tile's lowest id
+// (tile_bound): the penalty never raises a value, so the raw maximum bounds
+// the penalised ones.
+constexpr uint32_t kTileWaves = 4;                      // waves that read the tile words
+constexpr uint32_t kHistWaves = 4;                      // waves that build the history bitmap
+constexpr uint32_t kSelectThreads = 64u * (kTileWaves + kHistWaves);
 constexpr int kTileKeys = (kTilesPerRow + 63) / 64;    // 38 tile words per lane
+constexpr int kWaveKeys = (kTileKeys + (int)kTileWaves - 1) / (int)kTileWaves;  // 10 per tile wave
+constexpr uint32_t kWaveTiles = 16;                     // tiles a tile wave reads in the first round
+constexpr uint32_t kWaveElems = 64;                     // element slots of a tile wave
 constexpr uint32_t kTileCap = 20 * kTileKeys;          // tiles collected per round, at most
 constexpr int kChunkTiles = 32;                        // tiles read per pass
 constexpr uint32_t kElemCap = 20 * kChunkTiles;        // element keys collected per pass
+static_assert(kTileWaves * kWaveElems <= kElemCap, "the first round's elements fit the list");
+static_assert(kTileWaves * kWaveTiles <= 64, "wave 0 checks the first round's tiles one per lane");
 
 __device__ __forceinline__ uint64_t tile_key(uint32_t word, uint32_t tile) {
   return ((uint64_t)word << 32) | (0xffffu - tile);
-}
-__device__ __forceinline__ uint64_t word_bound(uint32_t word) {
-  return ((uint64_t)word << 32) | (uint64_t)((0x3ffffu << 1) | 1u);
 }
 // The same bound knowing the tile: its lowest id is 64 tile.
 __device__ __forceinline__ uint64_t tile_bound(uint64_t key) {
@@ -833,33 +838,41 @@ __device__ __forceinline__ uint64_t tile_bound(uint64_t key) {
   return (key & 0xffffffff00000000ull) | (uint64_t)(((0x3ffffu - tile * kTileIds) << 1) | 1u);
 }
 
-// Waves 1-3 build the row's history bitmap in LDS (once per unique id, the
-// first bad position) while wave 0 reads the row's 2,374 tile words and
-// picks candidate tiles.  Then wave 0 alone selects the exact top-20 of the
-// penalised logits best-first: each round takes the tiles whose keys reach
-// the 20th best of the lanes' best remaining tile keys (at least 20 tiles),
-// reads their logits, penalises them through the bitmap and merges them into
-// the row's top-20; it stops once the 20th best key beats word_bound of the
-// best tile not read yet -- usually after one round.  The row is finished
-// with finalize_row.  Error rows: the lowest tile flagged kNonFiniteTile
-// holds the first non-finite logit (NONFINITE_OUTPUT, which takes precedence),
-// else the first history id >= vocab (TOKEN_ID).
+// The first round, in the tile waves: thr_word is the 20th best of the 64
+// lanes' best tile words (lane l's best over tiles l + 64 j); every tile whose
+// word reaches it is read, and every element of those tiles whose raw value
+// reaches thr_word (usually a few more than 20) is keyed, penalised through
+// the bitmap, and sorted once.  Every element outside that set has a raw
+// word, and so a penalised word (the penalty never raises a value), below
+// thr_word: when the 20th best key of the set still reaches thr_word, the
+// set's top-20 is the row's.
 //
-// The first round works on the 32-bit words (the tile is implicit in the
-// lane and slot): its threshold is the 20th best of the lanes' best words,
-// and it takes every tile at or above it (a superset of the 64-bit rule's
-// tiles; when ties at that word overflow the list, the exact 64-bit rule
-// runs instead).  Its first pass needs one sort of elements: when at least 20
-// of its tiles hold no history id, their raw maxima are elements, all at or
-// above the threshold word, so every top-20 element reaches that word raw as
-// well as penalised; the elements whose raw value reaches it (usually a few
-// more than 20, at most 64 here) are keyed one per lane and sorted once.
+// Waves 0-3 split the tile words (wave w holds words j in [10 w, 10 w + 10)),
+// exchange their lanes' best words through LDS, and each reads and filters
+// its own tiles that reach thr_word; waves 4-7 build the row's history bitmap
+// in LDS (once per unique id) and find the first bad position.  After the
+// third barrier wave 0 keys and sorts the candidates.
+//
+// Any other case -- more than 16 tiles of one wave or more than 64 candidate
+// elements, a 20th best key below thr_word -- takes the general selection on
+// wave 0: rounds best-first over the 64-bit tile keys, each taking the tiles
+// whose keys reach the 20th best of the lanes' best remaining keys, reading
+// their logits, penalising them through the bitmap and merging them into the
+// row's top-20, until the 20th best key beats tile_bound of the best tile not
+// read.  Error rows: the lowest tile flagged kNonFiniteTile holds the first
+// non-finite logit (NONFINITE_OUTPUT, which takes precedence), else the first
+// history id >= vocab (TOKEN_ID).  The row is finished with finalize_row.
 __global__ __launch_bounds__(kSelectThreads) void lm_select_kernel(LmParams p, RowParams rp) {
   __shared__ __align__(16) uint32_t bm[kWordsPerRow];
   __shared__ uint32_t tcand[kTileCap];
   __shared__ uint64_t ecand[kElemCap];
   __shared__ uint64_t top[kTopK];
+  __shared__ uint32_t lane_best[kTileWaves][64];
+  __shared__ uint32_t wave_tiles[kTileWaves][kWaveTiles];
+  __shared__ uint32_t wave_ntiles[kTileWaves];
+  __shared__ uint32_t wave_nelems[kTileWaves];
   __shared__ uint32_t bad_hist;
+  __shared__ uint32_t nf_tile;
   const uint32_t row = blockIdx.x;
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = tid & 63u;
@@ -874,66 +887,142 @@ __global__ __launch_bounds__(kSelectThreads) void lm_select_kernel(LmParams p, R
     if ((size_t)len > rp.hist_ld) len = (uint32_t)rp.hist_ld;
   }
   const uint32_t* lrow = p.logits + (size_t)row * p.logits_ld;
+  const uint32_t* tm = p.tilemax + (size_t)row * kTilesPerRow;
+  const bool tile_wave = wave < kTileWaves;
 
-  // wave 0: the uniform and the tile words (tile lane + 64 j in words[j],
-  // 0 past the last tile), requested first
+  // tile waves: their tile words (tile lane + 64 (10 w + j) in words[j], 0
+  // past the last tile), requested first; wave 0 also the uniform
   uint32_t r24 = 0;
-  uint32_t words[kTileKeys];
-  if (wave == 0) {
-    r24 = rp.random_24[row];
-    const uint32_t* tm = p.tilemax + (size_t)row * kTilesPerRow;
+  uint32_t thr_first = 0;  // the first round's threshold word (tile waves)
+  uint32_t words[kWaveKeys];
+  if (tile_wave) {
+    if (wave == 0) r24 = rp.random_24[row];
 #pragma unroll
-    for (int j = 0; j < kTileKeys; ++j) {
-      const uint32_t t = lane + 64u * (uint32_t)j;
+    for (int j = 0; j < kWaveKeys; ++j) {
+      const uint32_t t = lane + 64u * (wave * (uint32_t)kWaveKeys + (uint32_t)j);
       words[j] = t < kTilesPerRow ? tm[t] : 0u;
     }
   }
+  // history waves: the first four uint4 (or eight words) of each thread
+  const uint32_t ht = tid - 64u * kTileWaves;
+  constexpr uint32_t kHistThreads = 64u * kHistWaves;
+  const uint32_t* hrow = len != 0 ? rp.hist + (size_t)row * rp.hist_ld : nullptr;
+  const v4u* h4 = reinterpret_cast<const v4u*>(hrow);
+  const uint32_t n4 = (len + 3u) / 4u;
+  v4u hv[4];
+  uint32_t hs[8];
+  auto load_hist = [&](uint32_t k0) {
+    if (rp.hist_vec4) {
+#pragma unroll
+      for (uint32_t u = 0; u < 4; ++u) hv[u] = h4[min(k0 + u * kHistThreads, n4 - 1u)];
+    } else {
+#pragma unroll
+      for (uint32_t u = 0; u < 8; ++u) hs[u] = hrow[min(k0 + u * kHistThreads, len - 1u)];
+    }
+  };
+  if (!tile_wave && ht < (rp.hist_vec4 ? n4 : len)) load_hist(ht);
+
   static_assert(kWordsPerRow % 4 == 0, "the bitmap is cleared 16 bytes at a time");
   for (uint32_t i = tid; i < kWordsPerRow / 4; i += kSelectThreads)
     reinterpret_cast<v4u*>(bm)[i] = v4u{0u, 0u, 0u, 0u};
-  if (tid == 0) bad_hist = kNone;
+  if (tid == 0) {
+    bad_hist = kNone;
+    nf_tile = kNone;
+  }
   if (tid < (uint32_t)kTopK) top[tid] = 0;
-  __syncthreads();
+  __syncthreads();  // (1) the bitmap is clear
 
-  // Collects the tiles with keys in [lo, hi) into tcand, in lane order per
-  // slot; `below` receives the lane's best key under lo.
-  auto collect_tiles = [&](uint64_t lo, uint64_t hi, uint64_t& below) -> uint32_t {
-    uint32_t count = 0;
-    below = 0;
+  if (tile_wave) {
+    // the lane's best word, and the wave's lowest tile flagged non-finite
+    uint32_t lbw = 0;
 #pragma unroll
-    for (int j = 0; j < kTileKeys; ++j) {
-      const uint32_t t = lane + 64u * (uint32_t)j;
-      const uint64_t k = words[j] != 0u ? tile_key(words[j], t) : 0ull;
-      const bool take = k != 0 && k >= lo && k < hi;
-      const uint64_t mask = __ballot(take);
-      if (mask) {
-        if (take) tcand[count + lanes_below(mask)] = t;
+    for (int j = 0; j < kWaveKeys; ++j) lbw = max(lbw, words[j]);
+    if (__ballot(lbw == kNonFiniteTile)) {
+      uint32_t nf = kNone;
+#pragma unroll
+      for (int j = 0; j < kWaveKeys; ++j) {
+        const uint32_t t = lane + 64u * (wave * (uint32_t)kWaveKeys + (uint32_t)j);
+        if (words[j] == kNonFiniteTile && t < nf) nf = t;
+      }
+      nf = wave_min_u32(nf);
+      if (lane == 0) atomicMin(&nf_tile, nf);
+    }
+    lane_best[wave][lane] = lbw;
+  }
+  __syncthreads();  // (2) the lanes' best words are published
+
+  if (tile_wave) {
+    uint32_t ntiles = kWaveTiles + 1u;  // past the cap: no first-round result
+    uint32_t nelems = 0;
+    if (nf_tile == kNone) {
+      uint32_t best = 0;
+#pragma unroll
+      for (uint32_t w = 0; w < kTileWaves; ++w) best = max(best, lane_best[w][lane]);
+      const uint32_t thr_word = uniform(bcast32(wave_sort_desc_u32(best, lane), kTopK - 1));
+      thr_first = thr_word;
+      // the wave's tiles whose word reaches it: a mask of the lane's words,
+      // then one round per word taken (the lanes' lowest remaining bits)
+      uint32_t m = 0;
+#pragma unroll
+      for (int j = 0; j < kWaveKeys; ++j) m |= (words[j] >= thr_word ? 1u : 0u) << j;
+      uint32_t count = 0;
+      for (uint64_t mask = __ballot(m != 0); mask != 0; mask = __ballot(m != 0)) {
+        if (m != 0) {
+          const uint32_t slot = count + lanes_below(mask);
+          const uint32_t j = (uint32_t)__builtin_ctz(m);
+          if (slot < kWaveTiles) wave_tiles[wave][slot] = lane + 64u * (wave * (uint32_t)kWaveKeys + j);
+          m &= m - 1u;
+        }
         count += (uint32_t)__popcll((unsigned long long)mask);
       }
-      below = (k < lo && k > below) ? k : below;
-    }
-    return uniform(count);
-  };
-
-  uint32_t nf_tile = kNone;   // wave 0: lowest tile holding a non-finite logit
-  uint64_t thr = 0;           // wave 0: this round's lowest tile key
-  uint32_t ntiles = 0;        // wave 0: tiles collected this round
-  uint64_t rem = 0;           // wave 0: a bound of every element key of the lane's tiles not read yet
-  uint32_t tl = 0;            // wave 0: lane i < kChunkTiles holds the pass's tile i
-  uint32_t xb[kChunkTiles];   // wave 0: the first pass's logits, requested before the barrier
-  // The pass's tiles, one per lane (the first tile again past the end), and
-  // their logits: tile i is wave-uniform (readlane), so each load is a scalar
-  // base plus the lane's offset.
-  auto fetch_pass = [&](uint32_t base, uint32_t nt) {
-    tl = tcand[base + (lane < nt ? lane : 0u)];
+      ntiles = uniform(count);
+      if (ntiles <= kWaveTiles) {
+        __builtin_amdgcn_wave_barrier();
+        // their logits (tile i of the wave is wave-uniform: readlane; past the
+        // list the row's tile 0 is read again), then the elements whose raw
+        // value reaches thr_word, as (id, raw bits), one round per element
+        const uint32_t tl = lane < ntiles ? wave_tiles[wave][lane] : 0u;
+        uint32_t xb[kWaveTiles];
 #pragma unroll
-    for (int i = 0; i < kChunkTiles; ++i) xb[i] = lrow[bcast32(tl, (uint32_t)i) * kTileIds + lane];
-  };
-  if (wave != 0) {
-    // ---- the history bitmap and the first bad position (waves 1-3) ----
-    const uint32_t t = tid - 64u;
-    constexpr uint32_t kHistThreads = kSelectThreads - 64u;
-    const uint32_t* hrow = len != 0 ? rp.hist + (size_t)row * rp.hist_ld : nullptr;
+        for (int i = 0; i < (int)kWaveTiles; ++i) xb[i] = lrow[bcast32(tl, (uint32_t)i) * kTileIds + lane];
+        const float floor_value = f_of(key_value_bits((uint64_t)thr_word << 32));
+        uint32_t e = 0;
+#pragma unroll
+        for (int i = 0; i < (int)kWaveTiles; ++i)
+          e |= ((uint32_t)i < ntiles && f_of(xb[i]) >= floor_value ? 1u : 0u) << i;
+        uint64_t* out = ecand + wave * kWaveElems;
+        for (uint64_t mask = __ballot(e != 0); mask != 0; mask = __ballot(e != 0)) {
+          if (e != 0) {
+            const uint32_t i = (uint32_t)__builtin_ctz(e);
+            // xb[i] for the lane's own i: a select tree on the bits of i (the
+            // bits pass through an empty asm, or the compiler turns the tree
+            // back into an indexed access through scratch memory)
+            uint32_t b0 = i & 1u, b1 = i & 2u, b2 = i & 4u, b3 = i & 8u;
+            __asm__ volatile("" : "+v"(b0), "+v"(b1), "+v"(b2), "+v"(b3));
+            uint32_t v8[8], v4[4], v2[2];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) v8[k] = b0 ? xb[2 * k + 1] : xb[2 * k];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) v4[k] = b1 ? v8[2 * k + 1] : v8[2 * k];
+#pragma unroll
+            for (int k = 0; k < 2; ++k) v2[k] = b2 ? v4[2 * k + 1] : v4[2 * k];
+            const uint32_t x = b3 ? v2[1] : v2[0];
+            const uint32_t slot = nelems + lanes_below(mask);
+            if (slot < kWaveElems)
+              out[slot] = ((uint64_t)(wave_tiles[wave][i] * kTileIds + lane) << 32) | x;
+            e &= e - 1u;
+          }
+          nelems += (uint32_t)__popcll((unsigned long long)mask);
+        }
+        nelems = uniform(nelems);
+      }
+    }
+    if (lane == 0) {
+      wave_ntiles[wave] = ntiles;
+      wave_nelems[wave] = nelems;
+    }
+  } else {
+    // ---- the history bitmap and the first bad position ----
     uint32_t my_bad = kNone;
     auto add = [&](uint32_t pos, uint32_t id) {
       if (pos >= len) return;
@@ -947,14 +1036,14 @@ __global__ __launch_bounds__(kSelectThreads) void lm_select_kernel(LmParams p, R
       }
     };
     if (rp.hist_vec4) {
-      // four uint4 (16 ids) per thread in flight; the last uint4 of a row
-      // stays inside it (hist_ld is a multiple of 4)
-      const v4u* h4 = reinterpret_cast<const v4u*>(hrow);
-      const uint32_t n4 = (len + 3u) / 4u;
-      for (uint32_t k0 = t; k0 < n4; k0 += 4u * kHistThreads) {
+      // four uint4 (16 ids) per thread per batch, the next batch requested
+      // before this one is used; the last uint4 of a row stays inside it
+      // (hist_ld is a multiple of 4)
+      for (uint32_t k0 = ht; k0 < n4; k0 += 4u * kHistThreads) {
         v4u v[4];
 #pragma unroll
-        for (uint32_t u = 0; u < 4; ++u) v[u] = h4[min(k0 + u * kHistThreads, n4 - 1u)];
+        for (uint32_t u = 0; u < 4; ++u) v[u] = hv[u];
+        if (k0 + 4u * kHistThreads < n4) load_hist(k0 + 4u * kHistThreads);
 #pragma unroll
         for (uint32_t u = 0; u < 4; ++u) {
           const uint32_t k = k0 + u * kHistThreads;
@@ -967,74 +1056,26 @@ __global__ __launch_bounds__(kSelectThreads) void lm_select_kernel(LmParams p, R
         }
       }
     } else {
-      for (uint32_t q0 = t; q0 < len; q0 += 8u * kHistThreads) {
+      for (uint32_t q0 = ht; q0 < len; q0 += 8u * kHistThreads) {
         uint32_t v[8];
 #pragma unroll
-        for (uint32_t u = 0; u < 8; ++u) v[u] = hrow[min(q0 + u * kHistThreads, len - 1u)];
+        for (uint32_t u = 0; u < 8; ++u) v[u] = hs[u];
+        if (q0 + 8u * kHistThreads < len) load_hist(q0 + 8u * kHistThreads);
 #pragma unroll
         for (uint32_t u = 0; u < 8; ++u) add(q0 + u * kHistThreads, v[u]);
       }
     }
     my_bad = wave_min_u32(my_bad);
     if (lane == 0 && my_bad != kNone) atomicMin(&bad_hist, my_bad);
-  } else {
-    // ---- wave 0: non-finite tiles, then the first round's candidate tiles ----
-    uint32_t lbw = 0;
-#pragma unroll
-    for (int j = 0; j < kTileKeys; ++j) lbw = max(lbw, words[j]);
-    if (__ballot(lbw == kNonFiniteTile)) {
-#pragma unroll
-      for (int j = 0; j < kTileKeys; ++j) {
-        const uint32_t t = lane + 64u * (uint32_t)j;
-        if (words[j] == kNonFiniteTile && t < nf_tile) nf_tile = t;
-      }
-      nf_tile = uniform(wave_min_u32(nf_tile));
-    } else {
-      const uint32_t thr_word = bcast32(wave_sort_desc_u32(lbw, lane), kTopK - 1);
-      // tiles whose word reaches it, and the lane's best word below it
-      uint32_t count = 0, below = 0;
-#pragma unroll
-      for (int j = 0; j < kTileKeys; ++j) {
-        const bool take = words[j] >= thr_word;
-        const uint64_t mask = __ballot(take);
-        if (mask) {
-          // past the list's end nothing is stored; the count then exceeds it
-          const uint32_t slot = count + lanes_below(mask);
-          if (take && slot < kTileCap) tcand[slot] = lane + 64u * (uint32_t)j;
-          count += (uint32_t)__popcll((unsigned long long)mask);
-        }
-        below = max(below, take ? 0u : words[j]);
-      }
-      count = uniform(count);
-      if (count <= kTileCap) {
-        thr = (uint64_t)thr_word << 32;
-        ntiles = count;
-        rem = below != 0 ? word_bound(below) : 0ull;
-      } else {
-        // ties at the threshold word overflow the list: the exact 64-bit rule
-        uint64_t lb = 0;
-#pragma unroll
-        for (int j = 0; j < kTileKeys; ++j) {
-          const uint64_t k = words[j] != 0u ? tile_key(words[j], lane + 64u * (uint32_t)j) : 0ull;
-          lb = k > lb ? k : lb;
-        }
-        thr = shfl64(wave_sort_desc(lb, lane), kTopK - 1);
-        uint64_t below64;
-        ntiles = collect_tiles(thr, ~0ull, below64);
-        rem = below64 != 0 ? tile_bound(below64) : 0ull;
-      }
-      __builtin_amdgcn_wave_barrier();
-      // the first pass's logits are requested now and used after the barrier
-      fetch_pass(0, min(ntiles, (uint32_t)kChunkTiles));
-    }
   }
-  __syncthreads();
+  __syncthreads();  // (3) the bitmap, the first-round lists and the errors are done
   if (wave != 0) return;
 
-  // ---- wave 0: errors, then the best-first selection ----
+  // ---- wave 0: errors, then the first round's candidates ----
   const uint32_t first_bad_hist = bad_hist;
-  if (nf_tile != kNone) {
-    const uint32_t id = nf_tile * kTileIds + lane;
+  const uint32_t nf = nf_tile;
+  if (nf != kNone) {
+    const uint32_t id = nf * kTileIds + lane;
     const uint32_t first = (lrow[id] & 0x7f800000u) == 0x7f800000u ? id : kNone;
     finalize_row(rp, row, 0, wave_min_u32(first), first_bad_hist, lane, r24);
     return;
@@ -1043,57 +1084,96 @@ __global__ __launch_bounds__(kSelectThreads) void lm_select_kernel(LmParams p, R
     finalize_row(rp, row, 0, kNone, first_bad_hist, lane, r24);
     return;
   }
-  uint64_t k20 = 0;  // the row's 20th best key so far
-  bool first_round = true;
-  for (;;) {
-    // every tile in tcand[0 .. ntiles) is read, kChunkTiles at a time; the
-    // first pass's logits are already in xb
-    for (uint32_t base = 0; base < ntiles; base += (uint32_t)kChunkTiles) {
-      const uint32_t nt = uniform(min(ntiles - base, (uint32_t)kChunkTiles));
-      if (base != 0) fetch_pass(base, nt);
-      if (first_round && ntiles <= (uint32_t)kChunkTiles) {
-        // a tile's 64 history bits are bitmap words 2t and 2t + 1: lane i < nt
-        // reads those of tile i
-        const uint64_t hbits =
-            *reinterpret_cast<const uint64_t*>(&bm[2u * (lane < nt ? tl : bcast32(tl, 0))]);
-        const uint32_t clean = uniform((uint32_t)__popcll((unsigned long long)(
-            __ballot(hbits == 0) & ((nt >= 64u ? 0ull : (1ull << nt)) - 1ull))));
-        if (clean >= (uint32_t)kTopK) {
-          // elements whose raw value reaches the threshold word move, one per
-          // lane, through LDS (id and raw bits)
-          const float floor_value = f_of(key_value_bits(thr));
-          uint32_t count = 0;
+  {
+    uint32_t ne[kTileWaves];
+    bool fits = true;
+    uint32_t elems = 0;
 #pragma unroll
-          for (int i = 0; i < kChunkTiles; ++i) {
-            const bool take = f_of(xb[i]) >= floor_value;
-            const uint64_t mask = (uint32_t)i < nt ? __ballot(take) : 0ull;
-            if (mask) {
-              const uint32_t id = bcast32(tl, (uint32_t)i) * kTileIds + lane;
-              const uint32_t slot = count + lanes_below(mask);
-              if (take && slot < kElemCap) ecand[slot] = ((uint64_t)id << 32) | xb[i];
-              count += (uint32_t)__popcll((unsigned long long)mask);
-            }
-          }
-          count = uniform(count);
-          if (count <= 64u) {
-            __builtin_amdgcn_wave_barrier();
-            uint64_t k = 0;
-            if (lane < count) {
-              const uint64_t e = ecand[lane];
-              const uint32_t id = (uint32_t)(e >> 32);
-              const uint32_t xbits = (uint32_t)e;
-              const bool hit = ((bm[id >> 5] >> (id & 31u)) & 1u) != 0u;
-              k = make_key(hit ? penalize_bits(xbits) : xbits, id);
-            }
-            __builtin_amdgcn_wave_barrier();
-            const uint64_t sorted = wave_sort_desc(k, lane);
-            if (lane < (uint32_t)kTopK) top[lane] = sorted;
-            __builtin_amdgcn_wave_barrier();
-            k20 = shfl64(sorted, kTopK - 1);
-            continue;
-          }
+    for (uint32_t w = 0; w < kTileWaves; ++w) {
+      ne[w] = uniform(wave_nelems[w]);
+      fits = fits && uniform(wave_ntiles[w]) <= kWaveTiles && ne[w] <= kWaveElems;
+      elems += ne[w];
+    }
+    if (fits && elems <= 64u) {
+      // lane i < elems keys element i of the concatenated lists
+      uint32_t ew = 0, ek = lane;
+#pragma unroll
+      for (uint32_t v = 0; v + 1u < kTileWaves; ++v) {
+        if (ew == v && ek >= ne[v]) {
+          ek -= ne[v];
+          ew = v + 1u;
         }
       }
+      uint64_t key = 0;
+      if (lane < elems) {
+        const uint64_t e = ecand[ew * kWaveElems + ek];
+        const uint32_t id = (uint32_t)(e >> 32);
+        const uint32_t xbits = (uint32_t)e;
+        const bool hit = ((bm[id >> 5] >> (id & 31u)) & 1u) != 0u;
+        key = make_key(hit ? penalize_bits(xbits) : xbits, id);
+      }
+      const uint64_t sorted = elems <= 32u ? wave_sort_desc<32>(key, lane) : wave_sort_desc(key, lane);
+      // Exact when the 20th best penalised key still reaches thr_word: every
+      // element not keyed has a raw word below it.
+      if ((uint32_t)(shfl64(sorted, kTopK - 1) >> 32) >= thr_first) {
+        finalize_row(rp, row, lane < (uint32_t)kTopK ? sorted : 0, kNone, kNone, lane, r24);
+        return;
+      }
+    }
+  }
+
+  // ---- wave 0: the general selection, best-first over the 64-bit tile keys ----
+  uint32_t all[kTileKeys];  // tile lane + 64 j in all[j], 0 past the last tile
+#pragma unroll
+  for (int j = 0; j < kTileKeys; ++j) {
+    const uint32_t t = lane + 64u * (uint32_t)j;
+    all[j] = t < kTilesPerRow ? tm[t] : 0u;
+  }
+  // Collects the tiles with keys in [lo, hi) into tcand, in lane order per
+  // slot; `below` receives the lane's best key under lo.
+  auto collect_tiles = [&](uint64_t lo, uint64_t hi, uint64_t& below) -> uint32_t {
+    uint32_t count = 0;
+    below = 0;
+#pragma unroll
+    for (int j = 0; j < kTileKeys; ++j) {
+      const uint32_t t = lane + 64u * (uint32_t)j;
+      const uint64_t k = all[j] != 0u ? tile_key(all[j], t) : 0ull;
+      const bool take = k != 0 && k >= lo && k < hi;
+      const uint64_t mask = __ballot(take);
+      if (mask) {
+        if (take) tcand[count + lanes_below(mask)] = t;
+        count += (uint32_t)__popcll((unsigned long long)mask);
+      }
+      below = (k < lo && k > below) ? k : below;
+    }
+    return uniform(count);
+  };
+  uint64_t k20 = 0;   // the row's 20th best key so far
+  uint64_t hi = ~0ull;
+  for (;;) {
+    // the next tiles best-first: keys below hi reaching the 20th best of the
+    // lanes' best such keys
+    uint64_t lb = 0;
+#pragma unroll
+    for (int j = 0; j < kTileKeys; ++j) {
+      const uint64_t k = all[j] != 0u ? tile_key(all[j], lane + 64u * (uint32_t)j) : 0ull;
+      lb = (k < hi && k > lb) ? k : lb;
+    }
+    uint64_t thr = shfl64(wave_sort_desc(lb, lane), kTopK - 1);
+    if (thr == 0) thr = 1;  // fewer than 20 lanes hold a tile: take them all
+    uint64_t below64;
+    const uint32_t ntiles = collect_tiles(thr, hi, below64);
+    const uint64_t rem = below64 != 0 ? tile_bound(below64) : 0ull;
+    __builtin_amdgcn_wave_barrier();
+    for (uint32_t base = 0; base < ntiles; base += (uint32_t)kChunkTiles) {
+      const uint32_t nt = uniform(min(ntiles - base, (uint32_t)kChunkTiles));
+      // the pass's tiles, one per lane (the first tile again past the end),
+      // and their logits: tile i is wave-uniform (readlane), so each load is
+      // a scalar base plus the lane's offset
+      const uint32_t tl = tcand[base + (lane < nt ? lane : 0u)];
+      uint32_t xb[kChunkTiles];
+#pragma unroll
+      for (int i = 0; i < kChunkTiles; ++i) xb[i] = lrow[bcast32(tl, (uint32_t)i) * kTileIds + lane];
       // history bits of the lane's element of each tile, all requested first
       // (element 64 t + lane sits in bitmap word 2 t + lane / 32, bit lane % 32)
       uint32_t hw[kChunkTiles];
@@ -1117,30 +1197,15 @@ __global__ __launch_bounds__(kSelectThreads) void lm_select_kernel(LmParams p, R
       uint64_t floor = shfl64(wave_sort_desc(lbe, lane), kTopK - 1);
       floor = floor > k20 ? floor : k20;
       uint64_t unused;
-      const uint32_t ne = collect_range(ecand, ek, floor, ~0ull, unused);
+      const uint32_t nk = collect_range(ecand, ek, floor, ~0ull, unused);
       __builtin_amdgcn_wave_barrier();
-      const uint64_t t20 = merge_all(top, ecand, ne, lane);
+      const uint64_t t20 = merge_all(top, ecand, nk, lane);
       k20 = t20 > k20 ? t20 : k20;
     }
     // stop once no tile left can reach the top-20
     const uint64_t best = wave_max64(rem);
     if (best == 0 || k20 > best) break;
-    // another round, on the 64-bit keys: the next tiles best-first
-    const uint64_t hi = thr;
-    uint64_t lb = 0;
-#pragma unroll
-    for (int j = 0; j < kTileKeys; ++j) {
-      const uint64_t k = words[j] != 0u ? tile_key(words[j], lane + 64u * (uint32_t)j) : 0ull;
-      lb = (k < hi && k > lb) ? k : lb;
-    }
-    thr = shfl64(wave_sort_desc(lb, lane), kTopK - 1);
-    if (thr == 0) thr = 1;  // fewer than 20 lanes hold a tile: take them all
-    uint64_t below64;
-    ntiles = collect_tiles(thr, hi, below64);
-    rem = below64 != 0 ? tile_bound(below64) : 0ull;
-    __builtin_amdgcn_wave_barrier();
-    fetch_pass(0, min(ntiles, (uint32_t)kChunkTiles));
-    first_round = false;
+    hi = thr;
   }
   const uint64_t key = top[lane < (uint32_t)kTopK ? lane : 0];
   finalize_row(rp, row, lane < (uint32_t)kTopK ? key : 0, kNone, kNone, lane, r24);
