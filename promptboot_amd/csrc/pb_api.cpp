@@ -142,10 +142,10 @@ static size_t max_slots(uint32_t rows, uint32_t forced_segments) {
 }
 
 // Fused LM head workspace for `rows` rows of `cols` columns (either format):
-// the Q8_0 activations and their scales, the tile maxima and, unless the
+// the Q8_0 activations and their scales, the tile maxima and second words and, unless the
 // caller keeps them, the logits.
 struct LmLayout {
-  size_t act_q, act_s, tilemax, logits, total;
+  size_t act_q, act_s, tilemax, tilesec, logits, total;
 };
 static LmLayout lm_layout(uint32_t rows, size_t cols, bool with_logits) {
   auto align = [](size_t x) { return (x + 255) & ~(size_t)255; };
@@ -155,7 +155,8 @@ static LmLayout lm_layout(uint32_t rows, size_t cols, bool with_logits) {
   l.act_q = 0;
   l.act_s = l.act_q + align(blocks * rows_pad * 32);
   l.tilemax = l.act_s + align(blocks * rows_pad * 4);
-  l.logits = l.tilemax + align((size_t)rows * (PB_VOCAB / 64) * 4);
+  l.tilesec = l.tilemax + align((size_t)rows * (PB_VOCAB / 64) * 4);
+  l.logits = l.tilesec + align((size_t)rows * (PB_VOCAB / 64) * 4);
   l.total = l.logits + (with_logits ? align((size_t)rows * PB_VOCAB * 4) : 0);
   return l;
 }
@@ -630,6 +631,7 @@ static uint32_t enqueue_lmhead(pb_context* ctx, const uint8_t* d_packed, size_t 
   p.act_q = reinterpret_cast<int8_t*>(base + lay.act_q);
   p.act_s = reinterpret_cast<float*>(base + lay.act_s);
   p.tilemax = reinterpret_cast<uint32_t*>(base + lay.tilemax);
+  p.tilesec = rows <= pb::kNarrowRows ? reinterpret_cast<uint32_t*>(base + lay.tilesec) : nullptr;
   p.logits = d_logits ? d_logits : reinterpret_cast<uint32_t*>(base + lay.logits);
   p.logits_ld = PB_VOCAB;
 

@@ -67,8 +67,13 @@ struct LmParams {
   size_t logits_ld;
   uint32_t* tilemax;        // rows x 2,374 order word of the largest raw logit per 64-id
                             // tile, 0xffffffff when the tile holds a non-finite logit
+  uint32_t* tilesec;        // rows x 2,374 second words (narrow GEMM only, else null):
+                            // a bound above every other logit's order word of the tile
+                            // (a multiple of 64) plus the maximum's index in the tile
 };
 
+// Batches up to this size take the narrow GEMM.
+constexpr uint32_t kNarrowRows = 64;
 // Rows up to which the narrow GEMM quantises the activations itself.
 constexpr uint32_t kFusedQuantRows = 4;
 

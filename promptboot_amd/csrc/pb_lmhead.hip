@@ -55,10 +55,9 @@ constexpr uint32_t kTileIds = 64;        // vocabulary ids per tile and per work
 constexpr uint32_t kRowsPerWave = 32;   // two 16-row MFMA row tiles per wave in the head
 constexpr uint32_t kGemmThreads = 512;  // eight waves
 constexpr uint32_t kRowsPerGroup = 256;
-// Batches up to this size take lm_gemm_narrow_kernel (measured per step, Q4_0 /
-// Q8_0: B = 64 74.8 / 73.7 us against 92.0 / 98.1 with the wide kernel; B = 128
-// 119.2 / 121.9 against 103.6 / 108.6).
-constexpr uint32_t kNarrowRows = 64;
+// Batches up to kNarrowRows take lm_gemm_narrow_kernel (measured per step,
+// Q4_0 / Q8_0: B = 64 74.8 / 73.7 us against 92.0 / 98.1 with the wide kernel;
+// B = 128 119.2 / 121.9 against 103.6 / 108.6).
 constexpr uint32_t kWordsPerRow = kVocab / 32;
 constexpr uint32_t kTilesPerRow = kVocab / kTileIds;  // 2,374
 constexpr uint32_t kTileBytes = kTileIds * 16;    // packed Q4_0 nibbles of one (block, tile)
@@ -81,6 +80,13 @@ __device__ __forceinline__ uint32_t row16_max_u32(uint32_t v) {
   v = max(v, dpp_or_zero<0x4E>(v));
   v = max(v, dpp_or_zero<0x124>(v));
   return max(v, dpp_or_zero<0x128>(v));
+}
+// The same minimum (every source lane of these patterns is in the row).
+__device__ __forceinline__ uint32_t row16_min_u32(uint32_t v) {
+  v = min(v, dpp_or_zero<0xB1>(v));
+  v = min(v, dpp_or_zero<0x4E>(v));
+  v = min(v, dpp_or_zero<0x124>(v));
+  return min(v, dpp_or_zero<0x128>(v));
 }
 
 // cvttss2si semantics (x86 truncation): NaN and out-of-range give INT_MIN.
@@ -272,16 +278,32 @@ __global__ __launch_bounds__(kBlockThreads) void lm_quant_kernel(LmParams p) {
 // one (above every finite order word, which is at most 0xff7fffff).
 constexpr uint32_t kNonFiniteTile = 0xffffffffu;
 
+// Order word of a finite binary32 value: adding +0 turns -0 into +0, then
+// negative values are inverted (so -0 and +0 share 0x80000000).
+__device__ __forceinline__ uint32_t order_word(float y) {
+  const uint32_t w = b_of(y + 0.0f);
+  return w ^ ((uint32_t)((int32_t)w >> 31) | 0x80000000u);
+}
+// The binary32 bits of a nonzero order word.
+__device__ __forceinline__ uint32_t order_word_bits(uint32_t w) {
+  return (w & 0x80000000u) ? (w & 0x7fffffffu) : ~w;
+}
+// Second word of a tile (kSecond): the tile's other logits all have order
+// words below (word & ~63), and the maximum is element word & 63 of the tile
+// (its lowest, among ties).  A tie at the maximum, or a maximum of zero (whose
+// sign the order word does not keep), gives a bound above the maximum.
+constexpr uint32_t kSecondIndexMask = 63u;
+
 // ---- a wave's results for one 64-id tile ----
 // total[rt][c][i] is row first_row + 16 rt + i, id 64 tile + 4n + c, where
 // first_row is the lane's row of step 0 (lanes 16q .. 16q+15 hold rows 4q + i
 // of each row tile, four consecutive ids per lane).  For the real rows among
 // result registers i < kI: stores the raw logits and the order word of the
 // tile's largest raw logit (kNonFiniteTile when one of them is infinite or
-// NaN).  The repetition penalty is not applied here: the selection applies it
-// to the few tiles it reads (it never raises a value, so the raw maximum
-// bounds the penalised ones).
-template <int kRT, int kI>
+// NaN), and with kSecond the tile's second word.  The repetition penalty is
+// not applied here: the selection applies it to the few tiles it reads (it
+// never raises a value, so the raw maximum bounds the penalised ones).
+template <int kRT, int kI, bool kSecond>
 __device__ __forceinline__ void write_tile(const LmParams& p, const float (&total)[kRT][4][4],
                                            uint32_t first_row, uint32_t tile, uint32_t n) {
   constexpr int kSteps = kRT * kI;
@@ -289,6 +311,7 @@ __device__ __forceinline__ void write_tile(const LmParams& p, const float (&tota
   const size_t ld = p.logits_ld;
   uint32_t* lbase = p.logits + (size_t)first_row * ld + v0 + 4u * n;
   uint32_t o[kSteps];
+  uint32_t ow[kSteps][4];
 #pragma unroll
   for (int s = 0; s < kSteps; ++s) {
     const int rt = s / kI, i = s % kI;
@@ -299,19 +322,39 @@ __device__ __forceinline__ void write_tile(const LmParams& p, const float (&tota
     const float probe = __builtin_fmaf(
         y[0], 0.0f, __builtin_fmaf(y[1], 0.0f, __builtin_fmaf(y[2], 0.0f, y[3] * 0.0f)));
     const float m = fmaxf(fmaxf(y[0], y[1]), fmaxf(y[2], y[3]));
-    // order word of the maximum: adding +0 turns -0 into +0, then negative
-    // values are inverted
-    uint32_t w = b_of(m + 0.0f);
-    w ^= (uint32_t)((int32_t)w >> 31) | 0x80000000u;
-    o[s] = probe != probe ? kNonFiniteTile : w;
+    o[s] = probe != probe ? kNonFiniteTile : order_word(m);
+    if constexpr (kSecond) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) ow[s][c] = order_word(y[c]);
+    }
   }
 #pragma unroll
   for (int s = 0; s < kSteps; ++s) o[s] = row16_max_u32(o[s]);
+  uint32_t sec[kSteps];
+  if constexpr (kSecond) {
+#pragma unroll
+    for (int s = 0; s < kSteps; ++s) {
+      // the maximum's lowest index, then the largest word of the others
+      uint32_t e = 0xffu;
+#pragma unroll
+      for (int c = 3; c >= 0; --c) e = ow[s][c] == o[s] ? 4u * n + (uint32_t)c : e;
+      const uint32_t first = row16_min_u32(e);
+      uint32_t other = 0;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) other = max(other, 4u * n + (uint32_t)c != first ? ow[s][c] : 0u);
+      other = row16_max_u32(other);
+      if (o[s] == 0x80000000u) other = o[s];
+      sec[s] = (((other >> 6) + 1u) << 6) | (first & kSecondIndexMask);
+    }
+  }
   if (n == 0u) {
 #pragma unroll
     for (int s = 0; s < kSteps; ++s) {
       const uint32_t row = first_row + 16u * (uint32_t)(s / kI) + (uint32_t)(s % kI);
-      if (row < p.rows) p.tilemax[(size_t)row * kTilesPerRow + tile] = o[s];
+      if (row < p.rows) {
+        p.tilemax[(size_t)row * kTilesPerRow + tile] = o[s];
+        if constexpr (kSecond) p.tilesec[(size_t)row * kTilesPerRow + tile] = sec[s];
+      }
     }
   }
 }
@@ -538,7 +581,7 @@ __global__ __launch_bounds__(kGemmThreads) void lm_gemm_kernel(LmParams p) {
     gemm(std::false_type{});
   }
 
-  write_tile<2, 4>(p, total, group0 + lrow0 + 4u * q, tile, n);
+  write_tile<2, 4, false>(p, total, group0 + lrow0 + 4u * q, tile, n);
 }
 
 // ---- the head for narrow batches (up to 64 rows) ----
@@ -555,7 +598,10 @@ __global__ __launch_bounds__(kGemmThreads) void lm_gemm_kernel(LmParams p) {
 // infinite or NaN weight scale takes the subtract-then-multiply form for all
 // its blocks.  The loop body has no branch: at a branch's join the compiler
 // waits for every load in flight, which would undo the loads issued ahead.
-// With at most four rows every real row is result register i < kI of lanes
+// For the same reason the Q4_0 block loop is unrolled whole at the model's
+// width (kNB = 28): in the loop form the compiler copies the next block's
+// operands between registers at the loop edge and waits for every load
+// there.  With at most four rows every real row is result register i < kI of lanes
 // 0 .. 15, so the epilogue of the other registers (padding rows) is left
 // out: kI = 1 for one conversation.
 //
@@ -564,7 +610,7 @@ __global__ __launch_bounds__(kGemmThreads) void lm_gemm_kernel(LmParams p) {
 // -- one launch less per step.  The first blocks' weights are requested
 // before the quantisation, so it overlaps their latency.
 constexpr uint32_t kMaxBlocks = 2048 / 32;
-template <bool kQ8, int kRT, int kSets, int kI, bool kFused>
+template <bool kQ8, int kRT, int kSets, int kI, bool kFused, int kNB>
 __global__ __launch_bounds__(256) void lm_gemm_narrow_kernel(LmParams p) {
   static_assert(kI == 4 || kRT == 1, "partial rows only with one row tile");
   static_assert(!kFused || (kRT == 1 && kI <= (int)kFusedQuantRows), "fused rows fit one row tile");
@@ -584,7 +630,9 @@ __global__ __launch_bounds__(256) void lm_gemm_narrow_kernel(LmParams p) {
   const uint32_t n = lane & 15u;
   const uint32_t q = lane >> 4;
   const uint32_t row0 = blockIdx.y * (16u * kRT);  // first row of the wave's group
-  const uint32_t blocks = p.cols / 32u;
+  // kNB > 0: the width is 32 kNB, known at compile time (the block loop is
+  // unrolled whole, so no loaded register crosses a loop edge)
+  const uint32_t blocks = kNB > 0 ? (uint32_t)kNB : p.cols / 32u;
   const uint32_t last = blocks - 1u;
   constexpr uint32_t kWords = kQ8 ? 2u : 1u;  // uint4 of packed weights per lane and block
   constexpr uint32_t kTile = kQ8 ? kTileBytesQ8 : kTileBytes;
@@ -652,7 +700,10 @@ __global__ __launch_bounds__(256) void lm_gemm_narrow_kernel(LmParams p) {
   const v4i magic = {(int)kMagicBits, (int)kMagicBits, (int)kMagicBits, (int)kMagicBits};
   const v4i zero = {0, 0, 0, 0};
 
-  auto run = [&](const Operands& o, auto odd_tag) {
+  // run() hands each value's term of the block (the reference's rounded
+  // product) to sink(rt, c, i, term); add() adds it to the running total.
+  auto add = [&](int rt, int c, int i, float term) { total[rt][c][i] = total[rt][c][i] + term; };
+  auto run = [&](const Operands& o, auto odd_tag, auto sink) {
     constexpr bool kOdd = decltype(odd_tag)::value;
     float wsv[4];
 #pragma unroll
@@ -687,7 +738,7 @@ __global__ __launch_bounds__(256) void lm_gemm_narrow_kernel(LmParams p) {
 #pragma unroll
           for (int i = 0; i < kI; ++i) {
             const float scale = wsv[c] * asv[i];
-            total[rt][c][i] = total[rt][c][i] + (float)d[rt][c][i] * scale;
+            sink(rt, c, i, (float)d[rt][c][i] * scale);
           }
       }
     } else {
@@ -702,7 +753,7 @@ __global__ __launch_bounds__(256) void lm_gemm_narrow_kernel(LmParams p) {
 #pragma unroll
             for (int i = 0; i < kI; ++i) {
               const float y = (__int_as_float(d[rt][c][i]) - kMagic) * wsv[c];
-              total[rt][c][i] = total[rt][c][i] + y * asv[i];
+              sink(rt, c, i, y * asv[i]);
             }
         }
       } else {
@@ -719,7 +770,7 @@ __global__ __launch_bounds__(256) void lm_gemm_narrow_kernel(LmParams p) {
 #pragma unroll
             for (int i = 0; i < kI; ++i) {
               const float y = __builtin_fmaf(__int_as_float(d[rt][c][i]), wsv[c], wnv[c]);
-              total[rt][c][i] = total[rt][c][i] + y * asv[i];
+              sink(rt, c, i, y * asv[i]);
             }
         }
       }
@@ -753,6 +804,19 @@ __global__ __launch_bounds__(256) void lm_gemm_narrow_kernel(LmParams p) {
 #pragma unroll
   for (int k = 0; k < kSets - 1; ++k) load_a(min((uint32_t)k, last), ops[k]);
   auto gemm = [&](auto odd_tag) {
+    if constexpr (kNB > 0) {
+#pragma unroll
+      for (int b = 0; b < kNB; ++b) {
+        if (b + kSets - 1 < kNB) {
+          load_w((uint32_t)(b + kSets - 1), ops[(b + kSets - 1) % kSets]);
+          load_a((uint32_t)(b + kSets - 1), ops[(b + kSets - 1) % kSets]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        run(ops[b % kSets], odd_tag, add);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      return;
+    }
     const uint32_t whole = blocks / kSets * kSets;
 #pragma unroll 1
     for (uint32_t b = 0; b < whole; b += kSets) {
@@ -762,13 +826,13 @@ __global__ __launch_bounds__(256) void lm_gemm_narrow_kernel(LmParams p) {
         load_w(ahead, ops[(k + kSets - 1) % kSets]);
         load_a(ahead, ops[(k + kSets - 1) % kSets]);
         __builtin_amdgcn_sched_barrier(0);
-        run(ops[k], odd_tag);
+        run(ops[k], odd_tag, add);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
 #pragma unroll
     for (int k = 0; k < kSets - 1; ++k)
-      if (whole + (uint32_t)k < blocks) run(ops[k], odd_tag);
+      if (whole + (uint32_t)k < blocks) run(ops[k], odd_tag, add);
   };
   if constexpr (kQ8) {
     gemm(std::false_type{});
@@ -781,7 +845,7 @@ __global__ __launch_bounds__(256) void lm_gemm_narrow_kernel(LmParams p) {
       gemm(std::false_type{});
     }
   }
-  if (live_wave) write_tile<kRT, kI>(p, total, row0 + 4u * q, tile, n);
+  if (live_wave) write_tile<kRT, kI, true>(p, total, row0 + 4u * q, tile, n);
 }
 
 // A value every lane holds alike, moved to a scalar register so that the
@@ -828,6 +892,24 @@ constexpr int kChunkTiles = 32;                        // tiles read per pass
 constexpr uint32_t kElemCap = 20 * kChunkTiles;        // element keys collected per pass
 static_assert(kTileWaves * kWaveElems <= kElemCap, "the first round's elements fit the list");
 static_assert(kTileWaves * kWaveTiles <= 64, "wave 0 checks the first round's tiles one per lane");
+
+// a[i] for a lane's own i < 16 (N <= 16 entries): a select tree on the bits
+// of i, which pass through an empty asm (else the compiler turns the tree back
+// into an indexed access through scratch memory).
+template <int N>
+__device__ __forceinline__ uint32_t pick(const uint32_t (&a)[N], uint32_t i) {
+  static_assert(N <= 16, "four select levels");
+  uint32_t b0 = i & 1u, b1 = i & 2u, b2 = i & 4u, b3 = i & 8u;
+  __asm__ volatile("" : "+v"(b0), "+v"(b1), "+v"(b2), "+v"(b3));
+  uint32_t v8[8], v4[4], v2[2];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) v8[k] = 2 * k >= N ? 0u : (2 * k + 1 < N && b0) ? a[2 * k + 1 < N ? 2 * k + 1 : 0] : a[2 * k < N ? 2 * k : 0];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) v4[k] = b1 ? v8[2 * k + 1] : v8[2 * k];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) v2[k] = b2 ? v4[2 * k + 1] : v4[2 * k];
+  return b3 ? v2[1] : v2[0];
+}
 
 __device__ __forceinline__ uint64_t tile_key(uint32_t word, uint32_t tile) {
   return ((uint64_t)word << 32) | (0xffffu - tile);
@@ -895,12 +977,16 @@ __global__ __launch_bounds__(kSelectThreads) void lm_select_kernel(LmParams p, R
   uint32_t r24 = 0;
   uint32_t thr_first = 0;  // the first round's threshold word (tile waves)
   uint32_t words[kWaveKeys];
+  uint32_t secs[kWaveKeys];  // their second words, when the GEMM wrote them
+  const bool has_sec = p.tilesec != nullptr;
   if (tile_wave) {
     if (wave == 0) r24 = rp.random_24[row];
+    const uint32_t* ts = p.tilesec + (size_t)row * kTilesPerRow;
 #pragma unroll
     for (int j = 0; j < kWaveKeys; ++j) {
       const uint32_t t = lane + 64u * (wave * (uint32_t)kWaveKeys + (uint32_t)j);
       words[j] = t < kTilesPerRow ? tm[t] : 0u;
+      secs[j] = has_sec && t < kTilesPerRow ? ts[t] : ~0u;
     }
   }
   // history waves: the first four uint4 (or eight words) of each thread
@@ -960,11 +1046,32 @@ __global__ __launch_bounds__(kSelectThreads) void lm_select_kernel(LmParams p, R
       for (uint32_t w = 0; w < kTileWaves; ++w) best = max(best, lane_best[w][lane]);
       const uint32_t thr_word = uniform(bcast32(wave_sort_desc_u32(best, lane), kTopK - 1));
       thr_first = thr_word;
-      // the wave's tiles whose word reaches it: a mask of the lane's words,
-      // then one round per word taken (the lanes' lowest remaining bits)
-      uint32_t m = 0;
+      // The wave's tiles whose word reaches it, as masks of the lane's words:
+      // a tile whose second word says that no other logit of it reaches
+      // thr_word gives its maximum directly (element word & 63, the bits of
+      // its order word); the others are read.  One round per bit taken (the
+      // lanes' lowest remaining bits).
+      uint32_t m = 0, d = 0;
 #pragma unroll
-      for (int j = 0; j < kWaveKeys; ++j) m |= (words[j] >= thr_word ? 1u : 0u) << j;
+      for (int j = 0; j < kWaveKeys; ++j) {
+        const bool take = words[j] >= thr_word;
+        m |= (take ? 1u : 0u) << j;
+        d |= (take && (secs[j] & ~kSecondIndexMask) <= thr_word ? 1u : 0u) << j;
+      }
+      m &= ~d;
+      uint64_t* out = ecand + wave * kWaveElems;
+      for (uint64_t mask = __ballot(d != 0); mask != 0; mask = __ballot(d != 0)) {
+        if (d != 0) {
+          const uint32_t j = (uint32_t)__builtin_ctz(d);
+          const uint32_t t = lane + 64u * (wave * (uint32_t)kWaveKeys + j);
+          const uint32_t slot = nelems + lanes_below(mask);
+          if (slot < kWaveElems)
+            out[slot] = ((uint64_t)(t * kTileIds + (pick(secs, j) & kSecondIndexMask)) << 32) |
+                        order_word_bits(pick(words, j));
+          d &= d - 1u;
+        }
+        nelems += (uint32_t)__popcll((unsigned long long)mask);
+      }
       uint32_t count = 0;
       for (uint64_t mask = __ballot(m != 0); mask != 0; mask = __ballot(m != 0)) {
         if (m != 0) {
@@ -976,7 +1083,7 @@ __global__ __launch_bounds__(kSelectThreads) void lm_select_kernel(LmParams p, R
         count += (uint32_t)__popcll((unsigned long long)mask);
       }
       ntiles = uniform(count);
-      if (ntiles <= kWaveTiles) {
+      if (ntiles != 0 && ntiles <= kWaveTiles) {
         __builtin_amdgcn_wave_barrier();
         // their logits (tile i of the wave is wave-uniform: readlane; past the
         // list the row's tile 0 is read again), then the elements whose raw
@@ -990,23 +1097,10 @@ __global__ __launch_bounds__(kSelectThreads) void lm_select_kernel(LmParams p, R
 #pragma unroll
         for (int i = 0; i < (int)kWaveTiles; ++i)
           e |= ((uint32_t)i < ntiles && f_of(xb[i]) >= floor_value ? 1u : 0u) << i;
-        uint64_t* out = ecand + wave * kWaveElems;
         for (uint64_t mask = __ballot(e != 0); mask != 0; mask = __ballot(e != 0)) {
           if (e != 0) {
             const uint32_t i = (uint32_t)__builtin_ctz(e);
-            // xb[i] for the lane's own i: a select tree on the bits of i (the
-            // bits pass through an empty asm, or the compiler turns the tree
-            // back into an indexed access through scratch memory)
-            uint32_t b0 = i & 1u, b1 = i & 2u, b2 = i & 4u, b3 = i & 8u;
-            __asm__ volatile("" : "+v"(b0), "+v"(b1), "+v"(b2), "+v"(b3));
-            uint32_t v8[8], v4[4], v2[2];
-#pragma unroll
-            for (int k = 0; k < 8; ++k) v8[k] = b0 ? xb[2 * k + 1] : xb[2 * k];
-#pragma unroll
-            for (int k = 0; k < 4; ++k) v4[k] = b1 ? v8[2 * k + 1] : v8[2 * k];
-#pragma unroll
-            for (int k = 0; k < 2; ++k) v2[k] = b2 ? v4[2 * k + 1] : v4[2 * k];
-            const uint32_t x = b3 ? v2[1] : v2[0];
+            const uint32_t x = pick(xb, i);
             const uint32_t slot = nelems + lanes_below(mask);
             if (slot < kWaveElems)
               out[slot] = ((uint64_t)(wave_tiles[wave][i] * kTileIds + lane) << 32) | x;
@@ -1269,6 +1363,23 @@ size_t gemm_lds_bytes(uint32_t cols) {
   return (size_t)(cols / 32u) * (kRowsPerGroup + 2u * kTileIds) * sizeof(float);
 }
 
+// The narrow GEMM for one configuration: the Q4_0 block loop unrolled whole
+// at the model's width of 896 (28 blocks), a loop otherwise.  (Unrolled, the
+// Q8_0 kernels are scheduled with every block's results live at once: 512
+// registers and scratch memory.)
+template <bool kQ8, int kRT, int kSets, int kI, bool kFused>
+static void launch_narrow(dim3 grid, hipStream_t stream, const LmParams& p) {
+  if constexpr (!kQ8) {
+    if (p.cols == 896u) {
+      hipLaunchKernelGGL((lm_gemm_narrow_kernel<kQ8, kRT, kSets, kI, kFused, 28>), grid, dim3(256),
+                         0, stream, p);
+      return;
+    }
+  }
+  hipLaunchKernelGGL((lm_gemm_narrow_kernel<kQ8, kRT, kSets, kI, kFused, 0>), grid, dim3(256), 0,
+                     stream, p);
+}
+
 hipError_t launch_lm_sample(const LmParams& p, const RowParams& rp, hipStream_t stream) {
   (void)hipGetLastError();  // report only this call's launch errors
   if (!p.fused_quant) {
@@ -1277,37 +1388,38 @@ hipError_t launch_lm_sample(const LmParams& p, const RowParams& rp, hipStream_t 
                        dim3(kBlockThreads), 0, stream, p);
   }
   if (p.rows <= kNarrowRows) {
-    // Measured (whole step, HIP events, us), loads one / two / three blocks
-    // ahead with one row tile: Q4_0 B = 1 23.3 / 24.0 / 24.7, B = 2 27.2 /
-    // 28.6 / 32.4, B = 4 29.8 / 30.8 / 33.9, B = 32 44.0 / 44.5 / 46.1; Q8_0
-    // B = 1 32.8 / 33.2 / 33.5, B = 4 36.1 / 37.5 / 41.2 (five, seven or ten
-    // ahead were slower still).  Two row tiles with one block ahead give
-    // B = 64 70.8 us (two ahead: 73.8; one tile: 75.3).
+    // Loads one block ahead.  Measured (whole step, HIP events, us) with the
+    // Q4_0 block loop unrolled at width 896, one / two / three / five / seven
+    // blocks ahead: B = 1 19.5 / 20.5 / 20.7 / 22.8 / 23.0, B = 4 26.3 / 26.3
+    // / 27.8 / 28.2 / 36.8, B = 32 39.7 / 40.7 / 42.2 / 43.2 / 51.7; two row
+    // tiles (B = 64) 59.2 / 60.2 / 60.4 / 76.4 / 79.2.  Splitting a tile's
+    // 28 blocks over two or four waves (each keeping its terms until the
+    // previous part's running totals arrive through LDS, so the sums stay in
+    // block order) was slower: B = 1 22.6-25.4 us.
     const uint32_t rt = p.rows <= 32u ? 1u : 2u;
     const dim3 grid((kTilesPerRow + 3) / 4, (p.rows + 16u * rt - 1) / (16u * rt));
-    const dim3 block(256);
     if (p.q8) {
       if (p.rows == 1)
-        hipLaunchKernelGGL((lm_gemm_narrow_kernel<true, 1, 2, 1, true>), grid, block, 0, stream, p);
+        launch_narrow<true, 1, 2, 1, true>(grid, stream, p);
       else if (p.rows == 2)
-        hipLaunchKernelGGL((lm_gemm_narrow_kernel<true, 1, 2, 2, true>), grid, block, 0, stream, p);
+        launch_narrow<true, 1, 2, 2, true>(grid, stream, p);
       else if (p.fused_quant)
-        hipLaunchKernelGGL((lm_gemm_narrow_kernel<true, 1, 2, 4, true>), grid, block, 0, stream, p);
+        launch_narrow<true, 1, 2, 4, true>(grid, stream, p);
       else if (rt == 1)
-        hipLaunchKernelGGL((lm_gemm_narrow_kernel<true, 1, 2, 4, false>), grid, block, 0, stream, p);
+        launch_narrow<true, 1, 2, 4, false>(grid, stream, p);
       else
-        hipLaunchKernelGGL((lm_gemm_narrow_kernel<true, 2, 2, 4, false>), grid, block, 0, stream, p);
+        launch_narrow<true, 2, 2, 4, false>(grid, stream, p);
     } else {
       if (p.rows == 1)
-        hipLaunchKernelGGL((lm_gemm_narrow_kernel<false, 1, 2, 1, true>), grid, block, 0, stream, p);
+        launch_narrow<false, 1, 2, 1, true>(grid, stream, p);
       else if (p.rows == 2)
-        hipLaunchKernelGGL((lm_gemm_narrow_kernel<false, 1, 2, 2, true>), grid, block, 0, stream, p);
+        launch_narrow<false, 1, 2, 2, true>(grid, stream, p);
       else if (p.fused_quant)
-        hipLaunchKernelGGL((lm_gemm_narrow_kernel<false, 1, 2, 4, true>), grid, block, 0, stream, p);
+        launch_narrow<false, 1, 2, 4, true>(grid, stream, p);
       else if (rt == 1)
-        hipLaunchKernelGGL((lm_gemm_narrow_kernel<false, 1, 2, 4, false>), grid, block, 0, stream, p);
+        launch_narrow<false, 1, 2, 4, false>(grid, stream, p);
       else
-        hipLaunchKernelGGL((lm_gemm_narrow_kernel<false, 2, 2, 4, false>), grid, block, 0, stream, p);
+        launch_narrow<false, 2, 2, 4, false>(grid, stream, p);
     }
   } else {
     const dim3 gemm_grid(kTilesPerRow, (p.rows_pad + kRowsPerGroup - 1) / kRowsPerGroup);

@@ -223,6 +223,36 @@ def test_history_holds_the_best_ids(smp, head):
     assert_rows_equal(gtok, gdet, gerr, rtok, rdet, rerr)
 
 
+@pytest.mark.parametrize("rows", [1, 140])
+def test_one_tile_holds_the_best_ids(smp, head, rows):
+    """All 64 ids of one tile get the weights of row 0's best id: row 0's
+    top-20 are 20 tied ids of that tile (lowest ids first), and more elements
+    reach the first round's threshold than it keys at once, so the select
+    takes its general path; through the narrow and the wide GEMM."""
+    import torch
+
+    w, _ = head
+    hidden = w["hidden"][:rows]
+    q4 = w["q4"].reshape(V, workloads.HIDDEN // 32, 18).copy()
+    rlog0 = o.lmhead_logits(hidden[:1], w["q4"], V, workloads.HIDDEN, threads=16)
+    best = int(np.argmax(rlog0[0].view(np.float32)))
+    tile = (best // 64 + 1000) % (V // 64)
+    q4[tile * 64:(tile + 1) * 64] = q4[best]
+    q4 = q4.reshape(-1)
+    packed = smp.pack_lmhead(torch.from_numpy(q4).to("cuda:0"))
+    torch.cuda.synchronize()
+    rlog = o.lmhead_logits(hidden, q4, V, workloads.HIDDEN, threads=16)
+    r0 = rlog[0].view(np.float32)
+    assert (r0[tile * 64:(tile + 1) * 64] == r0.max()).all()
+    r24 = w["random_24"][:rows]
+    glog, gtok, gdet, gerr = run_head(smp, packed, hidden, w["hist"][:rows], w["hist_len"][:rows], r24)
+    assert (glog == rlog).all()
+    rtok, rdet, rerr, _ = o.sample_batch(rlog, w["hist"][:rows], w["hist_len"][:rows], r24, threads=16)
+    assert_rows_equal(gtok, gdet, gerr, rtok, rdet, rerr)
+    top = rdet[0]["ids"]
+    assert ((top >= tile * 64) & (top < tile * 64 + 64)).sum() >= 10
+
+
 def test_every_logit_negative(smp):
     """A head whose logits are all negative: the tile maxima are negative, so
     the penalty multiplies by 1.1 instead of dividing."""
