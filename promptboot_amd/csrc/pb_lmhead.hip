@@ -886,11 +886,11 @@ constexpr uint32_t kSelectThreads = 64u * (kTileWaves + kHistWaves);
 constexpr int kTileKeys = (kTilesPerRow + 63) / 64;    // 38 tile words per lane
 constexpr int kWaveKeys = (kTileKeys + (int)kTileWaves - 1) / (int)kTileWaves;  // 10 per tile wave
 constexpr uint32_t kWaveTiles = 16;                     // tiles a tile wave reads in the first round
-constexpr uint32_t kWaveElems = 64;                     // element slots of a tile wave
+constexpr uint32_t kFirstElems = 64;                    // the first round's element slots
 constexpr uint32_t kTileCap = 20 * kTileKeys;          // tiles collected per round, at most
 constexpr int kChunkTiles = 32;                        // tiles read per pass
 constexpr uint32_t kElemCap = 20 * kChunkTiles;        // element keys collected per pass
-static_assert(kTileWaves * kWaveElems <= kElemCap, "the first round's elements fit the list");
+static_assert(kFirstElems <= kElemCap, "the first round's elements fit the list");
 static_assert(kTileWaves * kWaveTiles <= 64, "wave 0 checks the first round's tiles one per lane");
 
 // a[i] for a lane's own i < 16 (N <= 16 entries): a select tree on the bits
@@ -951,8 +951,8 @@ __global__ __launch_bounds__(kSelectThreads) void lm_select_kernel(LmParams p, R
   __shared__ uint64_t top[kTopK];
   __shared__ uint32_t lane_best[kTileWaves][64];
   __shared__ uint32_t wave_tiles[kTileWaves][kWaveTiles];
-  __shared__ uint32_t wave_ntiles[kTileWaves];
-  __shared__ uint32_t wave_nelems[kTileWaves];
+  __shared__ uint32_t first_elems;  // elements the tile waves appended to ecand
+  __shared__ uint32_t first_fail;   // a tile wave's tiles overflowed its list
   __shared__ uint32_t bad_hist;
   __shared__ uint32_t nf_tile;
   const uint32_t row = blockIdx.x;
@@ -1014,6 +1014,8 @@ __global__ __launch_bounds__(kSelectThreads) void lm_select_kernel(LmParams p, R
   if (tid == 0) {
     bad_hist = kNone;
     nf_tile = kNone;
+    first_elems = 0;
+    first_fail = 0;
   }
   if (tid < (uint32_t)kTopK) top[tid] = 0;
   __syncthreads();  // (1) the bitmap is clear
@@ -1038,8 +1040,14 @@ __global__ __launch_bounds__(kSelectThreads) void lm_select_kernel(LmParams p, R
   __syncthreads();  // (2) the lanes' best words are published
 
   if (tile_wave) {
-    uint32_t ntiles = kWaveTiles + 1u;  // past the cap: no first-round result
-    uint32_t nelems = 0;
+    // Appends a round's elements (mask: the lanes holding one) to ecand: one
+    // LDS atomic reserves their slots past the other waves' elements.
+    auto append = [&](uint64_t mask, bool mine, uint64_t e) {
+      uint32_t base = 0;
+      if (lane == 0) base = atomicAdd(&first_elems, (uint32_t)__popcll((unsigned long long)mask));
+      const uint32_t slot = bcast32(base, 0) + lanes_below(mask);
+      if (mine && slot < kFirstElems) ecand[slot] = e;
+    };
     if (nf_tile == kNone) {
       uint32_t best = 0;
 #pragma unroll
@@ -1059,18 +1067,16 @@ __global__ __launch_bounds__(kSelectThreads) void lm_select_kernel(LmParams p, R
         d |= (take && (secs[j] & ~kSecondIndexMask) <= thr_word ? 1u : 0u) << j;
       }
       m &= ~d;
-      uint64_t* out = ecand + wave * kWaveElems;
       for (uint64_t mask = __ballot(d != 0); mask != 0; mask = __ballot(d != 0)) {
+        uint64_t e = 0;
         if (d != 0) {
           const uint32_t j = (uint32_t)__builtin_ctz(d);
           const uint32_t t = lane + 64u * (wave * (uint32_t)kWaveKeys + j);
-          const uint32_t slot = nelems + lanes_below(mask);
-          if (slot < kWaveElems)
-            out[slot] = ((uint64_t)(t * kTileIds + (pick(secs, j) & kSecondIndexMask)) << 32) |
-                        order_word_bits(pick(words, j));
-          d &= d - 1u;
+          e = ((uint64_t)(t * kTileIds + (pick(secs, j) & kSecondIndexMask)) << 32) |
+              order_word_bits(pick(words, j));
         }
-        nelems += (uint32_t)__popcll((unsigned long long)mask);
+        append(mask, d != 0, e);
+        d &= d - 1u;
       }
       uint32_t count = 0;
       for (uint64_t mask = __ballot(m != 0); mask != 0; mask = __ballot(m != 0)) {
@@ -1082,7 +1088,8 @@ __global__ __launch_bounds__(kSelectThreads) void lm_select_kernel(LmParams p, R
         }
         count += (uint32_t)__popcll((unsigned long long)mask);
       }
-      ntiles = uniform(count);
+      const uint32_t ntiles = uniform(count);
+      if (ntiles > kWaveTiles && lane == 0) first_fail = 1u;
       if (ntiles != 0 && ntiles <= kWaveTiles) {
         __builtin_amdgcn_wave_barrier();
         // their logits (tile i of the wave is wave-uniform: readlane; past the
@@ -1098,22 +1105,15 @@ __global__ __launch_bounds__(kSelectThreads) void lm_select_kernel(LmParams p, R
         for (int i = 0; i < (int)kWaveTiles; ++i)
           e |= ((uint32_t)i < ntiles && f_of(xb[i]) >= floor_value ? 1u : 0u) << i;
         for (uint64_t mask = __ballot(e != 0); mask != 0; mask = __ballot(e != 0)) {
+          uint64_t x = 0;
           if (e != 0) {
             const uint32_t i = (uint32_t)__builtin_ctz(e);
-            const uint32_t x = pick(xb, i);
-            const uint32_t slot = nelems + lanes_below(mask);
-            if (slot < kWaveElems)
-              out[slot] = ((uint64_t)(wave_tiles[wave][i] * kTileIds + lane) << 32) | x;
-            e &= e - 1u;
+            x = ((uint64_t)(wave_tiles[wave][i] * kTileIds + lane) << 32) | pick(xb, i);
           }
-          nelems += (uint32_t)__popcll((unsigned long long)mask);
+          append(mask, e != 0, x);
+          e &= e - 1u;
         }
-        nelems = uniform(nelems);
       }
-    }
-    if (lane == 0) {
-      wave_ntiles[wave] = ntiles;
-      wave_nelems[wave] = nelems;
     }
   } else {
     // ---- the history bitmap and the first bad position ----
@@ -1166,8 +1166,12 @@ __global__ __launch_bounds__(kSelectThreads) void lm_select_kernel(LmParams p, R
   if (wave != 0) return;
 
   // ---- wave 0: errors, then the first round's candidates ----
+  // (every word read at once: one LDS round trip)
   const uint32_t first_bad_hist = bad_hist;
   const uint32_t nf = nf_tile;
+  const uint32_t elems = uniform(first_elems);
+  const bool fits = uniform(first_fail) == 0u && elems <= kFirstElems;
+  const uint64_t cand = ecand[lane];
   if (nf != kNone) {
     const uint32_t id = nf * kTileIds + lane;
     const uint32_t first = (lrow[id] & 0x7f800000u) == 0x7f800000u ? id : kNone;
@@ -1178,41 +1182,21 @@ __global__ __launch_bounds__(kSelectThreads) void lm_select_kernel(LmParams p, R
     finalize_row(rp, row, 0, kNone, first_bad_hist, lane, r24);
     return;
   }
-  {
-    uint32_t ne[kTileWaves];
-    bool fits = true;
-    uint32_t elems = 0;
-#pragma unroll
-    for (uint32_t w = 0; w < kTileWaves; ++w) {
-      ne[w] = uniform(wave_nelems[w]);
-      fits = fits && uniform(wave_ntiles[w]) <= kWaveTiles && ne[w] <= kWaveElems;
-      elems += ne[w];
+  if (fits) {
+    // lane i < elems keys element i
+    uint64_t key = 0;
+    if (lane < elems) {
+      const uint32_t id = (uint32_t)(cand >> 32);
+      const uint32_t xbits = (uint32_t)cand;
+      const bool hit = ((bm[id >> 5] >> (id & 31u)) & 1u) != 0u;
+      key = make_key(hit ? penalize_bits(xbits) : xbits, id);
     }
-    if (fits && elems <= 64u) {
-      // lane i < elems keys element i of the concatenated lists
-      uint32_t ew = 0, ek = lane;
-#pragma unroll
-      for (uint32_t v = 0; v + 1u < kTileWaves; ++v) {
-        if (ew == v && ek >= ne[v]) {
-          ek -= ne[v];
-          ew = v + 1u;
-        }
-      }
-      uint64_t key = 0;
-      if (lane < elems) {
-        const uint64_t e = ecand[ew * kWaveElems + ek];
-        const uint32_t id = (uint32_t)(e >> 32);
-        const uint32_t xbits = (uint32_t)e;
-        const bool hit = ((bm[id >> 5] >> (id & 31u)) & 1u) != 0u;
-        key = make_key(hit ? penalize_bits(xbits) : xbits, id);
-      }
-      const uint64_t sorted = elems <= 32u ? wave_sort_desc<32>(key, lane) : wave_sort_desc(key, lane);
-      // Exact when the 20th best penalised key still reaches thr_word: every
-      // element not keyed has a raw word below it.
-      if ((uint32_t)(shfl64(sorted, kTopK - 1) >> 32) >= thr_first) {
-        finalize_row(rp, row, lane < (uint32_t)kTopK ? sorted : 0, kNone, kNone, lane, r24);
-        return;
-      }
+    const uint64_t sorted = elems <= 32u ? wave_sort_desc<32>(key, lane) : wave_sort_desc(key, lane);
+    // Exact when the 20th best penalised key still reaches thr_word: every
+    // element not keyed has a raw word below it.
+    if ((uint32_t)(shfl64(sorted, kTopK - 1) >> 32) >= thr_first) {
+      finalize_row(rp, row, lane < (uint32_t)kTopK ? sorted : 0, kNone, kNone, lane, r24);
+      return;
     }
   }
 
