@@ -141,6 +141,17 @@ static size_t max_slots(uint32_t rows, uint32_t forced_segments) {
   return best;
 }
 
+// Batched sampler workspace for batches of up to `rows` rows: the slice
+// plan's lists, or the tile words of the small batches that take the LM
+// head's selection (the same region).
+static size_t sample_workspace_bytes(uint32_t rows, uint32_t forced_segments) {
+  const size_t slices = slice_workspace_bytes(max_slots(rows, forced_segments));
+  const size_t tiles =
+      forced_segments ? 0 : (size_t)(rows < pb::kTileSelectRows ? rows : pb::kTileSelectRows) *
+                                pb::kTileSelectBytesPerRow;
+  return slices > tiles ? slices : tiles;
+}
+
 // Fused LM head workspace for `rows` rows of `cols` columns (either format):
 // the Q8_0 activations and their scales, the tile maxima and second words and, unless the
 // caller keeps them, the logits.
@@ -303,7 +314,7 @@ uint32_t pb_context_create(int device, pb_context** out) {
   // the automatic plan for any batch
   if (e == hipSuccess) e = ensure_staging(ctx, PB_CONTEXT_IDS);
   if (e == hipSuccess)
-    e = grow_device(&ctx->d_work, &ctx->list_bytes, slice_workspace_bytes(max_slots(255, 0)));
+    e = grow_device(&ctx->d_work, &ctx->list_bytes, sample_workspace_bytes(255, 0));
   // the device address of pb_sample_batch_noalloc's static scratch, once per device
   void* scratch = nullptr;
   if (e == hipSuccess) e = pb::static_scratch_address(device, &scratch);
@@ -326,7 +337,7 @@ uint32_t pb_context_reserve(pb_context* ctx, uint32_t rows, size_t cols, pb_infe
   std::lock_guard<std::mutex> lock(ctx->mu);
   DeviceGuard guard(ctx->device);
   hipError_t e = grow_device(&ctx->d_work, &ctx->list_bytes,
-                             slice_workspace_bytes(max_slots(rows, ctx->forced_segments)));
+                             sample_workspace_bytes(rows, ctx->forced_segments));
   if (e == hipSuccess && cols != 0 && rows != 0)
     e = grow_device(&ctx->d_lm, &ctx->lm_bytes, lm_workspace_bytes(rows, cols, true));
   return e == hipSuccess ? PB_OK : device_error(err, e);
@@ -403,10 +414,26 @@ static uint32_t enqueue_sample_in(int device, uint32_t forced_segments, void* wo
   p.err = d_err;
   p.hist_vec4 = (p.hist != nullptr && hist_ld >= 4u && (hist_ld & 3u) == 0 &&
                  ((uintptr_t)d_hist & 15u) == 0);
+  set_decode(p, dec);
+  // Small batches (no `seen` exclusion, the automatic plan): the tile words
+  // of the logits, then the LM head's selection, when the workspace holds
+  // the words.
+  if (forced_segments == 0 && d_excl == nullptr && rows <= pb::kTileSelectRows &&
+      work != nullptr && work_bytes >= rows * pb::kTileSelectBytesPerRow) {
+    pb::LmParams lp{};
+    lp.logits = const_cast<uint32_t*>(d_logits);  // read only
+    lp.logits_ld = ld;
+    lp.rows = rows;
+    lp.tilemax = static_cast<uint32_t*>(work);
+    lp.tilesec = lp.tilemax + (size_t)rows * (PB_VOCAB / 64);
+    p.segs = 1;
+    DeviceGuard guard(device);
+    hipError_t e = pb::launch_tile_select(lp, p, stream);
+    return e == hipSuccess ? PB_OK : device_error(err, e);
+  }
   pb::plan_segments(rows, forced_segments, &p.segs, &p.seg_f4);
   p.part_keys = nullptr;
   p.part_meta = nullptr;
-  set_decode(p, dec);
   if (p.segs > 1) {
     const size_t slots = (size_t)rows * p.segs;
     const size_t need = slice_workspace_bytes(slots);

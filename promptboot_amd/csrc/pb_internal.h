@@ -82,6 +82,14 @@ hipError_t launch_lm_pack(const uint8_t* in, uint8_t* out, uint32_t vocab, uint3
 hipError_t launch_lm_pack_q8(const uint8_t* in, uint8_t* out, uint32_t vocab, uint32_t blocks,
                              hipStream_t stream);
 hipError_t launch_lm_sample(const LmParams& p, const RowParams& rp, hipStream_t stream);
+// The batched sampler through the LM head's selection: tile words of the
+// logits (p.logits, p.logits_ld, p.tilemax, p.tilesec, p.rows), then the
+// select kernel.
+hipError_t launch_tile_select(const LmParams& p, const RowParams& rp, hipStream_t stream);
+// Batches up to this size take launch_tile_select (without a `seen`
+// exclusion or a forced slice plan): rows x 2,374 x 8 bytes of workspace.
+constexpr uint32_t kTileSelectRows = 192;
+constexpr size_t kTileSelectBytesPerRow = (size_t)(PB_VOCAB / 64) * 8;
 hipError_t launch_mfma_selftest(int32_t* out, hipStream_t stream);
 
 uint32_t segments_for_rows(uint32_t rows);

@@ -294,6 +294,32 @@ __device__ __forceinline__ uint32_t order_word_bits(uint32_t w) {
 // sign the order word does not keep), gives a bound above the maximum.
 constexpr uint32_t kSecondIndexMask = 63u;
 
+// The lane's part of a tile word: the order word of the largest of its four
+// logits, kNonFiniteTile when one of them is infinite or NaN (y * 0 is NaN
+// exactly then).  The tile word is the maximum over the tile's 16 lanes.
+__device__ __forceinline__ uint32_t lane_tile_word(const float (&y)[4]) {
+  const float probe = __builtin_fmaf(
+      y[0], 0.0f, __builtin_fmaf(y[1], 0.0f, __builtin_fmaf(y[2], 0.0f, y[3] * 0.0f)));
+  const float m = fmaxf(fmaxf(y[0], y[1]), fmaxf(y[2], y[3]));
+  return probe != probe ? kNonFiniteTile : order_word(m);
+}
+// The tile's second word, given the tile word and the lane's four order
+// words (ids 4n .. 4n+3 of the tile); every lane of the 16-lane row returns it.
+__device__ __forceinline__ uint32_t tile_second_word(const uint32_t (&ow)[4], uint32_t word,
+                                                     uint32_t n) {
+  // the maximum's lowest index, then the largest word of the others
+  uint32_t e = 0xffu;
+#pragma unroll
+  for (int c = 3; c >= 0; --c) e = ow[c] == word ? 4u * n + (uint32_t)c : e;
+  const uint32_t first = row16_min_u32(e);
+  uint32_t other = 0;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) other = max(other, 4u * n + (uint32_t)c != first ? ow[c] : 0u);
+  other = row16_max_u32(other);
+  if (word == 0x80000000u) other = word;
+  return (((other >> 6) + 1u) << 6) | (first & kSecondIndexMask);
+}
+
 // ---- a wave's results for one 64-id tile ----
 // total[rt][c][i] is row first_row + 16 rt + i, id 64 tile + 4n + c, where
 // first_row is the lane's row of step 0 (lanes 16q .. 16q+15 hold rows 4q + i
@@ -318,11 +344,7 @@ __device__ __forceinline__ void write_tile(const LmParams& p, const float (&tota
     const float y[4] = {total[rt][0][i], total[rt][1][i], total[rt][2][i], total[rt][3][i]};
     if (first_row + 16u * (uint32_t)rt + (uint32_t)i < p.rows)
       *reinterpret_cast<v4f*>(lbase + (size_t)(16 * rt + i) * ld) = v4f{y[0], y[1], y[2], y[3]};
-    // y * 0 is NaN exactly when y is infinite or NaN
-    const float probe = __builtin_fmaf(
-        y[0], 0.0f, __builtin_fmaf(y[1], 0.0f, __builtin_fmaf(y[2], 0.0f, y[3] * 0.0f)));
-    const float m = fmaxf(fmaxf(y[0], y[1]), fmaxf(y[2], y[3]));
-    o[s] = probe != probe ? kNonFiniteTile : order_word(m);
+    o[s] = lane_tile_word(y);
     if constexpr (kSecond) {
 #pragma unroll
       for (int c = 0; c < 4; ++c) ow[s][c] = order_word(y[c]);
@@ -333,19 +355,7 @@ __device__ __forceinline__ void write_tile(const LmParams& p, const float (&tota
   uint32_t sec[kSteps];
   if constexpr (kSecond) {
 #pragma unroll
-    for (int s = 0; s < kSteps; ++s) {
-      // the maximum's lowest index, then the largest word of the others
-      uint32_t e = 0xffu;
-#pragma unroll
-      for (int c = 3; c >= 0; --c) e = ow[s][c] == o[s] ? 4u * n + (uint32_t)c : e;
-      const uint32_t first = row16_min_u32(e);
-      uint32_t other = 0;
-#pragma unroll
-      for (int c = 0; c < 4; ++c) other = max(other, 4u * n + (uint32_t)c != first ? ow[s][c] : 0u);
-      other = row16_max_u32(other);
-      if (o[s] == 0x80000000u) other = o[s];
-      sec[s] = (((other >> 6) + 1u) << 6) | (first & kSecondIndexMask);
-    }
+    for (int s = 0; s < kSteps; ++s) sec[s] = tile_second_word(ow[s], o[s], n);
   }
   if (n == 0u) {
 #pragma unroll
@@ -872,6 +882,40 @@ __device__ __forceinline__ uint32_t collect_range(uint64_t* cand, const uint64_t
   return uniform(count);
 }
 
+// ---- tile words of given logits (the batched sampler's small batches) ----
+// The same tile and second words as the narrow GEMM writes, from logits in
+// memory: one 16-lane row per (row, 64-id tile), lane n reading ids
+// 4n .. 4n+3 of the tile (one 16-byte load each, read once).  A workgroup
+// takes 64 consecutive tiles of one row, each 16-lane row four of them (tiles
+// g, g + 16, g + 32, g + 48: every load instruction covers 16 whole tiles),
+// all four loads in flight together; the grid's y runs over the rows.
+constexpr uint32_t kTilesPerGroup = 64;
+__global__ __launch_bounds__(256) void tile_words_kernel(LmParams p) {
+  const uint32_t n = threadIdx.x & 15u;
+  const uint32_t g = threadIdx.x >> 4;
+  const uint32_t row = blockIdx.y;
+  const uint32_t* lrow = p.logits + (size_t)row * p.logits_ld;
+  v4u x[4];
+#pragma unroll
+  for (uint32_t k = 0; k < 4; ++k) {
+    // past the last tile the row's last tile is read again (and not stored)
+    const uint32_t t = min(blockIdx.x * kTilesPerGroup + g + 16u * k, kTilesPerRow - 1u);
+    x[k] = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(lrow + t * kTileIds + 4u * n));
+  }
+#pragma unroll
+  for (uint32_t k = 0; k < 4; ++k) {
+    const uint32_t tile = blockIdx.x * kTilesPerGroup + g + 16u * k;
+    const float y[4] = {f_of(x[k].x), f_of(x[k].y), f_of(x[k].z), f_of(x[k].w)};
+    const uint32_t word = row16_max_u32(lane_tile_word(y));
+    const uint32_t ow[4] = {order_word(y[0]), order_word(y[1]), order_word(y[2]), order_word(y[3])};
+    const uint32_t sec = tile_second_word(ow, word, n);
+    if (n == 0u && tile < kTilesPerRow) {
+      p.tilemax[(size_t)row * kTilesPerRow + tile] = word;
+      p.tilesec[(size_t)row * kTilesPerRow + tile] = sec;
+    }
+  }
+}
+
 // ---- selection: one workgroup per row ----
 // A tile's key is its order word with 0xffff - tile below it: tiles hold
 // consecutive ids, so among tiles with equal maxima the lower tile holds the
@@ -886,7 +930,7 @@ constexpr uint32_t kSelectThreads = 64u * (kTileWaves + kHistWaves);
 constexpr int kTileKeys = (kTilesPerRow + 63) / 64;    // 38 tile words per lane
 constexpr int kWaveKeys = (kTileKeys + (int)kTileWaves - 1) / (int)kTileWaves;  // 10 per tile wave
 constexpr uint32_t kWaveTiles = 16;                     // tiles a tile wave reads in the first round
-constexpr uint32_t kFirstElems = 64;                    // the first round's element slots
+constexpr uint32_t kFirstElems = 256;                   // a fast round's element slots
 constexpr uint32_t kTileCap = 20 * kTileKeys;          // tiles collected per round, at most
 constexpr int kChunkTiles = 32;                        // tiles read per pass
 constexpr uint32_t kElemCap = 20 * kChunkTiles;        // element keys collected per pass
@@ -953,6 +997,8 @@ __global__ __launch_bounds__(kSelectThreads) void lm_select_kernel(LmParams p, R
   __shared__ uint32_t wave_tiles[kTileWaves][kWaveTiles];
   __shared__ uint32_t first_elems;  // elements the tile waves appended to ecand
   __shared__ uint32_t first_fail;   // a tile wave's tiles overflowed its list
+  __shared__ uint32_t round2;       // a second round runs, at round2_thr
+  __shared__ uint32_t round2_thr;
   __shared__ uint32_t bad_hist;
   __shared__ uint32_t nf_tile;
   const uint32_t row = blockIdx.x;
@@ -1039,117 +1085,148 @@ __global__ __launch_bounds__(kSelectThreads) void lm_select_kernel(LmParams p, R
   }
   __syncthreads();  // (2) the lanes' best words are published
 
-  if (tile_wave) {
-    // Appends a round's elements (mask: the lanes holding one) to ecand: one
-    // LDS atomic reserves their slots past the other waves' elements.
+  // One round of the tile waves at threshold word `thr`: the wave's tiles whose
+  // word reaches it, as masks of the lane's words.  A tile whose second word
+  // says that no other logit of it reaches thr gives its maximum directly
+  // (element word & 63, the bits of its order word); the others are read
+  // (up to kWaveTiles per wave, else first_fail), and their elements whose raw
+  // value reaches thr kept.  Every element whose raw word reaches thr ends up
+  // in ecand (up to kFirstElems of them; first_elems counts them all).  One
+  // pass per bit taken (the lanes' lowest remaining bits).
+  auto tile_round = [&](uint32_t thr) {
+    // appends a pass's elements (mask: the lanes holding one): one LDS
+    // atomic reserves their slots past the other waves' elements
     auto append = [&](uint64_t mask, bool mine, uint64_t e) {
       uint32_t base = 0;
       if (lane == 0) base = atomicAdd(&first_elems, (uint32_t)__popcll((unsigned long long)mask));
       const uint32_t slot = bcast32(base, 0) + lanes_below(mask);
       if (mine && slot < kFirstElems) ecand[slot] = e;
     };
+    uint32_t m = 0, d = 0;
+#pragma unroll
+    for (int j = 0; j < kWaveKeys; ++j) {
+      const bool take = words[j] >= thr;
+      m |= (take ? 1u : 0u) << j;
+      d |= (take && (secs[j] & ~kSecondIndexMask) <= thr ? 1u : 0u) << j;
+    }
+    m &= ~d;
+    for (uint64_t mask = __ballot(d != 0); mask != 0; mask = __ballot(d != 0)) {
+      uint64_t e = 0;
+      if (d != 0) {
+        const uint32_t j = (uint32_t)__builtin_ctz(d);
+        const uint32_t t = lane + 64u * (wave * (uint32_t)kWaveKeys + j);
+        e = ((uint64_t)(t * kTileIds + (pick(secs, j) & kSecondIndexMask)) << 32) |
+            order_word_bits(pick(words, j));
+      }
+      append(mask, d != 0, e);
+      d &= d - 1u;
+    }
+    uint32_t count = 0;
+    for (uint64_t mask = __ballot(m != 0); mask != 0; mask = __ballot(m != 0)) {
+      if (m != 0) {
+        const uint32_t slot = count + lanes_below(mask);
+        const uint32_t j = (uint32_t)__builtin_ctz(m);
+        if (slot < kWaveTiles) wave_tiles[wave][slot] = lane + 64u * (wave * (uint32_t)kWaveKeys + j);
+        m &= m - 1u;
+      }
+      count += (uint32_t)__popcll((unsigned long long)mask);
+    }
+    const uint32_t ntiles = uniform(count);
+    if (ntiles > kWaveTiles && lane == 0) first_fail = 1u;
+    if (ntiles != 0 && ntiles <= kWaveTiles) {
+      __builtin_amdgcn_wave_barrier();
+      // their logits (tile i of the wave is wave-uniform: readlane; past the
+      // list the row's tile 0 is read again), then the elements whose raw
+      // value reaches thr, as (id, raw bits)
+      const uint32_t tl = lane < ntiles ? wave_tiles[wave][lane] : 0u;
+      uint32_t xb[kWaveTiles];
+#pragma unroll
+      for (int i = 0; i < (int)kWaveTiles; ++i) xb[i] = lrow[bcast32(tl, (uint32_t)i) * kTileIds + lane];
+      const float floor_value = f_of(key_value_bits((uint64_t)thr << 32));
+      uint32_t e = 0;
+#pragma unroll
+      for (int i = 0; i < (int)kWaveTiles; ++i)
+        e |= ((uint32_t)i < ntiles && f_of(xb[i]) >= floor_value ? 1u : 0u) << i;
+      for (uint64_t mask = __ballot(e != 0); mask != 0; mask = __ballot(e != 0)) {
+        uint64_t x = 0;
+        if (e != 0) {
+          const uint32_t i = (uint32_t)__builtin_ctz(e);
+          x = ((uint64_t)(wave_tiles[wave][i] * kTileIds + lane) << 32) | pick(xb, i);
+        }
+        append(mask, e != 0, x);
+        e &= e - 1u;
+      }
+    }
+  };
+
+  if (tile_wave) {
     if (nf_tile == kNone) {
       uint32_t best = 0;
 #pragma unroll
       for (uint32_t w = 0; w < kTileWaves; ++w) best = max(best, lane_best[w][lane]);
-      const uint32_t thr_word = uniform(bcast32(wave_sort_desc_u32(best, lane), kTopK - 1));
-      thr_first = thr_word;
-      // The wave's tiles whose word reaches it, as masks of the lane's words:
-      // a tile whose second word says that no other logit of it reaches
-      // thr_word gives its maximum directly (element word & 63, the bits of
-      // its order word); the others are read.  One round per bit taken (the
-      // lanes' lowest remaining bits).
-      uint32_t m = 0, d = 0;
-#pragma unroll
-      for (int j = 0; j < kWaveKeys; ++j) {
-        const bool take = words[j] >= thr_word;
-        m |= (take ? 1u : 0u) << j;
-        d |= (take && (secs[j] & ~kSecondIndexMask) <= thr_word ? 1u : 0u) << j;
-      }
-      m &= ~d;
-      for (uint64_t mask = __ballot(d != 0); mask != 0; mask = __ballot(d != 0)) {
-        uint64_t e = 0;
-        if (d != 0) {
-          const uint32_t j = (uint32_t)__builtin_ctz(d);
-          const uint32_t t = lane + 64u * (wave * (uint32_t)kWaveKeys + j);
-          e = ((uint64_t)(t * kTileIds + (pick(secs, j) & kSecondIndexMask)) << 32) |
-              order_word_bits(pick(words, j));
-        }
-        append(mask, d != 0, e);
-        d &= d - 1u;
-      }
-      uint32_t count = 0;
-      for (uint64_t mask = __ballot(m != 0); mask != 0; mask = __ballot(m != 0)) {
-        if (m != 0) {
-          const uint32_t slot = count + lanes_below(mask);
-          const uint32_t j = (uint32_t)__builtin_ctz(m);
-          if (slot < kWaveTiles) wave_tiles[wave][slot] = lane + 64u * (wave * (uint32_t)kWaveKeys + j);
-          m &= m - 1u;
-        }
-        count += (uint32_t)__popcll((unsigned long long)mask);
-      }
-      const uint32_t ntiles = uniform(count);
-      if (ntiles > kWaveTiles && lane == 0) first_fail = 1u;
-      if (ntiles != 0 && ntiles <= kWaveTiles) {
-        __builtin_amdgcn_wave_barrier();
-        // their logits (tile i of the wave is wave-uniform: readlane; past the
-        // list the row's tile 0 is read again), then the elements whose raw
-        // value reaches thr_word, as (id, raw bits), one round per element
-        const uint32_t tl = lane < ntiles ? wave_tiles[wave][lane] : 0u;
-        uint32_t xb[kWaveTiles];
-#pragma unroll
-        for (int i = 0; i < (int)kWaveTiles; ++i) xb[i] = lrow[bcast32(tl, (uint32_t)i) * kTileIds + lane];
-        const float floor_value = f_of(key_value_bits((uint64_t)thr_word << 32));
-        uint32_t e = 0;
-#pragma unroll
-        for (int i = 0; i < (int)kWaveTiles; ++i)
-          e |= ((uint32_t)i < ntiles && f_of(xb[i]) >= floor_value ? 1u : 0u) << i;
-        for (uint64_t mask = __ballot(e != 0); mask != 0; mask = __ballot(e != 0)) {
-          uint64_t x = 0;
-          if (e != 0) {
-            const uint32_t i = (uint32_t)__builtin_ctz(e);
-            x = ((uint64_t)(wave_tiles[wave][i] * kTileIds + lane) << 32) | pick(xb, i);
-          }
-          append(mask, e != 0, x);
-          e &= e - 1u;
-        }
-      }
+      thr_first = uniform(bcast32(wave_sort_desc_u32(best, lane), kTopK - 1));
+      tile_round(thr_first);
     }
   } else {
     // ---- the history bitmap and the first bad position ----
     uint32_t my_bad = kNone;
-    auto add = [&](uint32_t pos, uint32_t id) {
-      if (pos >= len) return;
-      if (id >= kVocab) {
-        my_bad = pos < my_bad ? pos : my_bad;
-      } else {
-        uint32_t* word = &bm[id >> 5];
-        const uint32_t bit = 1u << (id & 31u);
-        if ((__hip_atomic_load(word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) & bit) == 0u)
-          atomicOr(word, bit);
-      }
-    };
     if (rp.hist_vec4) {
-      // four uint4 (16 ids) per thread per batch, the next batch requested
-      // before this one is used; the last uint4 of a row stays inside it
-      // (hist_ld is a multiple of 4)
-      for (uint32_t k0 = ht; k0 < n4; k0 += 4u * kHistThreads) {
-        v4u v[4];
-#pragma unroll
-        for (uint32_t u = 0; u < 4; ++u) v[u] = hv[u];
-        if (k0 + 4u * kHistThreads < n4) load_hist(k0 + 4u * kHistThreads);
+      // Sixteen ids (four uint4) per thread per batch: their bitmap words are
+      // read together (one LDS round trip), then only the missing bits are
+      // set (Zipf histories repeat a few ids thousands of times).  Two batches
+      // alternate between register sets and the loads are unconditional
+      // (clamped inside the row; hist_ld is a multiple of 4), so no loaded
+      // register crosses the loop edge and the next batch is in flight while
+      // this one is used.
+      auto batch = [&](uint32_t k0, const v4u (&h)[4]) {
+        uint32_t wi[16], bit[16];
 #pragma unroll
         for (uint32_t u = 0; u < 4; ++u) {
           const uint32_t k = k0 + u * kHistThreads;
-          if (k < n4) {
-            add(4u * k + 0u, v[u].x);
-            add(4u * k + 1u, v[u].y);
-            add(4u * k + 2u, v[u].z);
-            add(4u * k + 3u, v[u].w);
+          const uint32_t ids[4] = {h[u].x, h[u].y, h[u].z, h[u].w};
+#pragma unroll
+          for (uint32_t c = 0; c < 4; ++c) {
+            const uint32_t pos = 4u * k + c;
+            const uint32_t id = ids[c];
+            const bool live = k < n4 && pos < len;
+            if (live && id >= kVocab) my_bad = pos < my_bad ? pos : my_bad;
+            const bool set = live && id < kVocab;
+            wi[4 * u + c] = set ? id >> 5 : 0u;
+            bit[4 * u + c] = set ? 1u << (id & 31u) : 0u;
           }
         }
+        uint32_t cur[16];
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+          cur[e] = __hip_atomic_load(&bm[wi[e]], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+          if ((cur[e] & bit[e]) == 0u && bit[e] != 0u) atomicOr(&bm[wi[e]], bit[e]);
+      };
+      auto load4 = [&](uint32_t k0, v4u (&h)[4]) {
+#pragma unroll
+        for (uint32_t u = 0; u < 4; ++u) h[u] = h4[min(k0 + u * kHistThreads, n4 - 1u)];
+      };
+      v4u hb[4];
+      for (uint32_t k0 = ht; k0 < n4; k0 += 8u * kHistThreads) {
+        load4(k0 + 4u * kHistThreads, hb);
+        batch(k0, hv);
+        if (k0 + 4u * kHistThreads >= n4) break;
+        load4(k0 + 8u * kHistThreads, hv);
+        batch(k0 + 4u * kHistThreads, hb);
       }
     } else {
+      auto add = [&](uint32_t pos, uint32_t id) {
+        if (pos >= len) return;
+        if (id >= kVocab) {
+          my_bad = pos < my_bad ? pos : my_bad;
+        } else {
+          uint32_t* word = &bm[id >> 5];
+          const uint32_t bit = 1u << (id & 31u);
+          if ((__hip_atomic_load(word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) & bit) == 0u)
+            atomicOr(word, bit);
+        }
+      };
       for (uint32_t q0 = ht; q0 < len; q0 += 8u * kHistThreads) {
         uint32_t v[8];
 #pragma unroll
@@ -1163,44 +1240,97 @@ __global__ __launch_bounds__(kSelectThreads) void lm_select_kernel(LmParams p, R
     if (lane == 0 && my_bad != kNone) atomicMin(&bad_hist, my_bad);
   }
   __syncthreads();  // (3) the bitmap, the first-round lists and the errors are done
-  if (wave != 0) return;
 
   // ---- wave 0: errors, then the first round's candidates ----
-  // (every word read at once: one LDS round trip)
-  const uint32_t first_bad_hist = bad_hist;
-  const uint32_t nf = nf_tile;
-  const uint32_t elems = uniform(first_elems);
-  const bool fits = uniform(first_fail) == 0u && elems <= kFirstElems;
-  const uint64_t cand = ecand[lane];
-  if (nf != kNone) {
-    const uint32_t id = nf * kTileIds + lane;
-    const uint32_t first = (lrow[id] & 0x7f800000u) == 0x7f800000u ? id : kNone;
-    finalize_row(rp, row, 0, wave_min_u32(first), first_bad_hist, lane, r24);
-    return;
-  }
-  if (first_bad_hist != kNone) {
-    finalize_row(rp, row, 0, kNone, first_bad_hist, lane, r24);
-    return;
-  }
-  if (fits) {
-    // lane i < elems keys element i
-    uint64_t key = 0;
-    if (lane < elems) {
-      const uint32_t id = (uint32_t)(cand >> 32);
-      const uint32_t xbits = (uint32_t)cand;
-      const bool hit = ((bm[id >> 5] >> (id & 31u)) & 1u) != 0u;
-      key = make_key(hit ? penalize_bits(xbits) : xbits, id);
+  // (every word read at once: one LDS round trip).  Keys the candidates:
+  // lane i < elems keys element i; they are sorted, and the selection is
+  // exact when the 20th best penalised key still reaches the threshold word
+  // (every element not keyed has a raw word below it).
+  enum { kDone, kError, kRound2, kGeneral };
+  int action = kDone;
+  uint32_t first_bad_hist = kNone, nf = kNone;
+  uint64_t sorted = 0;
+  // (up to 64 candidates in one sort; more are keyed in place and merged into
+  // top, 44 at a time)
+  auto key_of = [&](uint64_t cand) {
+    const uint32_t id = (uint32_t)(cand >> 32);
+    const uint32_t xbits = (uint32_t)cand;
+    const bool hit = ((bm[id >> 5] >> (id & 31u)) & 1u) != 0u;
+    return make_key(hit ? penalize_bits(xbits) : xbits, id);
+  };
+  auto key_candidates = [&](uint32_t elems) -> uint64_t {
+    if (elems <= 64u) {
+      const uint64_t cand = ecand[lane];
+      const uint64_t key = lane < elems ? key_of(cand) : 0ull;
+      return elems <= 32u ? wave_sort_desc<32>(key, lane) : wave_sort_desc(key, lane);
     }
-    const uint64_t sorted = elems <= 32u ? wave_sort_desc<32>(key, lane) : wave_sort_desc(key, lane);
-    // Exact when the 20th best penalised key still reaches thr_word: every
-    // element not keyed has a raw word below it.
-    if ((uint32_t)(shfl64(sorted, kTopK - 1) >> 32) >= thr_first) {
+    for (uint32_t i = lane; i < elems; i += 64u) ecand[i] = key_of(ecand[i]);
+    if (lane < (uint32_t)kTopK) top[lane] = 0;
+    __builtin_amdgcn_wave_barrier();
+    merge_all(top, ecand, elems, lane);
+    const uint64_t best = top[lane < (uint32_t)kTopK ? lane : 0];
+    return lane < (uint32_t)kTopK ? best : 0ull;
+  };
+  if (wave == 0) {
+    first_bad_hist = bad_hist;
+    nf = nf_tile;
+    const uint32_t elems = uniform(first_elems);
+    const bool fits = uniform(first_fail) == 0u && elems <= kFirstElems;
+    if (nf != kNone || first_bad_hist != kNone) {
+      action = kError;
+    } else if (fits) {
+      sorted = key_candidates(elems);
+      const uint32_t k20_word = uniform((uint32_t)(shfl64(sorted, kTopK - 1) >> 32));
+      if (k20_word >= thr_first) {
+        action = kDone;
+      } else {
+        // Penalties took the 20th best below the threshold: a second round
+        // at its word.  Every element whose raw word is below it has a key
+        // below the 20th best already held, and the new round's elements
+        // include this round's, so its top-20 is the row's.
+        action = kRound2;
+        if (lane == 0) {
+          round2_thr = k20_word;
+          first_elems = 0;
+          first_fail = 0;
+        }
+      }
+    } else {
+      action = kGeneral;
+    }
+    if (lane == 0) round2 = action == kRound2 ? 1u : 0u;
+  }
+  __syncthreads();  // (4) the decision
+  if (wave == 0 && action == kError) {
+    if (nf != kNone) {
+      const uint32_t id = nf * kTileIds + lane;
+      const uint32_t first = (lrow[id] & 0x7f800000u) == 0x7f800000u ? id : kNone;
+      finalize_row(rp, row, 0, wave_min_u32(first), first_bad_hist, lane, r24);
+    } else {
+      finalize_row(rp, row, 0, kNone, first_bad_hist, lane, r24);
+    }
+    return;
+  }
+  if (wave == 0 && action == kDone) {
+    finalize_row(rp, row, lane < (uint32_t)kTopK ? sorted : 0, kNone, kNone, lane, r24);
+    return;
+  }
+  if (uniform(round2) != 0u) {
+    if (tile_wave) tile_round(uniform(round2_thr));
+    __syncthreads();  // (5) the second round's candidates
+    if (wave != 0) return;
+    const uint32_t elems = uniform(first_elems);
+    if (uniform(first_fail) == 0u && elems <= kFirstElems) {
+      sorted = key_candidates(elems);
       finalize_row(rp, row, lane < (uint32_t)kTopK ? sorted : 0, kNone, kNone, lane, r24);
       return;
     }
   }
+  if (wave != 0) return;
 
   // ---- wave 0: the general selection, best-first over the 64-bit tile keys ----
+  if (lane < (uint32_t)kTopK) top[lane] = 0;
+  __builtin_amdgcn_wave_barrier();
   uint32_t all[kTileKeys];  // tile lane + 64 j in all[j], 0 past the last tile
 #pragma unroll
   for (int j = 0; j < kTileKeys; ++j) {
@@ -1414,6 +1544,15 @@ hipError_t launch_lm_sample(const LmParams& p, const RowParams& rp, hipStream_t 
       hipLaunchKernelGGL(lm_gemm_kernel<false>, gemm_grid, dim3(kGemmThreads),
                          gemm_lds_bytes(p.cols), stream, p);
   }
+  hipLaunchKernelGGL(lm_select_kernel, dim3(p.rows), dim3(kSelectThreads), 0, stream, p, rp);
+  return hipGetLastError();
+}
+
+hipError_t launch_tile_select(const LmParams& p, const RowParams& rp, hipStream_t stream) {
+  (void)hipGetLastError();  // report only this call's launch errors
+  hipLaunchKernelGGL(tile_words_kernel,
+                     dim3((kTilesPerRow + kTilesPerGroup - 1) / kTilesPerGroup, p.rows), dim3(256), 0,
+                     stream, p);
   hipLaunchKernelGGL(lm_select_kernel, dim3(p.rows), dim3(kSelectThreads), 0, stream, p, rp);
   return hipGetLastError();
 }

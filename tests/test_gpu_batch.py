@@ -1,9 +1,11 @@
 """Batched device sampler vs the oracle, row by row, every output bit-exact (GPU).
 
 Covers the workloads of promptboot_amd.workloads (B=1, 64, adversarial
-B=1024 cases, a B=4096 slice of full-context histories), both the
+B=1024 cases, a B=4096 slice of full-context histories), the small batches'
+path through the tile words and the LM head's selection, the
 single-workgroup path (one slice per row) and the multi-slice path with the
-cross-slice merge, error rows, and the in-place penalty variant.
+cross-slice merge (forced slice plans), error rows, and the in-place penalty
+variant.
 """
 import numpy as np
 import pytest
@@ -65,6 +67,19 @@ def test_batch_matches_oracle(sampler, name, rows, segments):
 def test_large_rows_with_full_context_histories(sampler):
     w = workloads.make("large", rows=512)
     assert w["hist"].shape[1] == 32768 and w["hist_len"].max() > 30000
+    got = run_gpu(sampler, w)
+    want = run_oracle(w)
+    assert_rows_equal(*got, *want)
+
+
+@pytest.mark.parametrize("name,rows", [("large", 192), ("ties", 128), ("flat", 128),
+                                       ("dominant", 64)])
+def test_small_batches_take_the_tile_selection(sampler, name, rows):
+    """Up to 192 rows the automatic plan samples through the tile words and the
+    LM head's selection: full-context histories (whose penalties push some
+    rows' top-20 below the first round's threshold, into a second round or
+    the general selection) and the adversarial rows, bit-exact."""
+    w = workloads.make(name, rows=rows)
     got = run_gpu(sampler, w)
     want = run_oracle(w)
     assert_rows_equal(*got, *want)
