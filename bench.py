@@ -28,7 +28,9 @@ The printed JSON line also carries:
                       pinned CPU oracle, min/median/max;
   parity              token agreement with the oracle over every row;
   adversarial_B1024   the flat / ties / dominant / half-vocabulary-history
-                      sub-cases, each timed and checked against the oracle;
+                      sub-cases, each timed and checked against the oracle,
+                      with the read ceiling of the same byte count
+                      (pb_device_read_probe) beside it;
   lmhead_fused        the fused Q4_0 LM head + sampler step (B=256);
   lmhead_q8_fused     the same with the Q8_0 head (the model's output head);
   lmhead_B1           one conversation's step (B=1) through each head;
@@ -249,6 +251,8 @@ def time_batch(smp, w: dict, steps: int, warmup: int, stream) -> dict:
             "launch_ms": kernel_ms, "alg_bytes": alg,
             "achieved_gbs": alg / (kernel_ms / 1e3) / 1e9,
             "segments": int(smp.segments or s.lib().pb_segments_for_rows(B)),
+            "path": ("tile selection" if not smp.segments and B <= s.TILE_SELECT_ROWS
+                     else "slices"),
             "_tokens": tokens, "_detail": detail}
 
 
@@ -482,6 +486,7 @@ def time_adversarial(smp, steps: int, warmup: int, threads: int, stream) -> dict
         log(f"adversarial {name}: generating, timing, checking")
         w = workloads.make(name)
         r = time_batch(smp, w, steps, warmup, stream)
+        ceiling = read_ceiling(r["alg_bytes"], stream)
         rtok, rdet, _, _ = o.sample_batch(w["logits"], w["hist"], w["hist_len"],
                                           w["random_24"], threads=threads)
         boundary = r["_detail"]["flags"] != 0
@@ -489,6 +494,8 @@ def time_adversarial(smp, steps: int, warmup: int, threads: int, stream) -> dict
         out[name] = {"rows": int(len(rtok)), "rows_per_s": round(r["rows_per_s"], 1),
                      "launch_ms": round(r["launch_ms"], 4),
                      "hbm_frac": round(r["achieved_gbs"] / PEAK_HBM_GBS, 4),
+                     "read_ceiling_gbs": ceiling["read_gbs"],
+                     "frac_of_read_ceiling": round(r["achieved_gbs"] / ceiling["read_gbs"], 4),
                      "segments_per_row": r["segments"],
                      "token_agreement": float(agree.mean()),
                      "token_agreement_non_boundary": float(agree[~boundary].mean())
@@ -787,7 +794,8 @@ def main() -> int:
                             "launch_ms": round(r["launch_ms"], 4),
                             "achieved_gbs": round(r["achieved_gbs"], 1),
                             "hbm_frac": round(r["achieved_gbs"] / PEAK_HBM_GBS, 4),
-                            "segments_per_row": r["segments"]}
+                            "segments_per_row": r["segments"] if r["path"] == "slices" else None,
+                            "path": r["path"]}
     out = {
         "metric": METRIC,
         "value": round(main_res["rows_per_s"], 1),

@@ -399,12 +399,20 @@ void pb_decode_draw(pb_sampling_state *states, const uint32_t *row_state, uint32
 uint32_t pb_decode_settle(pb_sampling_state *states, const pb_sampling_state *saved,
                           const uint32_t *state_before, const uint32_t *tokens, uint32_t rows);
 
-/* Segments per row the batched sampler will use for `rows` (diagnostic). */
+/* Batches of up to PB_TILE_SELECT_ROWS rows under the automatic plan (and
+ * without a `seen` exclusion) are sampled through per-tile summaries of the
+ * logits and the fused LM head's selection kernel; larger batches, and every
+ * batch under a forced slice plan, stream each row in slices. */
+#define PB_TILE_SELECT_ROWS 192u
+
+/* Slices per row of the slice plan for `rows` (diagnostic; see
+ * PB_TILE_SELECT_ROWS for the batches that do not use it). */
 uint32_t pb_segments_for_rows(uint32_t rows);
 
 /* Forces the number of row slices of this context's batched calls (0 = auto,
- * otherwise clamped to 1..32).  For tuning and for testing both the
- * single-workgroup and the multi-slice paths on the same rows. */
+ * otherwise clamped to 1..32).  For tuning and for testing the
+ * single-workgroup and the multi-slice paths on the same rows (a forced plan
+ * also turns off the small batches' tile selection). */
 void pb_context_set_segments(pb_context *ctx, uint32_t segments);
 
 /* ---- device arithmetic probes (verification hooks, no reference

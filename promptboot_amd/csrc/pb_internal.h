@@ -88,7 +88,10 @@ hipError_t launch_lm_sample(const LmParams& p, const RowParams& rp, hipStream_t 
 hipError_t launch_tile_select(const LmParams& p, const RowParams& rp, hipStream_t stream);
 // Batches up to this size take launch_tile_select (without a `seen`
 // exclusion or a forced slice plan): rows x 2,374 x 8 bytes of workspace.
-constexpr uint32_t kTileSelectRows = 192;
+// Measured per step (us, tile selection / slice plan), full-context
+// histories: B = 128 34.3 / 36.1, 192 40.6 / 42.2, 255 47.5 / 45.7, 512
+// 87.7 / 63.2; histories of at most 4,096 ids, B = 128: 23.9 / 28.7.
+constexpr uint32_t kTileSelectRows = PB_TILE_SELECT_ROWS;
 constexpr size_t kTileSelectBytesPerRow = (size_t)(PB_VOCAB / 64) * 8;
 hipError_t launch_mfma_selftest(int32_t* out, hipStream_t stream);
 

@@ -34,6 +34,7 @@ import numpy as np
 from . import hip
 
 VOCAB = 151_936
+TILE_SELECT_ROWS = 192  # PB_TILE_SELECT_ROWS: batches up to it take the tile selection
 TOP_K = 20
 SEEN_BYTES = (VOCAB + 7) // 8
 NO_TOKEN = 0xFFFF_FFFF
