@@ -249,29 +249,52 @@ __device__ __forceinline__ void load_block(const LmParams& p, uint32_t row, uint
 
 // ---- Q8_0 activations of every (row, block), batches above kFusedQuantRows ----
 // act_q: [blocks][rows_pad][32] int8 in the contraction order; act_s:
-// [blocks][rows_pad] scales / 16.  Padding rows are zero.  One thread per
-// (row, block).
+// [blocks][rows_pad] scales / 16.  Padding rows are zero.  Eight lanes per
+// (row, block), four activations each (one 16-byte load): lane l holds
+// elements 4l .. 4l+3, which are exactly packed word 2l (l < 4) or 2(l-4)+1 of
+// the contraction order.  The block's largest magnitude (NaN ignored, as
+// quantize_block does) is a maximum over the eight lanes; the arithmetic per
+// element is quantize_block's.
 __global__ __launch_bounds__(kBlockThreads) void lm_quant_kernel(LmParams p) {
   const uint32_t blocks = p.cols / 32u;
-  const uint32_t g = blockIdx.x * kBlockThreads + threadIdx.x;
-  if (g >= p.rows_pad * blocks) return;
-  const uint32_t row = g / blocks;
-  const uint32_t b = g - row * blocks;
-  const bool live = row < p.rows;
-  uint32_t x[32];
-  if (live) {
-    load_block(p, row, b, x);
-  } else {
+  const uint32_t g = blockIdx.x * (kBlockThreads / 8u) + threadIdx.x / 8u;  // (row, block)
+  const uint32_t l = threadIdx.x & 7u;
+  const uint32_t lane = threadIdx.x & 63u;
+  const bool in_range = g < p.rows_pad * blocks;
+  const uint32_t row = in_range ? g / blocks : 0u;
+  const uint32_t b = in_range ? g - row * blocks : 0u;
+  const bool live = in_range && row < p.rows;
+  v4u v = {0u, 0u, 0u, 0u};
+  if (live) v = *reinterpret_cast<const v4u*>(p.hidden + (size_t)row * p.cols + b * 32u + 4u * l);
+  const uint32_t x[4] = {v.x, v.y, v.z, v.w};
+  // magnitudes as order-preserving integers (non-negative floats), NaN as 0
+  uint32_t maximum = 0u;
 #pragma unroll
-    for (int e = 0; e < 32; ++e) x[e] = 0u;
+  for (int e = 0; e < 4; ++e) {
+    const uint32_t magnitude = x[e] & 0x7fffffffu;
+    maximum = magnitude > 0x7f800000u ? maximum : max(maximum, magnitude);
   }
-  uint32_t packed[8];
-  float scale16;
-  quantize_block(x, live, packed, scale16);
-  v4u* dst = reinterpret_cast<v4u*>(p.act_q + ((size_t)b * p.rows_pad + row) * 32);
-  dst[0] = v4u{packed[0], packed[1], packed[2], packed[3]};
-  dst[1] = v4u{packed[4], packed[5], packed[6], packed[7]};
-  p.act_s[(size_t)b * p.rows_pad + row] = scale16;
+  maximum = max(maximum, lane_xor(maximum, 1, lane));
+  maximum = max(maximum, lane_xor(maximum, 2, lane));
+  maximum = max(maximum, lane_xor(maximum, 4, lane));
+  const float scale = f_of(maximum) / f_of(0x42fe0000u);  // / 127
+  const uint32_t h = f32_bits_to_half(b_of(scale));
+  const float act_scale = f_of(half_to_f32_bits(h));
+  const float inverse = b_of(scale) == 0u ? 0.0f : f_of(0x3f800000u) / scale;
+  uint32_t word = 0u;
+  if (live) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float q = f_of(x[e]) * inverse;
+      const float half = (b_of(q) >> 31) == 0u ? f_of(0x3f000000u) : f_of(0xbf000000u);
+      word |= ((uint32_t)trunc_i32_x86(q + half) & 0xffu) << (8 * e);
+    }
+  }
+  if (in_range) {
+    const uint32_t w = l < 4u ? 2u * l : 2u * (l - 4u) + 1u;
+    reinterpret_cast<uint32_t*>(p.act_q + ((size_t)b * p.rows_pad + row) * 32)[w] = word;
+    if (l == 0u) p.act_s[(size_t)b * p.rows_pad + row] = live ? act_scale * 0.0625f : 0.0f;
+  }
 }
 
 // Tile word of a row whose 64 logits in the tile include an infinite or NaN
@@ -1497,8 +1520,8 @@ static void launch_narrow(dim3 grid, hipStream_t stream, const LmParams& p) {
 hipError_t launch_lm_sample(const LmParams& p, const RowParams& rp, hipStream_t stream) {
   (void)hipGetLastError();  // report only this call's launch errors
   if (!p.fused_quant) {
-    const uint32_t pairs = p.rows_pad * (p.cols / 32u);
-    hipLaunchKernelGGL(lm_quant_kernel, dim3((pairs + kBlockThreads - 1) / kBlockThreads),
+    const uint32_t pairs = p.rows_pad * (p.cols / 32u);  // eight lanes each
+    hipLaunchKernelGGL(lm_quant_kernel, dim3((pairs + kBlockThreads / 8u - 1) / (kBlockThreads / 8u)),
                        dim3(kBlockThreads), 0, stream, p);
   }
   if (p.rows <= kNarrowRows) {
