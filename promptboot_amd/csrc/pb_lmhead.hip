@@ -442,38 +442,8 @@ __global__ __launch_bounds__(kGemmThreads) void lm_gemm_kernel(LmParams p) {
   const uint16_t* wscale16 =
       reinterpret_cast<const uint16_t*>(p.weights + (size_t)blocks * kVocab * (kQ8 ? 32 : 16));
 
-  uint32_t odd = 0;  // this tile has an infinite or NaN weight scale
-  for (uint32_t i = tid; i < blocks * kTileIds; i += kGemmThreads) {
-    const uint32_t b = i / kTileIds;
-    const float ws =
-        __half2float(__ushort_as_half(wscale16[(size_t)b * kVocab + v0 + (i - b * kTileIds)]));
-    w_scale[i] = ws;
-    if (!kQ8) {
-      w_neg[i] = ws * -kMagic;
-      odd |= (b_of(ws) & 0x7f800000u) == 0x7f800000u ? 1u : 0u;
-    }
-  }
-  for (uint32_t i = tid; i < blocks * kRowsPerGroup; i += kGemmThreads) {
-    const uint32_t b = i / kRowsPerGroup;
-    const uint32_t r = group0 + (i - b * kRowsPerGroup);
-    // lm_quant_kernel stores a_scale / 16 (exact); the Q8_0 epilogue needs a_scale
-    const float as16 = r < p.rows_pad ? p.act_s[(size_t)b * p.rows_pad + r] : 0.0f;
-    act_scale[i] = kQ8 ? as16 * 16.0f : as16;
-  }
-  const bool odd_tile = __syncthreads_or((int)odd) != 0;
-
   const uint32_t rw0 = group0 + wave * kRowsPerWave;  // this wave's 32 rows
-  if (rw0 >= p.rows_pad) return;  // whole wave idle (no barrier follows)
-  const uint32_t lrow0 = wave * kRowsPerWave;       // first row inside the group
-
-  float total[2][4][4];  // [row tile][column tile][result register]
-#pragma unroll
-  for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-    for (int c = 0; c < 4; ++c)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) total[rt][c][i] = 0.0f;
-
+  const bool live = rw0 < p.rows_pad;                 // else the whole wave idles
   const v4i magic = {(int)kMagicBits, (int)kMagicBits, (int)kMagicBits, (int)kMagicBits};
   const uint8_t* a_base = reinterpret_cast<const uint8_t*>(p.act_q) + ((size_t)rw0 + n) * 32 + 8u * q;
   const size_t a_stride = (size_t)p.rows_pad * 32;  // bytes per block
@@ -502,6 +472,46 @@ __global__ __launch_bounds__(kGemmThreads) void lm_gemm_kernel(LmParams p) {
     for (uint32_t k = 0; k < kWords; ++k)
       o.raw[k] = *reinterpret_cast<const v4u*>(p.weights + (wo + 16u * k));
   };
+  // The first blocks' operands are requested before the scales are staged,
+  // so their latency overlaps the staging and its barrier.
+  Operands s0, s1, s2;
+  const uint32_t last = blocks - 1u;
+  if (live) {
+    load(0, s0);
+    if (kQ8) load(min(1u, last), s1);
+  }
+
+  uint32_t odd = 0;  // this tile has an infinite or NaN weight scale
+  for (uint32_t i = tid; i < blocks * kTileIds; i += kGemmThreads) {
+    const uint32_t b = i / kTileIds;
+    const float ws =
+        __half2float(__ushort_as_half(wscale16[(size_t)b * kVocab + v0 + (i - b * kTileIds)]));
+    w_scale[i] = ws;
+    if (!kQ8) {
+      w_neg[i] = ws * -kMagic;
+      odd |= (b_of(ws) & 0x7f800000u) == 0x7f800000u ? 1u : 0u;
+    }
+  }
+  for (uint32_t i = tid; i < blocks * kRowsPerGroup; i += kGemmThreads) {
+    const uint32_t b = i / kRowsPerGroup;
+    const uint32_t r = group0 + (i - b * kRowsPerGroup);
+    // lm_quant_kernel stores a_scale / 16 (exact); the Q8_0 epilogue needs a_scale
+    const float as16 = r < p.rows_pad ? p.act_s[(size_t)b * p.rows_pad + r] : 0.0f;
+    act_scale[i] = kQ8 ? as16 * 16.0f : as16;
+  }
+  const bool odd_tile = __syncthreads_or((int)odd) != 0;
+
+  if (!live) return;  // whole wave idle (no barrier follows)
+  const uint32_t lrow0 = wave * kRowsPerWave;       // first row inside the group
+
+  float total[2][4][4];  // [row tile][column tile][result register]
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) total[rt][c][i] = 0.0f;
+
   auto run = [&](uint32_t b, const Operands& o, auto odd_tag) {
     constexpr bool kOdd = decltype(odd_tag)::value;
     const v4f ws = *reinterpret_cast<const v4f*>(&w_scale[b * kTileIds + 4u * n]);
@@ -564,9 +574,8 @@ __global__ __launch_bounds__(kGemmThreads) void lm_gemm_kernel(LmParams p) {
   // tail), and scheduling barriers keep each prefetch ahead of the compute it
   // overlaps: otherwise the loads are sunk next to their first use.
   auto gemm = [&](auto odd_tag) {
-    const uint32_t last = blocks - 1u;
-    Operands even, odd_ops;
-    load(0, even);
+    Operands& even = s0;
+    Operands& odd_ops = s1;
 #pragma unroll 1
     for (uint32_t b = 0; b + 1u < blocks; b += 2) {
       load(b + 1u, odd_ops);
@@ -583,10 +592,6 @@ __global__ __launch_bounds__(kGemmThreads) void lm_gemm_kernel(LmParams p) {
   // The Q8_0 head reads twice the weight bytes per block: its loads run two
   // blocks ahead (three operand sets in rotation, the same clamped loads).
   auto gemm_ahead2 = [&]() {
-    const uint32_t last = blocks - 1u;
-    Operands s0, s1, s2;
-    load(0, s0);
-    load(min(1u, last), s1);
     uint32_t b = 0;
 #pragma unroll 1
     for (; b + 2u < blocks; b += 3) {
