@@ -522,12 +522,12 @@ def measured_traffic(version: str) -> dict:
 
 # The kernels of one LM-head step, as (name prefix, grid threads), by leg.
 LM_STEP_KERNELS = {
-    ("q4_0", 256): [("pb::lm_quant_kernel", 7168), ("pb::lm_gemm_kernel<false>", 1215488),
-                    ("pb::lm_select_kernel", 65536)],
-    ("q8_0", 256): [("pb::lm_quant_kernel", 7168), ("pb::lm_gemm_kernel<true>", 1215488),
-                    ("pb::lm_select_kernel", 65536)],
-    ("q4_0", 1): [("pb::lm_gemm_narrow_kernel<false", 152064), ("pb::lm_select_kernel", 256)],
-    ("q8_0", 1): [("pb::lm_gemm_narrow_kernel<true", 152064), ("pb::lm_select_kernel", 256)],
+    ("q4_0", 256): [("pb::lm_quant_kernel", 57344), ("pb::lm_gemm_kernel<false>", 1215488),
+                    ("pb::lm_select_kernel", 131072)],
+    ("q8_0", 256): [("pb::lm_quant_kernel", 57344), ("pb::lm_gemm_kernel<true>", 1215488),
+                    ("pb::lm_select_kernel", 131072)],
+    ("q4_0", 1): [("pb::lm_gemm_narrow_kernel<false", 152064), ("pb::lm_select_kernel", 512)],
+    ("q8_0", 1): [("pb::lm_gemm_narrow_kernel<true", 152064), ("pb::lm_select_kernel", 512)],
 }
 
 
