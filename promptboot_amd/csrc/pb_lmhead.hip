@@ -626,8 +626,9 @@ __global__ __launch_bounds__(kGemmThreads) void lm_gemm_kernel(LmParams p) {
 // The wide kernel stages the scales of 256 rows in LDS and gives each wave
 // 32 rows of one 64-id tile; with few rows most of that work is padding.
 // Here one wave takes one 64-id tile and 16 kRT rows (one MFMA row tile up
-// to 32 rows, two above), four waves per workgroup over consecutive tiles,
-// the grid's y over the row groups.  Each block's weight and activation
+// to 32 rows, two above), four waves per workgroup (two for the Q8_0 head
+// up to 32 rows) over consecutive tiles, the grid's y over the row groups.
+// Each block's weight and activation
 // scales are loaded with its operands (four fp16 weight scales and 4 kRT
 // activation scales per lane), and the loads run kSets - 1 blocks ahead in
 // rotating operand sets: with one wave per tile, the memory in flight per
@@ -648,8 +649,8 @@ __global__ __launch_bounds__(kGemmThreads) void lm_gemm_kernel(LmParams p) {
 // -- one launch less per step.  The first blocks' weights are requested
 // before the quantisation, so it overlaps their latency.
 constexpr uint32_t kMaxBlocks = 2048 / 32;
-template <bool kQ8, int kRT, int kSets, int kI, bool kFused, int kNB>
-__global__ __launch_bounds__(256) void lm_gemm_narrow_kernel(LmParams p) {
+template <bool kQ8, int kRT, int kSets, int kI, bool kFused, int kNB, int kNW>
+__global__ __launch_bounds__(64 * kNW) void lm_gemm_narrow_kernel(LmParams p) {
   static_assert(kI == 4 || kRT == 1, "partial rows only with one row tile");
   static_assert(!kFused || (kRT == 1 && kI <= (int)kFusedQuantRows), "fused rows fit one row tile");
   // kFused: [block][row] quants (8 words) and scales / 16 of the real rows
@@ -659,7 +660,7 @@ __global__ __launch_bounds__(256) void lm_gemm_narrow_kernel(LmParams p) {
   // the tile is wave-uniform: held in scalar registers, so every load below
   // is a scalar base plus a 32-bit lane offset, with no 64-bit address
   // arithmetic per lane
-  const uint32_t tile_raw = blockIdx.x * 4u + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t tile_raw = blockIdx.x * (uint32_t)kNW + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const bool live_wave = tile_raw < kTilesPerRow;
   // waves past the last tile work on the last one (and store nothing), so
   // that every wave reaches the workgroup barrier of the fused quantisation
@@ -826,7 +827,7 @@ __global__ __launch_bounds__(256) void lm_gemm_narrow_kernel(LmParams p) {
   for (int k = 0; k < kSets - 1; ++k) load_w(min((uint32_t)k, last), ops[k]);
   if constexpr (kFused) {
     // the rows' activations, quantised into LDS while those loads fly
-    for (uint32_t pair = threadIdx.x; pair < p.rows * blocks; pair += 256u) {
+    for (uint32_t pair = threadIdx.x; pair < p.rows * blocks; pair += 64u * kNW) {
       const uint32_t r = pair / blocks;
       const uint32_t b = pair - r * blocks;
       uint32_t x[32], packed[8];
@@ -1121,7 +1122,7 @@ __global__ __launch_bounds__(kSelectThreads) void lm_select_kernel(LmParams p, R
   // value reaches thr kept.  Every element whose raw word reaches thr ends up
   // in ecand (up to kFirstElems of them; first_elems counts them all).  One
   // pass per bit taken (the lanes' lowest remaining bits).
-  auto tile_round = [&](uint32_t thr) {
+  auto tile_round = [&](uint32_t thr) __attribute__((always_inline)) {
     // appends a pass's elements (mask: the lanes holding one): one LDS
     // atomic reserves their slots past the other waves' elements
     auto append = [&](uint64_t mask, bool mine, uint64_t e) {
@@ -1236,12 +1237,19 @@ __global__ __launch_bounds__(kSelectThreads) void lm_select_kernel(LmParams p, R
         for (uint32_t u = 0; u < 4; ++u) h[u] = h4[min(k0 + u * kHistThreads, n4 - 1u)];
       };
       v4u hb[4];
-      for (uint32_t k0 = ht; k0 < n4; k0 += 8u * kHistThreads) {
-        load4(k0 + 4u * kHistThreads, hb);
-        batch(k0, hv);
-        if (k0 + 4u * kHistThreads >= n4) break;
-        load4(k0 + 8u * kHistThreads, hv);
-        batch(k0 + 4u * kHistThreads, hb);
+      if (uniform(n4) <= 4u * kHistThreads) {
+        // the loads made at entry hold the whole history: no batch is
+        // requested ahead (a load nothing uses would still be waited for at
+        // the next barrier)
+        if (ht < n4) batch(ht, hv);
+      } else {
+        for (uint32_t k0 = ht; k0 < n4; k0 += 8u * kHistThreads) {
+          load4(k0 + 4u * kHistThreads, hb);
+          batch(k0, hv);
+          if (k0 + 4u * kHistThreads >= n4) break;
+          load4(k0 + 8u * kHistThreads, hv);
+          batch(k0 + 4u * kHistThreads, hb);
+        }
       }
     } else {
       auto add = [&](uint32_t pos, uint32_t id) {
@@ -1286,7 +1294,7 @@ __global__ __launch_bounds__(kSelectThreads) void lm_select_kernel(LmParams p, R
     const bool hit = ((bm[id >> 5] >> (id & 31u)) & 1u) != 0u;
     return make_key(hit ? penalize_bits(xbits) : xbits, id);
   };
-  auto key_candidates = [&](uint32_t elems) -> uint64_t {
+  auto key_candidates = [&](uint32_t elems) __attribute__((always_inline)) -> uint64_t {
     if (elems <= 64u) {
       const uint64_t cand = ecand[lane];
       const uint64_t key = lane < elems ? key_of(cand) : 0ull;
@@ -1508,18 +1516,24 @@ size_t gemm_lds_bytes(uint32_t cols) {
 // The narrow GEMM for one configuration: the Q4_0 block loop unrolled whole
 // at the model's width of 896 (28 blocks), a loop otherwise.  (Unrolled, the
 // Q8_0 kernels are scheduled with every block's results live at once: 512
-// registers and scratch memory.)
+// registers and scratch memory.)  Workgroups of four waves, two for the Q8_0
+// head with one row tile.  Measured (whole step, us, Q4_0 / Q8_0), four /
+// two / one / eight waves: B = 1 20.2 / 29.9, 21.2 / 29.1, 21.3 / 29.6,
+// 21.1 / 32.1; B = 4 26.5 / 33.2, 27.2 / 33.4, 29.0 / 35.2, 27.5 / 36.1;
+// B = 16 27.5 / 34.8, 28.2 / 33.8, 27.8 / 34.5, 30.2 / 38.9.
 template <bool kQ8, int kRT, int kSets, int kI, bool kFused>
-static void launch_narrow(dim3 grid, hipStream_t stream, const LmParams& p) {
+static void launch_narrow(uint32_t rows, hipStream_t stream, const LmParams& p) {
+  constexpr int kNW = kQ8 && kRT == 1 ? 2 : 4;
+  const dim3 grid((kTilesPerRow + kNW - 1) / kNW, (rows + 16u * kRT - 1) / (16u * kRT));
   if constexpr (!kQ8) {
     if (p.cols == 896u) {
-      hipLaunchKernelGGL((lm_gemm_narrow_kernel<kQ8, kRT, kSets, kI, kFused, 28>), grid, dim3(256),
-                         0, stream, p);
+      hipLaunchKernelGGL((lm_gemm_narrow_kernel<kQ8, kRT, kSets, kI, kFused, 28, kNW>), grid,
+                         dim3(64 * kNW), 0, stream, p);
       return;
     }
   }
-  hipLaunchKernelGGL((lm_gemm_narrow_kernel<kQ8, kRT, kSets, kI, kFused, 0>), grid, dim3(256), 0,
-                     stream, p);
+  hipLaunchKernelGGL((lm_gemm_narrow_kernel<kQ8, kRT, kSets, kI, kFused, 0, kNW>), grid,
+                     dim3(64 * kNW), 0, stream, p);
 }
 
 hipError_t launch_lm_sample(const LmParams& p, const RowParams& rp, hipStream_t stream) {
@@ -1539,29 +1553,28 @@ hipError_t launch_lm_sample(const LmParams& p, const RowParams& rp, hipStream_t 
     // previous part's running totals arrive through LDS, so the sums stay in
     // block order) was slower: B = 1 22.6-25.4 us.
     const uint32_t rt = p.rows <= 32u ? 1u : 2u;
-    const dim3 grid((kTilesPerRow + 3) / 4, (p.rows + 16u * rt - 1) / (16u * rt));
     if (p.q8) {
       if (p.rows == 1)
-        launch_narrow<true, 1, 2, 1, true>(grid, stream, p);
+        launch_narrow<true, 1, 2, 1, true>(p.rows, stream, p);
       else if (p.rows == 2)
-        launch_narrow<true, 1, 2, 2, true>(grid, stream, p);
+        launch_narrow<true, 1, 2, 2, true>(p.rows, stream, p);
       else if (p.fused_quant)
-        launch_narrow<true, 1, 2, 4, true>(grid, stream, p);
+        launch_narrow<true, 1, 2, 4, true>(p.rows, stream, p);
       else if (rt == 1)
-        launch_narrow<true, 1, 2, 4, false>(grid, stream, p);
+        launch_narrow<true, 1, 2, 4, false>(p.rows, stream, p);
       else
-        launch_narrow<true, 2, 2, 4, false>(grid, stream, p);
+        launch_narrow<true, 2, 2, 4, false>(p.rows, stream, p);
     } else {
       if (p.rows == 1)
-        launch_narrow<false, 1, 2, 1, true>(grid, stream, p);
+        launch_narrow<false, 1, 2, 1, true>(p.rows, stream, p);
       else if (p.rows == 2)
-        launch_narrow<false, 1, 2, 2, true>(grid, stream, p);
+        launch_narrow<false, 1, 2, 2, true>(p.rows, stream, p);
       else if (p.fused_quant)
-        launch_narrow<false, 1, 2, 4, true>(grid, stream, p);
+        launch_narrow<false, 1, 2, 4, true>(p.rows, stream, p);
       else if (rt == 1)
-        launch_narrow<false, 1, 2, 4, false>(grid, stream, p);
+        launch_narrow<false, 1, 2, 4, false>(p.rows, stream, p);
       else
-        launch_narrow<false, 2, 2, 4, false>(grid, stream, p);
+        launch_narrow<false, 2, 2, 4, false>(p.rows, stream, p);
     }
   } else {
     const dim3 gemm_grid(kTilesPerRow, (p.rows_pad + kRowsPerGroup - 1) / kRowsPerGroup);
