@@ -352,6 +352,12 @@ __device__ __forceinline__ uint32_t tile_second_word(const uint32_t (&ow)[4], ui
 // NaN), and with kSecond the tile's second word.  The repetition penalty is
 // not applied here: the selection applies it to the few tiles it reads (it
 // never raises a value, so the raw maximum bounds the penalised ones).
+// The logits are written with non-temporal stores: the selection reads a few
+// tiles of them, and ordinary stores of a 256-row step (155.6 MB) evict the
+// packed weights that a workgroup's eight waves share through the L2.
+// Measured per 256-row step: Q8_0 161.3-162.0 -> 142.1-149.8 us, Q4_0 about
+// even (128.9-130.0 -> 129.4-134.9 us, HIP events 129.0-131.5 ->
+// 129.4-130.4 us).
 template <int kRT, int kI, bool kSecond>
 __device__ __forceinline__ void write_tile(const LmParams& p, const float (&total)[kRT][4][4],
                                            uint32_t first_row, uint32_t tile, uint32_t n) {
@@ -366,7 +372,8 @@ __device__ __forceinline__ void write_tile(const LmParams& p, const float (&tota
     const int rt = s / kI, i = s % kI;
     const float y[4] = {total[rt][0][i], total[rt][1][i], total[rt][2][i], total[rt][3][i]};
     if (first_row + 16u * (uint32_t)rt + (uint32_t)i < p.rows)
-      *reinterpret_cast<v4f*>(lbase + (size_t)(16 * rt + i) * ld) = v4f{y[0], y[1], y[2], y[3]};
+      __builtin_nontemporal_store(v4f{y[0], y[1], y[2], y[3]},
+                                  reinterpret_cast<v4f*>(lbase + (size_t)(16 * rt + i) * ld));
     o[s] = lane_tile_word(y);
     if constexpr (kSecond) {
 #pragma unroll
