@@ -49,6 +49,7 @@ namespace {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+typedef uint32_t v2u __attribute__((ext_vector_type(2)));
 
 constexpr uint32_t kBlockThreads = 256;
 constexpr uint32_t kTileIds = 64;        // vocabulary ids per tile and per workgroup
@@ -64,6 +65,9 @@ constexpr uint32_t kTileBytes = kTileIds * 16;    // packed Q4_0 nibbles of one 
 constexpr uint32_t kTileBytesQ8 = kTileIds * 32;  // packed Q8_0 weights of one (block, tile)
 // M = 1.5 * 2^23: its binade has unit spacing, so M + i is exact for |i| < 2^22.
 constexpr uint32_t kMagicBits = 0x4b400000u;
+// Word 3 of a buffer resource on gfx9-family parts: 32-bit data format (a
+// raw buffer load needs a valid format), no swizzle, no stride.
+constexpr int kBufferFlags = 0x00020000;
 constexpr float kMagic = 12582912.0f;
 
 // Maximum over the 16 lanes of a DPP row (lanes 16r .. 16r+15), in every
@@ -452,15 +456,21 @@ __global__ __launch_bounds__(kGemmThreads) void lm_gemm_kernel(LmParams p) {
   const uint32_t rw0 = group0 + wave * kRowsPerWave;  // this wave's 32 rows
   const bool live = rw0 < p.rows_pad;                 // else the whole wave idles
   const v4i magic = {(int)kMagicBits, (int)kMagicBits, (int)kMagicBits, (int)kMagicBits};
-  const uint8_t* a_base = reinterpret_cast<const uint8_t*>(p.act_q) + ((size_t)rw0 + n) * 32 + 8u * q;
-  const size_t a_stride = (size_t)p.rows_pad * 32;  // bytes per block
   constexpr uint32_t kWords = kQ8 ? 2u : 1u;  // uint4 of packed weights per lane and block
   constexpr uint32_t kTile = kQ8 ? kTileBytesQ8 : kTileBytes;
-  // The weights are read at the kernel argument plus one 32-bit byte offset
-  // (a scalar base, no 64-bit lane arithmetic): widths of at most 2048 keep
-  // the packed head under 330 MB.
+  // The operands are buffer loads: a lane's byte offset is fixed, the block's
+  // offset is a scalar, so a load costs no VALU address arithmetic (three to
+  // five instructions per block otherwise).  Widths of at most 2048 keep the
+  // packed head under 330 MB, and the activations take blocks * rows_pad * 32
+  // bytes, far below 4 GB for any workspace that holds the rows' logits.
   const uint32_t w_stride = kTilesPerRow * kTile;  // bytes per block
   const uint32_t w_off = tile * kTile + 16u * kWords * lane;
+  const uint32_t a_stride = p.rows_pad * 32u;  // bytes per block
+  const uint32_t a_off = (rw0 + n) * 32u + 8u * q;
+  const __amdgpu_buffer_rsrc_t w_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t*>(p.weights), (short)0, (int)(blocks * w_stride), kBufferFlags);
+  const __amdgpu_buffer_rsrc_t a_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<int8_t*>(p.act_q), (short)0, (int)(blocks * a_stride), kBufferFlags);
 
   // Operands of one block: both row tiles' activation fragments and the
   // lane's packed weight words (one per column tile).  Two sets alternate
@@ -471,13 +481,16 @@ __global__ __launch_bounds__(kGemmThreads) void lm_gemm_kernel(LmParams p) {
     v4u raw[kWords];
   };
   auto load = [&](uint32_t b, Operands& o) {
-    const uint8_t* ab = a_base + (size_t)b * a_stride;
-    o.a[0] = *reinterpret_cast<const uint64_t*>(ab);
-    o.a[1] = *reinterpret_cast<const uint64_t*>(ab + 16u * 32u);
-    const uint32_t wo = b * w_stride + w_off;
+    const uint32_t ab = b * a_stride;
+#pragma unroll
+    for (uint32_t rt = 0; rt < 2; ++rt) {
+      const v2u x = __builtin_amdgcn_raw_buffer_load_b64(a_rsrc, a_off + 16u * 32u * rt, ab, 0);
+      o.a[rt] = (uint64_t)x.x | ((uint64_t)x.y << 32);
+    }
+    const uint32_t wb = b * w_stride;
 #pragma unroll
     for (uint32_t k = 0; k < kWords; ++k)
-      o.raw[k] = *reinterpret_cast<const v4u*>(p.weights + (wo + 16u * k));
+      o.raw[k] = __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, w_off + 16u * k, wb, 0);
   };
   // The first blocks' operands are requested before the scales are staged,
   // so their latency overlaps the staging and its barrier.
