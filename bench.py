@@ -14,8 +14,9 @@ The printed JSON line also carries:
   roofline            the segment kernel's algorithmic HBM bytes per launch
                       over its average launch time (HIP events on the launch
                       stream) against the 8 TB/s MI355X peak; the read
-                      bandwidth the same load pattern reaches on this device
-                      (pb_device_read_probe over the same number of bytes);
+                      bandwidth a plain streaming read of the same number of
+                      bytes reaches on this device (pb_device_read_probe, the
+                      faster of 4096 and 32,768 workgroups);
                       and the HBM traffic measured by rocprofv3 counters,
                       taken from the committed summary only when that summary
                       names this very build (pb_version);
@@ -30,7 +31,7 @@ The printed JSON line also carries:
   adversarial_B1024   the flat / ties / dominant / half-vocabulary-history
                       sub-cases, each timed and checked against the oracle,
                       with the read ceiling of the same byte count
-                      (pb_device_read_probe) beside it;
+                      (pb_device_read_probe, as above) beside it;
   lmhead_fused        the fused Q4_0 LM head + sampler step (B=256);
   lmhead_q8_fused     the same with the Q8_0 head (the model's output head);
   lmhead_B1           one conversation's step (B=1) through each head;
@@ -257,8 +258,12 @@ def time_batch(smp, w: dict, steps: int, warmup: int, stream) -> dict:
 
 
 def read_ceiling(nbytes: int, stream, steps: int = 20) -> dict:
-    """Read bandwidth of the sampler's load pattern (pb_device_read_probe)
-    over a buffer of `nbytes`, 4096 workgroups as in the B=4096 launch."""
+    """Read bandwidth of a plain streaming read (pb_device_read_probe:
+    non-temporal 16-byte loads, one contiguous range per workgroup) over a
+    buffer of `nbytes`, in two shapes: 4096 workgroups (the B=4096 launch's
+    grid) and 32,768 (ranges of a few tens of KB, so the workgroups resident
+    at once read a compact window of the buffer).  The faster shape is the
+    ceiling; both are reported."""
     import ctypes
 
     from promptboot_amd import hip
@@ -266,19 +271,27 @@ def read_ceiling(nbytes: int, stream, steps: int = 20) -> dict:
 
     words = nbytes // 16 * 4
     buf = hip.DeviceArray(words, np.uint32)
-    out = hip.DeviceArray.zeros(4096, np.uint32)
+    out = hip.DeviceArray.zeros(32768, np.uint32)
     h = ctypes.c_void_p(hip.stream_handle(stream))
+    shapes = {}
+    for blocks in (4096, 32768):
+        def step():
+            st = s.lib().pb_device_read_probe(ctypes.c_void_p(buf.data_ptr()), words,
+                                              ctypes.c_void_p(out.data_ptr()), blocks, h)
+            assert st == s.OK
 
-    def step():
-        st = s.lib().pb_device_read_probe(ctypes.c_void_p(buf.data_ptr()), words,
-                                          ctypes.c_void_p(out.data_ptr()), 4096, h)
-        assert st == s.OK
-
-    settle(step)
-    ms = event_pass(step, steps, stream)
+        settle(step)
+        shapes[blocks] = event_pass(step, steps, stream)
     buf.free()
+    out.free()
+    best = min(shapes, key=shapes.get)
+    ms = shapes[best]
     return {"read_gbs": round(words * 4 / (ms / 1e3) / 1e9, 1), "bytes": words * 4,
-            "launch_ms": round(ms, 4), "kernel": "pb::read_probe_kernel (pb_device_read_probe)"}
+            "launch_ms": round(ms, 4), "workgroups": best,
+            "by_workgroups": {str(b): {"launch_ms": round(m, 4),
+                                       "read_gbs": round(words * 4 / (m / 1e3) / 1e9, 1)}
+                              for b, m in shapes.items()},
+            "kernel": "pb::read_probe_kernel (pb_device_read_probe)"}
 
 
 def time_production(stream) -> dict:
@@ -527,7 +540,7 @@ LM_STEP_KERNELS = {
     ("q8_0", 256): [("pb::lm_quant_kernel", 57344), ("pb::lm_gemm_kernel<true>", 1215488),
                     ("pb::lm_select_kernel", 131072)],
     ("q4_0", 1): [("pb::lm_gemm_narrow_kernel<false", 152064), ("pb::lm_select_kernel", 512)],
-    ("q8_0", 1): [("pb::lm_gemm_narrow_kernel<true", 152064), ("pb::lm_select_kernel", 512)],
+    ("q8_0", 1): [("pb::lm_gemm_narrow_kernel<true", 151936), ("pb::lm_select_kernel", 512)],
 }
 
 

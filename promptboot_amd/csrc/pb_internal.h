@@ -62,7 +62,7 @@ struct LmParams {
   uint32_t rows_pad;        // rows rounded up to 64
   uint32_t cols;            // hidden width, multiple of 32
   int8_t* act_q;            // [blocks][rows_pad][32] Q8_0 quants
-  float* act_s;             // [blocks][rows_pad] activation scales / 16
+  float* act_s;             // [blocks][rows_pad] activation scales (a_scale / 16 for Q4_0, a_scale for Q8_0)
   uint32_t* logits;         // rows x logits_ld raw logits (binary32 words)
   size_t logits_ld;
   uint32_t* tilemax;        // rows x 2,374 order word of the largest raw logit per 64-id

@@ -8,10 +8,10 @@
 // followed by the sampler of pb_sampler.hip on the resulting logits rows.
 //
 // Kernels, in launch order:
-//   lm_quant_kernel    (more than kFusedQuantRows rows) one thread per (row,
-//                      block): the Q8_0 activations in the head's contraction
-//                      order and the fp32 activation scales divided by 16,
-//                      zeros for padding rows.
+//   lm_quant_kernel    (more than kFusedQuantRows rows) eight lanes per
+//                      (row, block): the Q8_0 activations in the head's
+//                      contraction order and the fp32 activation scales (for
+//                      the Q4_0 head divided by 16), zeros for padding rows.
 //   lm_gemm_kernel     one workgroup per (64-id vocabulary tile, 256 rows):
 //                      v_mfma_i32_16x16x32_i8 gives each block's exact int32
 //                      dot; the reference's per-block binary32 epilogue runs on
@@ -253,7 +253,8 @@ __device__ __forceinline__ void load_block(const LmParams& p, uint32_t row, uint
 
 // ---- Q8_0 activations of every (row, block), batches above kFusedQuantRows ----
 // act_q: [blocks][rows_pad][32] int8 in the contraction order; act_s:
-// [blocks][rows_pad] scales / 16.  Padding rows are zero.  Eight lanes per
+// [blocks][rows_pad] scales, a_scale / 16 for the Q4_0 head and a_scale for
+// the Q8_0 head (the forms their epilogues take).  Padding rows are zero.  Eight lanes per
 // (row, block), four activations each (one 16-byte load): lane l holds
 // elements 4l .. 4l+3, which are exactly packed word 2l (l < 4) or 2(l-4)+1 of
 // the contraction order.  The block's largest magnitude (NaN ignored, as
@@ -297,7 +298,9 @@ __global__ __launch_bounds__(kBlockThreads) void lm_quant_kernel(LmParams p) {
   if (in_range) {
     const uint32_t w = l < 4u ? 2u * l : 2u * (l - 4u) + 1u;
     reinterpret_cast<uint32_t*>(p.act_q + ((size_t)b * p.rows_pad + row) * 32)[w] = word;
-    if (l == 0u) p.act_s[(size_t)b * p.rows_pad + row] = live ? act_scale * 0.0625f : 0.0f;
+    // the Q4_0 epilogue takes a_scale / 16 (exact), the Q8_0 one a_scale
+    if (l == 0u)
+      p.act_s[(size_t)b * p.rows_pad + row] = live ? (p.q8 ? act_scale : act_scale * 0.0625f) : 0.0f;
   }
 }
 
@@ -501,23 +504,31 @@ __global__ __launch_bounds__(kGemmThreads) void lm_gemm_kernel(LmParams p) {
     if (kQ8) load(min(1u, last), s1);
   }
 
+  // Staged four values per thread and load: the weight scales of four
+  // consecutive ids (8 bytes), the activation scales of four consecutive rows
+  // (16 bytes; rows_pad is a multiple of 64, so four rows are all inside the
+  // padded batch or all past it).  lm_quant_kernel stores a_scale / 16 for the
+  // Q4_0 epilogue and a_scale for the Q8_0 one.
   uint32_t odd = 0;  // this tile has an infinite or NaN weight scale
-  for (uint32_t i = tid; i < blocks * kTileIds; i += kGemmThreads) {
-    const uint32_t b = i / kTileIds;
-    const float ws =
-        __half2float(__ushort_as_half(wscale16[(size_t)b * kVocab + v0 + (i - b * kTileIds)]));
-    w_scale[i] = ws;
-    if (!kQ8) {
-      w_neg[i] = ws * -kMagic;
-      odd |= (b_of(ws) & 0x7f800000u) == 0x7f800000u ? 1u : 0u;
+  for (uint32_t j = tid; j < blocks * (kTileIds / 4u); j += kGemmThreads) {
+    const uint32_t b = j / (kTileIds / 4u);
+    const uint32_t c = j - b * (kTileIds / 4u);
+    const uint64_t h4 = *reinterpret_cast<const uint64_t*>(wscale16 + b * kVocab + v0 + 4u * c);
+    v4f ws;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) ws[k] = __half2float(__ushort_as_half((unsigned short)(h4 >> (16 * k))));
+    *reinterpret_cast<v4f*>(&w_scale[4u * j]) = ws;
+    if constexpr (!kQ8) {
+      *reinterpret_cast<v4f*>(&w_neg[4u * j]) = ws * -kMagic;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) odd |= (b_of(ws[k]) & 0x7f800000u) == 0x7f800000u ? 1u : 0u;
     }
   }
-  for (uint32_t i = tid; i < blocks * kRowsPerGroup; i += kGemmThreads) {
-    const uint32_t b = i / kRowsPerGroup;
-    const uint32_t r = group0 + (i - b * kRowsPerGroup);
-    // lm_quant_kernel stores a_scale / 16 (exact); the Q8_0 epilogue needs a_scale
-    const float as16 = r < p.rows_pad ? p.act_s[(size_t)b * p.rows_pad + r] : 0.0f;
-    act_scale[i] = kQ8 ? as16 * 16.0f : as16;
+  for (uint32_t j = tid; j < blocks * (kRowsPerGroup / 4u); j += kGemmThreads) {
+    const uint32_t b = j / (kRowsPerGroup / 4u);
+    const uint32_t r = group0 + 4u * (j - b * (kRowsPerGroup / 4u));
+    const v4f as = *reinterpret_cast<const v4f*>(p.act_s + b * p.rows_pad + min(r, p.rows_pad - 4u));
+    *reinterpret_cast<v4f*>(&act_scale[4u * j]) = r < p.rows_pad ? as : v4f{0.0f, 0.0f, 0.0f, 0.0f};
   }
   const bool odd_tile = __syncthreads_or((int)odd) != 0;
 
@@ -791,7 +802,7 @@ __global__ __launch_bounds__(64 * kNW) void lm_gemm_narrow_kernel(LmParams p) {
       for (int rt = 0; rt < kRT; ++rt) {
         float asv[kI];
 #pragma unroll
-        for (int i = 0; i < kI; ++i) asv[i] = o.as[rt][i] * 16.0f;
+        for (int i = 0; i < kI; ++i) asv[i] = o.as[rt][i];
 #pragma unroll
         for (int c = 0; c < 4; ++c)
 #pragma unroll
@@ -856,7 +867,7 @@ __global__ __launch_bounds__(64 * kNW) void lm_gemm_narrow_kernel(LmParams p) {
       quantize_block(x, true, packed, scale16);
       *reinterpret_cast<v4u*>(&aq_lds[b][r][0]) = v4u{packed[0], packed[1], packed[2], packed[3]};
       *reinterpret_cast<v4u*>(&aq_lds[b][r][4]) = v4u{packed[4], packed[5], packed[6], packed[7]};
-      as_lds[b][r] = scale16;
+      as_lds[b][r] = kQ8 ? scale16 * 16.0f : scale16;  // a_scale for the Q8_0 epilogue
     }
     __syncthreads();
   }
