@@ -327,10 +327,17 @@ constexpr uint32_t kSecondIndexMask = 63u;
 // The lane's part of a tile word: the order word of the largest of its four
 // logits, kNonFiniteTile when one of them is infinite or NaN (y * 0 is NaN
 // exactly then).  The tile word is the maximum over the tile's 16 lanes.
+// The largest of four values is only used when all four are finite, so it
+// is taken with v_max3_f32 and v_max_f32 as they are: fmaxf would first
+// quieten a signalling NaN in each two-operand maximum's inputs (one more
+// instruction per operand).
 __device__ __forceinline__ uint32_t lane_tile_word(const float (&y)[4]) {
   const float probe = __builtin_fmaf(
       y[0], 0.0f, __builtin_fmaf(y[1], 0.0f, __builtin_fmaf(y[2], 0.0f, y[3] * 0.0f)));
-  const float m = fmaxf(fmaxf(y[0], y[1]), fmaxf(y[2], y[3]));
+  float m;
+  __asm__("v_max3_f32 %0, %1, %2, %3\n\tv_max_f32 %0, %0, %4"
+          : "=&v"(m)
+          : "v"(y[0]), "v"(y[1]), "v"(y[2]), "v"(y[3]));
   return probe != probe ? kNonFiniteTile : order_word(m);
 }
 // The tile's second word, given the tile word and the lane's four order
