@@ -34,7 +34,10 @@ The printed JSON line also carries:
                       (pb_device_read_probe, as above) beside it;
   lmhead_fused        the fused Q4_0 LM head + sampler step (B=256);
   lmhead_q8_fused     the same with the Q8_0 head (the model's output head);
-  lmhead_B1           one conversation's step (B=1) through each head;
+  lmhead_B1           one conversation's step (B=1) through each head,
+                      with a plain read of the same byte count beside it
+                      (read_ceiling_ms; frac_of_read_ceiling = that read's
+                      time over the step's);
                       each LM-head leg also gives its step's HBM traffic
                       (the per-kernel counter figures of the committed
                       summary, same-build only) over its algorithmic bytes;
@@ -466,6 +469,14 @@ def time_lmhead(smp, steps: int, warmup: int, stream, q8: bool = False, rows: in
     # the conversion, w_scale * a_scale, the product and the sum.
     epilogue = (4.0 if q8 else 3.0) * B * workloads.VOCAB * (workloads.HIDDEN // 32)
     alg = workloads.lmhead_algorithmic_bytes(B, w["hist_len"], q8=q8)
+    # one conversation's step streams the head once: beside it, a plain read of
+    # the same number of bytes on this device
+    extra = {}
+    if B == 1:
+        ceiling = read_ceiling(alg, stream)
+        extra = {"read_ceiling_gbs": ceiling["read_gbs"],
+                 "read_ceiling_ms": ceiling["launch_ms"],
+                 "frac_of_read_ceiling": round(ceiling["launch_ms"] / step_ms, 4)}
     return {"rows": B, "ms_per_step": round(wall / steps * 1e3, 4),
             "launch_ms": round(step_ms, 4),
             "rows_per_s": round(B / (wall / steps), 1),
@@ -475,6 +486,7 @@ def time_lmhead(smp, steps: int, warmup: int, stream, q8: bool = False, rows: in
             "alg_bytes": alg,
             "hbm_gbs": round(alg / (step_ms / 1e3) / 1e9, 1),
             "hbm_frac": round(alg / (step_ms / 1e3) / 1e9 / PEAK_HBM_GBS, 4),
+            **extra,
             "parity": parity,
             "workload": (f"B={B} hidden N(0,1) x 896, Q8_0 head 151936x896 (fp16 scales "
                          "U(0.0005,0.004), int8 weights), histories U[16,1024] Zipf; logits "
