@@ -68,6 +68,8 @@ constexpr uint32_t kMagicBits = 0x4b400000u;
 // Word 3 of a buffer resource on gfx9-family parts: 32-bit data format (a
 // raw buffer load needs a valid format), no swizzle, no stride.
 constexpr int kBufferFlags = 0x00020000;
+// Cache policy of a buffer store: non-temporal (the "nt" bit).
+constexpr int kNonTemporal = 2;
 constexpr float kMagic = 12582912.0f;
 
 // Maximum over the 16 lanes of a DPP row (lanes 16r .. 16r+15), in every
@@ -358,15 +360,19 @@ __device__ __forceinline__ uint32_t tile_second_word(const uint32_t (&ow)[4], ui
 }
 
 // ---- a wave's results for one 64-id tile ----
-// total[rt][c][i] is row first_row + 16 rt + i, id 64 tile + 4n + c, where
-// first_row is the lane's row of step 0 (lanes 16q .. 16q+15 hold rows 4q + i
-// of each row tile, four consecutive ids per lane).  For the real rows among
+// total[rt][c][i] is row base_row + lane_row + 16 rt + i, id 64 tile + 4n + c,
+// where base_row is the first row of the wave's group of group_rows rows and
+// lane_row the lane's row of step 0 inside it (lanes 16q .. 16q+15 hold rows
+// 4q + i of each row tile, four consecutive ids per lane).  For the real rows among
 // result registers i < kI: stores the raw logits and the order word of the
 // tile's largest raw logit (kNonFiniteTile when one of them is infinite or
 // NaN), and with kSecond the tile's second word.  The repetition penalty is
 // not applied here: the selection applies it to the few tiles it reads (it
 // never raises a value, so the raw maximum bounds the penalised ones).
-// The logits are written with non-temporal stores: the selection reads a few
+// The logits go out as buffer stores over the group's real rows: a padding
+// row's store falls outside the buffer and is dropped, so no store needs a
+// row test, and each address is the lane's 32-bit offset plus the step's.
+// They are non-temporal: the selection reads a few
 // tiles of them, and ordinary stores of a 256-row step (155.6 MB) evict the
 // packed weights that a workgroup's eight waves share through the L2.
 // Measured per 256-row step: Q8_0 161.3-162.0 -> 142.1-149.8 us, Q4_0 about
@@ -374,20 +380,27 @@ __device__ __forceinline__ uint32_t tile_second_word(const uint32_t (&ow)[4], ui
 // 129.4-130.4 us).
 template <int kRT, int kI, bool kSecond>
 __device__ __forceinline__ void write_tile(const LmParams& p, const float (&total)[kRT][4][4],
-                                           uint32_t first_row, uint32_t tile, uint32_t n) {
+                                           uint32_t base_row, uint32_t group_rows,
+                                           uint32_t lane_row, uint32_t tile, uint32_t n) {
   constexpr int kSteps = kRT * kI;
   const uint32_t v0 = tile * kTileIds;
-  const size_t ld = p.logits_ld;
-  uint32_t* lbase = p.logits + (size_t)first_row * ld + v0 + 4u * n;
+  const uint32_t first_row = base_row + lane_row;
+  // the LM heads' logits are [rows][PB_VOCAB]: a group's rows span at most
+  // 256 x 151,936 words
+  const uint32_t ld = (uint32_t)p.logits_ld;
+  const uint32_t real = p.rows > base_row ? min(p.rows - base_row, group_rows) : 0u;
+  const __amdgpu_buffer_rsrc_t logits = __builtin_amdgcn_make_buffer_rsrc(
+      p.logits + (size_t)base_row * ld, (short)0, (int)(real * ld * 4u), kBufferFlags);
+  const uint32_t lane_off = (lane_row * ld + v0 + 4u * n) * 4u;
   uint32_t o[kSteps];
   uint32_t ow[kSteps][4];
 #pragma unroll
   for (int s = 0; s < kSteps; ++s) {
     const int rt = s / kI, i = s % kI;
     const float y[4] = {total[rt][0][i], total[rt][1][i], total[rt][2][i], total[rt][3][i]};
-    if (first_row + 16u * (uint32_t)rt + (uint32_t)i < p.rows)
-      __builtin_nontemporal_store(v4f{y[0], y[1], y[2], y[3]},
-                                  reinterpret_cast<v4f*>(lbase + (size_t)(16 * rt + i) * ld));
+    __builtin_amdgcn_raw_buffer_store_b128(v4u{b_of(y[0]), b_of(y[1]), b_of(y[2]), b_of(y[3])},
+                                           logits, lane_off + (uint32_t)(16 * rt + i) * ld * 4u, 0,
+                                           kNonTemporal);
     o[s] = lane_tile_word(y);
     if constexpr (kSecond) {
 #pragma unroll
@@ -516,7 +529,6 @@ __global__ __launch_bounds__(kGemmThreads) void lm_gemm_kernel(LmParams p) {
   // (16 bytes; rows_pad is a multiple of 64, so four rows are all inside the
   // padded batch or all past it).  lm_quant_kernel stores a_scale / 16 for the
   // Q4_0 epilogue and a_scale for the Q8_0 one.
-  uint32_t odd = 0;  // this tile has an infinite or NaN weight scale
   for (uint32_t j = tid; j < blocks * (kTileIds / 4u); j += kGemmThreads) {
     const uint32_t b = j / (kTileIds / 4u);
     const uint32_t c = j - b * (kTileIds / 4u);
@@ -525,11 +537,7 @@ __global__ __launch_bounds__(kGemmThreads) void lm_gemm_kernel(LmParams p) {
 #pragma unroll
     for (int k = 0; k < 4; ++k) ws[k] = __half2float(__ushort_as_half((unsigned short)(h4 >> (16 * k))));
     *reinterpret_cast<v4f*>(&w_scale[4u * j]) = ws;
-    if constexpr (!kQ8) {
-      *reinterpret_cast<v4f*>(&w_neg[4u * j]) = ws * -kMagic;
-#pragma unroll
-      for (int k = 0; k < 4; ++k) odd |= (b_of(ws[k]) & 0x7f800000u) == 0x7f800000u ? 1u : 0u;
-    }
+    if constexpr (!kQ8) *reinterpret_cast<v4f*>(&w_neg[4u * j]) = ws * -kMagic;
   }
   for (uint32_t j = tid; j < blocks * (kRowsPerGroup / 4u); j += kGemmThreads) {
     const uint32_t b = j / (kRowsPerGroup / 4u);
@@ -537,7 +545,10 @@ __global__ __launch_bounds__(kGemmThreads) void lm_gemm_kernel(LmParams p) {
     const v4f as = *reinterpret_cast<const v4f*>(p.act_s + b * p.rows_pad + min(r, p.rows_pad - 4u));
     *reinterpret_cast<v4f*>(&act_scale[4u * j]) = r < p.rows_pad ? as : v4f{0.0f, 0.0f, 0.0f, 0.0f};
   }
-  const bool odd_tile = __syncthreads_or((int)odd) != 0;
+  __syncthreads();
+  // a Q4_0 tile with an infinite or NaN weight scale (flagged at pack time)
+  const bool odd_tile =
+      !kQ8 && reinterpret_cast<const uint32_t*>(p.weights + (size_t)blocks * kVocab * 18)[tile] != 0u;
 
   if (!live) return;  // whole wave idle (no barrier follows)
   const uint32_t lrow0 = wave * kRowsPerWave;       // first row inside the group
@@ -657,7 +668,7 @@ __global__ __launch_bounds__(kGemmThreads) void lm_gemm_kernel(LmParams p) {
     gemm(std::false_type{});
   }
 
-  write_tile<2, 4, false>(p, total, group0 + lrow0 + 4u * q, tile, n);
+  write_tile<2, 4, false>(p, total, group0, kRowsPerGroup, lrow0 + 4u * q, tile, n);
 }
 
 // ---- the head for narrow batches (up to 64 rows) ----
@@ -922,7 +933,7 @@ __global__ __launch_bounds__(64 * kNW) void lm_gemm_narrow_kernel(LmParams p) {
       gemm(std::false_type{});
     }
   }
-  if (live_wave) write_tile<kRT, kI, true>(p, total, row0 + 4u * q, tile, n);
+  if (live_wave) write_tile<kRT, kI, true>(p, total, row0, 16u * kRT, 4u * q, tile, n);
 }
 
 // A value every lane holds alike, moved to a scalar register so that the
