@@ -457,7 +457,7 @@ __device__ __forceinline__ void write_tile(const LmParams& p, const float (&tota
 // significant bits.  Folding the conversion into an FMA as above would work,
 // but it needs -M * ws * a_scale per value: one op either way.)
 template <bool kQ8>
-__global__ __launch_bounds__(kGemmThreads) void lm_gemm_kernel(LmParams p) {
+__global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(4))) void lm_gemm_kernel(LmParams p) {
   // Dynamic LDS: the activation scales / 16 of every block for the group's
   // 256 rows, then this tile's weight scales and -M * weight scales by block.
   extern __shared__ __align__(16) float lds[];
@@ -553,15 +553,18 @@ __global__ __launch_bounds__(kGemmThreads) void lm_gemm_kernel(LmParams p) {
   if (!live) return;  // whole wave idle (no barrier follows)
   const uint32_t lrow0 = wave * kRowsPerWave;       // first row inside the group
 
-  float total[2][4][4];  // [row tile][column tile][result register]
-#pragma unroll
-  for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-    for (int c = 0; c < 4; ++c)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) total[rt][c][i] = 0.0f;
+  // [row tile][column tile][result register]; block 0 starts them (first_tag)
+  // as 0 + term, the reference's first add from a zero total, so no register
+  // is cleared beforehand
+  float total[2][4][4];
+  auto sum = [&](int rt, int c, int i, float term, auto first_tag) {
+    if constexpr (decltype(first_tag)::value)
+      total[rt][c][i] = 0.0f + term;
+    else
+      total[rt][c][i] = total[rt][c][i] + term;
+  };
 
-  auto run = [&](uint32_t b, const Operands& o, auto odd_tag) {
+  auto run = [&](uint32_t b, const Operands& o, auto odd_tag, auto first_tag) {
     constexpr bool kOdd = decltype(odd_tag)::value;
     const v4f ws = *reinterpret_cast<const v4f*>(&w_scale[b * kTileIds + 4u * n]);
     const v4f wn = *reinterpret_cast<const v4f*>(&w_neg[b * kTileIds + 4u * n]);
@@ -605,11 +608,11 @@ __global__ __launch_bounds__(kGemmThreads) void lm_gemm_kernel(LmParams p) {
         for (int i = 0; i < 4; ++i) {
           if constexpr (kQ8) {
             const float scale = wsv[c] * asv[i];
-            total[rt][c][i] = total[rt][c][i] + (float)d[rt][c][i] * scale;
+            sum(rt, c, i, (float)d[rt][c][i] * scale, first_tag);
           } else {
             const float x = __int_as_float(d[rt][c][i]);
             const float y = kOdd ? (x - kMagic) * wsv[c] : __builtin_fmaf(x, wsv[c], wnv[c]);
-            total[rt][c][i] = total[rt][c][i] + y * asv[i];
+            sum(rt, c, i, y * asv[i], first_tag);
           }
         }
       }
@@ -622,43 +625,67 @@ __global__ __launch_bounds__(kGemmThreads) void lm_gemm_kernel(LmParams p) {
   // Both halves of the loop body run unconditionally (an odd last block is a
   // tail), and scheduling barriers keep each prefetch ahead of the compute it
   // overlaps: otherwise the loads are sunk next to their first use.
+  // The first round is peeled: its block 0 starts the totals.
+  constexpr std::true_type kFirst{};
+  constexpr std::false_type kNext{};
   auto gemm = [&](auto odd_tag) {
     Operands& even = s0;
     Operands& odd_ops = s1;
+    load(min(1u, last), odd_ops);
+    __builtin_amdgcn_sched_barrier(0);
+    run(0u, even, odd_tag, kFirst);
+    __builtin_amdgcn_sched_barrier(0);
+    load(min(2u, last), even);
+    __builtin_amdgcn_sched_barrier(0);
+    if (blocks > 1u) run(1u, odd_ops, odd_tag, kNext);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll 1
-    for (uint32_t b = 0; b + 1u < blocks; b += 2) {
+    for (uint32_t b = 2; b + 1u < blocks; b += 2) {
       load(b + 1u, odd_ops);
       __builtin_amdgcn_sched_barrier(0);
-      run(b, even, odd_tag);
+      run(b, even, odd_tag, kNext);
       __builtin_amdgcn_sched_barrier(0);
       load(min(b + 2u, last), even);
       __builtin_amdgcn_sched_barrier(0);
-      run(b + 1u, odd_ops, odd_tag);
+      run(b + 1u, odd_ops, odd_tag, kNext);
       __builtin_amdgcn_sched_barrier(0);
     }
-    if (blocks & 1u) run(last, even, odd_tag);
+    if ((blocks & 1u) != 0u && blocks > 1u) run(last, even, odd_tag, kNext);
   };
   // The Q8_0 head reads twice the weight bytes per block: its loads run two
   // blocks ahead (three operand sets in rotation, the same clamped loads).
   auto gemm_ahead2 = [&]() {
-    uint32_t b = 0;
+    constexpr std::false_type kEven{};
+    load(min(2u, last), s2);
+    __builtin_amdgcn_sched_barrier(0);
+    run(0u, s0, kEven, kFirst);
+    __builtin_amdgcn_sched_barrier(0);
+    load(min(3u, last), s0);
+    __builtin_amdgcn_sched_barrier(0);
+    if (blocks > 1u) run(1u, s1, kEven, kNext);
+    __builtin_amdgcn_sched_barrier(0);
+    load(min(4u, last), s1);
+    __builtin_amdgcn_sched_barrier(0);
+    if (blocks > 2u) run(2u, s2, kEven, kNext);
+    __builtin_amdgcn_sched_barrier(0);
+    uint32_t b = 3;
 #pragma unroll 1
     for (; b + 2u < blocks; b += 3) {
       load(min(b + 2u, last), s2);
       __builtin_amdgcn_sched_barrier(0);
-      run(b, s0, std::false_type{});
+      run(b, s0, kEven, kNext);
       __builtin_amdgcn_sched_barrier(0);
       load(min(b + 3u, last), s0);
       __builtin_amdgcn_sched_barrier(0);
-      run(b + 1u, s1, std::false_type{});
+      run(b + 1u, s1, kEven, kNext);
       __builtin_amdgcn_sched_barrier(0);
       load(min(b + 4u, last), s1);
       __builtin_amdgcn_sched_barrier(0);
-      run(b + 2u, s2, std::false_type{});
+      run(b + 2u, s2, kEven, kNext);
       __builtin_amdgcn_sched_barrier(0);
     }
-    if (b < blocks) run(b, s0, std::false_type{});
-    if (b + 1u < blocks) run(b + 1u, s1, std::false_type{});
+    if (b < blocks) run(b, s0, kEven, kNext);
+    if (b + 1u < blocks) run(b + 1u, s1, kEven, kNext);
   };
   if constexpr (kQ8) {
     gemm_ahead2();
