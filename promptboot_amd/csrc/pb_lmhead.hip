@@ -1141,44 +1141,67 @@ __global__ __launch_bounds__(kSelectThreads) void lm_select_kernel(LmParams p, R
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = tid & 63u;
   const uint32_t wave = tid >> 6;
-  if (row_skipped(rp, row)) {  // decode loop: the row has ended or has no room
-    if (tid == 0) skip_row(rp, row);
-    return;
-  }
-  uint32_t len = 0;
-  if (rp.hist != nullptr && rp.hist_len != nullptr) {
-    len = row_word(rp.hist_len + row);
-    if ((size_t)len > rp.hist_ld) len = (uint32_t)rp.hist_ld;
-  }
   const uint32_t* lrow = p.logits + (size_t)row * p.logits_ld;
   const uint32_t* tm = p.tilemax + (size_t)row * kTilesPerRow;
   const bool tile_wave = wave < kTileWaves;
 
-  // tile waves: their tile words (tile lane + 64 (10 w + j) in words[j], 0
-  // past the last tile), requested first; wave 0 also the uniform
-  uint32_t r24 = 0;
+  // The loads that need only the kernel's arguments go out first, before the
+  // row's state and length are read (each of those is a memory round trip
+  // that the compiler would otherwise wait for first); a row that turns out
+  // to be skipped leaves with them in flight.
+  //
+  // Tile waves: their tile words (tile lane + 64 (10 w + j) in words[j], 0
+  // past the last tile).  The loads are unconditional (the index is clamped
+  // to the last tile, the second words read the tile words again when the
+  // GEMM wrote none); lanes past the last tile and missing second words are
+  // masked after the first barrier, where the values are used.
   uint32_t thr_first = 0;  // the first round's threshold word (tile waves)
   uint32_t words[kWaveKeys];
   uint32_t secs[kWaveKeys];  // their second words, when the GEMM wrote them
   const bool has_sec = p.tilesec != nullptr;
   if (tile_wave) {
-    if (wave == 0) r24 = rp.random_24[row];
-    const uint32_t* ts = p.tilesec + (size_t)row * kTilesPerRow;
+    const uint32_t* ts = has_sec ? p.tilesec + (size_t)row * kTilesPerRow : tm;
 #pragma unroll
     for (int j = 0; j < kWaveKeys; ++j) {
       const uint32_t t = lane + 64u * (wave * (uint32_t)kWaveKeys + (uint32_t)j);
-      words[j] = t < kTilesPerRow ? tm[t] : 0u;
-      secs[j] = has_sec && t < kTilesPerRow ? ts[t] : ~0u;
+      words[j] = tm[min(t, kTilesPerRow - 1u)];
+      secs[j] = ts[min(t, kTilesPerRow - 1u)];
     }
   }
-  // history waves: the first four uint4 (or eight words) of each thread
+  // History threads: each requests its first uint4 (or word) of the row,
+  // clamped to the row's capacity (hist_ld ids are readable per row); the
+  // other three (seven) follow once the length shows that the row needs
+  // them.
   const uint32_t ht = tid - 64u * kTileWaves;
   constexpr uint32_t kHistThreads = 64u * kHistWaves;
-  const uint32_t* hrow = len != 0 ? rp.hist + (size_t)row * rp.hist_ld : nullptr;
+  const bool has_hist = rp.hist != nullptr && rp.hist_len != nullptr && rp.hist_ld != 0;
+  const uint32_t* hbase = has_hist ? rp.hist + (size_t)row * rp.hist_ld : nullptr;
+  v4u hv[4] = {};
+  uint32_t hs[8] = {};
+  if (!tile_wave && has_hist) {
+    if (rp.hist_vec4)
+      hv[0] = reinterpret_cast<const v4u*>(hbase)[min(ht, (uint32_t)(rp.hist_ld / 4u) - 1u)];
+    else
+      hs[0] = hbase[min(ht, (uint32_t)min(rp.hist_ld, (size_t)kHistThreads) - 1u)];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  if (row_skipped(rp, row)) {  // decode loop: the row has ended or has no room
+    if (tid == 0) skip_row(rp, row);
+    return;
+  }
+  uint32_t len = 0;
+  if (has_hist) {
+    len = row_word(rp.hist_len + row);
+    if ((size_t)len > rp.hist_ld) len = (uint32_t)rp.hist_ld;
+  }
+  // The row's uniform, which wave 0 uses to finish the row, through the
+  // scalar cache: a vector load of this wave-uniform word is moved to a
+  // scalar register at once, which waits for it.
+  const uint32_t r24 = row_word(rp.random_24 + row);
+  const uint32_t* hrow = len != 0 ? hbase : nullptr;
   const v4u* h4 = reinterpret_cast<const v4u*>(hrow);
   const uint32_t n4 = (len + 3u) / 4u;
-  v4u hv[4];
-  uint32_t hs[8];
   auto load_hist = [&](uint32_t k0) {
     if (rp.hist_vec4) {
 #pragma unroll
@@ -1188,7 +1211,15 @@ __global__ __launch_bounds__(kSelectThreads) void lm_select_kernel(LmParams p, R
       for (uint32_t u = 0; u < 8; ++u) hs[u] = hrow[min(k0 + u * kHistThreads, len - 1u)];
     }
   };
-  if (!tile_wave && ht < (rp.hist_vec4 ? n4 : len)) load_hist(ht);
+  if (!tile_wave && uniform(rp.hist_vec4 ? n4 : len) > kHistThreads) {
+    if (rp.hist_vec4) {
+#pragma unroll
+      for (uint32_t u = 1; u < 4; ++u) hv[u] = h4[min(ht + u * kHistThreads, n4 - 1u)];
+    } else {
+#pragma unroll
+      for (uint32_t u = 1; u < 8; ++u) hs[u] = hrow[min(ht + u * kHistThreads, len - 1u)];
+    }
+  }
 
   static_assert(kWordsPerRow % 4 == 0, "the bitmap is cleared 16 bytes at a time");
   for (uint32_t i = tid; i < kWordsPerRow / 4; i += kSelectThreads)
@@ -1203,6 +1234,12 @@ __global__ __launch_bounds__(kSelectThreads) void lm_select_kernel(LmParams p, R
   __syncthreads();  // (1) the bitmap is clear
 
   if (tile_wave) {
+#pragma unroll
+    for (int j = 0; j < kWaveKeys; ++j) {
+      const uint32_t t = lane + 64u * (wave * (uint32_t)kWaveKeys + (uint32_t)j);
+      if (t >= kTilesPerRow) words[j] = 0u;
+      if (t >= kTilesPerRow || !has_sec) secs[j] = ~0u;
+    }
     // the lane's best word, and the wave's lowest tile flagged non-finite
     uint32_t lbw = 0;
 #pragma unroll
