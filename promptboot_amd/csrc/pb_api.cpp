@@ -69,22 +69,24 @@ struct pb_context {
   size_t lm_bytes = 0;
 
   // Single-row staging: one input region, pinned on the host and mirrored on
-  // the device ([history length, uniform, -, -][row][history ids]), and one
+  // the device ([row][history length, uniform, -, -][history ids]), and one
   // output region ([token, -, -, -][error record][detail][penalised history
-  // values]), so that a call makes one copy each way.  The pointers below
-  // point into them; `seen` has its own pair, copied only when non-zero.
+  // values]).  The pinned regions are coherent and mapped (z_in, z_out are
+  // their device addresses): a call reads the input region from the host in
+  // its first launch, which leaves a copy in d_in, and its kernels write the
+  // outputs straight into h_out.  Calls with a non-zero `seen` copy the
+  // regions instead, one copy each way.  The pointers below point into them;
+  // `seen` has its own pair, copied only when non-zero.
   size_t hist_cap = 0;
   uint8_t* d_in = nullptr;
   uint8_t* h_in = nullptr;
   uint8_t* d_out = nullptr;
   uint8_t* h_out = nullptr;
+  uint8_t* z_in = nullptr;
+  uint8_t* z_out = nullptr;
   uint32_t* d_small = nullptr;  // [0] history length, [1] uniform
   uint32_t* d_row = nullptr;
   uint32_t* d_hist = nullptr;
-  uint32_t* d_token = nullptr;
-  pb_inference_error* d_err = nullptr;
-  pb_sample_detail* d_detail = nullptr;
-  uint32_t* d_gather = nullptr;
   uint32_t* h_small = nullptr;
   uint32_t* h_row = nullptr;
   uint32_t* h_hist = nullptr;
@@ -96,15 +98,17 @@ struct pb_context {
   uint8_t* h_seen = nullptr;
 };
 
-// Offsets inside the staging regions.  The row starts 16 bytes in, so it
-// keeps the 16-byte alignment of the float4 loads, and so does the history.
-constexpr size_t kInRow = 16;
-constexpr size_t kInHist = kInRow + kRowBytes;
+// Offsets inside the staging regions.  The row comes first, 16-byte aligned
+// for the float4 loads; the scalars and the history ids follow it, so that
+// they are one 16-byte aligned range.
+constexpr size_t kInRow = 0;
+constexpr size_t kInSmall = kRowBytes;
+constexpr size_t kInHist = kInSmall + 16;
 constexpr size_t kOutErr = 16;
 constexpr size_t kOutDetail = 64;
 constexpr size_t kOutGather = (kOutDetail + sizeof(pb_sample_detail) + 15) / 16 * 16;
 static_assert(kOutErr + sizeof(pb_inference_error) <= kOutDetail, "error record overlaps");
-static_assert(kInHist % 16 == 0, "history ids must stay 16-byte aligned");
+static_assert(kInSmall % 16 == 0 && kInHist % 16 == 0, "history ids must stay 16-byte aligned");
 
 // Grows a device workspace to `bytes` (never shrinks it).  Only set-up calls
 // (pb_context_create, pb_context_reserve) use it: hipFree waits for the
@@ -180,9 +184,14 @@ static void free_staging(pb_context* ctx) {
   if (ctx->d_out) (void)hipFree(ctx->d_out);
   if (ctx->h_in) (void)hipHostFree(ctx->h_in);
   if (ctx->h_out) (void)hipHostFree(ctx->h_out);
-  ctx->d_in = ctx->d_out = ctx->h_in = ctx->h_out = nullptr;
+  ctx->d_in = ctx->d_out = ctx->h_in = ctx->h_out = ctx->z_in = ctx->z_out = nullptr;
   ctx->hist_cap = 0;
 }
+
+// Pinned staging that kernels read and write in place: coherent, so that no
+// GPU cache holds a previous call's bytes and the host sees a kernel's
+// stores once the stream has synchronised.
+constexpr unsigned kMappedFlags = hipHostMallocMapped | hipHostMallocCoherent;
 
 // Staging regions for histories of up to `ids` ids.  The drop-ins hold the
 // context's lock and synchronise before they return, so no copy or launch
@@ -196,20 +205,20 @@ static hipError_t ensure_staging(pb_context* ctx, size_t ids) {
   hipError_t e;
   if ((e = hipMalloc(&ctx->d_in, in_bytes)) != hipSuccess ||
       (e = hipMalloc(&ctx->d_out, out_bytes)) != hipSuccess ||
-      (e = hipHostMalloc(&ctx->h_in, in_bytes, hipHostMallocDefault)) != hipSuccess ||
-      (e = hipHostMalloc(&ctx->h_out, out_bytes, hipHostMallocDefault)) != hipSuccess) {
+      (e = hipHostMalloc(&ctx->h_in, in_bytes, kMappedFlags)) != hipSuccess ||
+      (e = hipHostMalloc(&ctx->h_out, out_bytes, kMappedFlags)) != hipSuccess ||
+      (e = hipHostGetDevicePointer(reinterpret_cast<void**>(&ctx->z_in), ctx->h_in, 0)) !=
+          hipSuccess ||
+      (e = hipHostGetDevicePointer(reinterpret_cast<void**>(&ctx->z_out), ctx->h_out, 0)) !=
+          hipSuccess) {
     free_staging(ctx);
     return e;
   }
   ctx->hist_cap = cap;
-  ctx->d_small = reinterpret_cast<uint32_t*>(ctx->d_in);
+  ctx->d_small = reinterpret_cast<uint32_t*>(ctx->d_in + kInSmall);
   ctx->d_row = reinterpret_cast<uint32_t*>(ctx->d_in + kInRow);
   ctx->d_hist = reinterpret_cast<uint32_t*>(ctx->d_in + kInHist);
-  ctx->d_token = reinterpret_cast<uint32_t*>(ctx->d_out);
-  ctx->d_err = reinterpret_cast<pb_inference_error*>(ctx->d_out + kOutErr);
-  ctx->d_detail = reinterpret_cast<pb_sample_detail*>(ctx->d_out + kOutDetail);
-  ctx->d_gather = reinterpret_cast<uint32_t*>(ctx->d_out + kOutGather);
-  ctx->h_small = reinterpret_cast<uint32_t*>(ctx->h_in);
+  ctx->h_small = reinterpret_cast<uint32_t*>(ctx->h_in + kInSmall);
   ctx->h_row = reinterpret_cast<uint32_t*>(ctx->h_in + kInRow);
   ctx->h_hist = reinterpret_cast<uint32_t*>(ctx->h_in + kInHist);
   ctx->h_token = reinterpret_cast<uint32_t*>(ctx->h_out);
@@ -371,6 +380,18 @@ static bool decode_args_ok(const DecodeArgs& dec, pb_inference_error* err) {
 // Validates and enqueues one batched sample (every variant) with the slice
 // workspace `work` of `work_bytes` bytes.  Never allocates: a plan that
 // needs more workspace than that is refused with PB_CAPACITY.
+// A single-row drop-in's inputs still in mapped pinned memory: the tile-words
+// launch reads the row at `row` and stores it at d_logits, and copies v4
+// 16-byte groups from src to dst (the scalars and the history ids); the
+// select kernel writes the history's penalised logits to `gather`.
+struct StagedInput {
+  const uint32_t* row;
+  const uint32_t* src;
+  uint32_t* dst;
+  uint32_t v4;
+  uint32_t* gather;  // the penalised logits at the history ids (the write-back), or null
+};
+
 static uint32_t enqueue_sample_in(int device, uint32_t forced_segments, void* work,
                                   size_t work_bytes, const uint32_t* d_logits, size_t vocab,
                                   size_t ld, uint32_t rows, const uint32_t* d_hist,
@@ -378,7 +399,8 @@ static uint32_t enqueue_sample_in(int device, uint32_t forced_segments, void* wo
                                   const uint32_t* d_random_24, const uint8_t* d_excl,
                                   uint32_t* d_token, pb_sample_detail* d_detail,
                                   pb_inference_error* d_err, hipStream_t stream,
-                                  pb_inference_error* err, const DecodeArgs* dec = nullptr) {
+                                  pb_inference_error* err, const DecodeArgs* dec = nullptr,
+                                  const StagedInput* staged = nullptr) {
   clear_error(err);
   if (vocab != PB_VOCAB) {
     // logits_error (inference.rs:737-754)
@@ -426,10 +448,22 @@ static uint32_t enqueue_sample_in(int device, uint32_t forced_segments, void* wo
     lp.rows = rows;
     lp.tilemax = static_cast<uint32_t*>(work);
     lp.tilesec = lp.tilemax + (size_t)rows * (PB_VOCAB / 64);
+    if (staged) {
+      lp.logits = const_cast<uint32_t*>(staged->row);  // read only
+      lp.logits_copy = const_cast<uint32_t*>(d_logits);
+      lp.stage_src = staged->src;
+      lp.stage_dst = staged->dst;
+      lp.stage_v4 = staged->v4;
+      p.gather = staged->gather;
+    }
     p.segs = 1;
     DeviceGuard guard(device);
     hipError_t e = pb::launch_tile_select(lp, p, stream);
     return e == hipSuccess ? PB_OK : device_error(err, e);
+  }
+  if (staged) {  // only the tile selection copies staged inputs
+    set_error(err, PB_STATE, PB_DOMAIN_NONE, 2, 0, PB_FIELD_NONE, 0);
+    return PB_STATE;
   }
   pb::plan_segments(rows, forced_segments, &p.segs, &p.seg_f4);
   p.part_keys = nullptr;
@@ -466,7 +500,8 @@ static uint32_t enqueue_sample(pb_context* ctx, const uint32_t* d_logits, size_t
                                pb_sample_detail* d_detail, pb_inference_error* d_err,
                                hipStream_t stream, pb_inference_error* err,
                                const DecodeArgs* dec = nullptr, bool locked = false,
-                               const Workspace* ws = nullptr) {
+                               const Workspace* ws = nullptr,
+                               const StagedInput* staged = nullptr) {
   uint32_t st = enqueue_sample_in(-1, 0, nullptr, 0, d_logits, vocab, ld, 0, d_hist, hist_ld,
                                   d_hist_len, d_random_24, d_excl, d_token, d_detail, d_err,
                                   stream, err, dec);
@@ -486,7 +521,7 @@ static uint32_t enqueue_sample(pb_context* ctx, const uint32_t* d_logits, size_t
   const size_t work_bytes = ws ? ws->bytes : ctx->list_bytes;
   return enqueue_sample_in(ctx->device, ctx->forced_segments, work, work_bytes, d_logits, vocab,
                            ld, rows, d_hist, hist_ld, d_hist_len, d_random_24, d_excl, d_token,
-                           d_detail, d_err, stream, err, dec);
+                           d_detail, d_err, stream, err, dec, staged);
 }
 
 namespace pb {
@@ -647,7 +682,7 @@ static uint32_t enqueue_lmhead(pb_context* ctx, const uint8_t* d_packed, size_t 
   }
   DeviceGuard guard(ctx->device);
   char* base = static_cast<char*>(ctx->d_lm);
-  pb::LmParams p;
+  pb::LmParams p{};
   p.weights = d_packed;
   p.q8 = q8;
   p.hidden = d_hidden;
@@ -809,9 +844,15 @@ enum RowMode { kSample = 0, kSampleWithHistory = 1 };
 // Runs one row through the batched kernels on the context's own stream.
 // Fills *ctx->h_token, ctx->h_detail and ctx->h_err; when `history` is
 // non-null also the penalised write-back values in h_gather and, with
-// `seen_dirty`, the updated scratch in h_seen.  The scalars, the row and the
-// history go up in one copy and the results come back in one: each copy on
-// the stream costs several microseconds of latency, more than its bytes.
+// `seen_dirty`, the updated scratch in h_seen.  Each copy on the stream costs
+// several microseconds of latency, more than its bytes: without a dirty
+// `seen` (and with the automatic plan) the call makes none and launches
+// twice.  The tile-words launch reads the staged row, scalars and history
+// from the mapped pinned region and leaves them in d_in; the select launch
+// writes the token, records and the penalised history values into the mapped
+// output region.  Otherwise the scalars, the row and the history go up in one
+// copy, a write-back launch follows the selection and the results come back
+// in one copy.
 static uint32_t run_single_row(pb_context* ctx, const uint32_t* logits, const uint32_t* history,
                                size_t history_len, const uint8_t* seen, bool seen_dirty,
                                uint32_t random_24, pb_inference_error* err) {
@@ -821,14 +862,24 @@ static uint32_t run_single_row(pb_context* ctx, const uint32_t* logits, const ui
   const bool with_hist = history != nullptr && history_len > 0;
   if (with_hist && (e = ensure_staging(ctx, history_len)) != hipSuccess)
     return device_error(err, e);
+  const bool mapped = !(with_hist && seen_dirty) && ctx->forced_segments == 0;
   ctx->h_small[0] = (uint32_t)history_len;
   ctx->h_small[1] = random_24;
   memcpy(ctx->h_row, logits, kRowBytes);
   if (with_hist) memcpy(ctx->h_hist, history, history_len * 4);
-  const size_t in_bytes = kInHist + (with_hist ? history_len * 4 : 0);
-  if ((e = hipMemcpyAsync(ctx->d_in, ctx->h_in, in_bytes, hipMemcpyHostToDevice, s)) !=
-      hipSuccess)
-    return device_error(err, e);
+  StagedInput staged{};
+  if (mapped) {
+    staged.row = reinterpret_cast<const uint32_t*>(ctx->z_in + kInRow);
+    staged.src = reinterpret_cast<const uint32_t*>(ctx->z_in + kInSmall);
+    staged.dst = ctx->d_small;
+    staged.v4 = (uint32_t)((kInHist - kInSmall + (with_hist ? history_len * 4 : 0) + 15) / 16);
+    staged.gather = with_hist ? reinterpret_cast<uint32_t*>(ctx->z_out + kOutGather) : nullptr;
+  } else {
+    const size_t in_bytes = kInHist + (with_hist ? history_len * 4 : 0);
+    if ((e = hipMemcpyAsync(ctx->d_in, ctx->h_in, in_bytes, hipMemcpyHostToDevice, s)) !=
+        hipSuccess)
+      return device_error(err, e);
+  }
   // Without history ids the scratch is returned as it came, so it stays on the host.
   if (with_hist && seen_dirty) {
     memcpy(ctx->h_seen, seen, PB_SEEN_BYTES);
@@ -837,18 +888,21 @@ static uint32_t run_single_row(pb_context* ctx, const uint32_t* logits, const ui
       return device_error(err, e);
   }
 
+  uint8_t* out = mapped ? ctx->z_out : ctx->d_out;
+  uint32_t* token = reinterpret_cast<uint32_t*>(out);
   uint8_t* seen_dev = with_hist && seen_dirty ? ctx->d_seen : nullptr;
   pb_inference_error enqueue_err;
-  uint32_t st = enqueue_sample(ctx, ctx->d_row, PB_VOCAB, PB_VOCAB, 1,
-                               with_hist ? ctx->d_hist : nullptr, ctx->hist_cap,
-                               with_hist ? ctx->d_small : nullptr, ctx->d_small + 1, seen_dev,
-                               ctx->d_token, ctx->d_detail, ctx->d_err, s, &enqueue_err, nullptr,
-                               true);
+  uint32_t st = enqueue_sample(
+      ctx, ctx->d_row, PB_VOCAB, PB_VOCAB, 1, with_hist ? ctx->d_hist : nullptr, ctx->hist_cap,
+      with_hist ? ctx->d_small : nullptr, ctx->d_small + 1, seen_dev, token,
+      reinterpret_cast<pb_sample_detail*>(out + kOutDetail),
+      reinterpret_cast<pb_inference_error*>(out + kOutErr), s, &enqueue_err, nullptr, true,
+      nullptr, mapped ? &staged : nullptr);
   if (st != PB_OK) {
     if (err) *err = enqueue_err;
     return st;
   }
-  if (with_hist) {
+  if (with_hist && !mapped) {
     pb::WritebackParams w;
     w.logits = ctx->d_row;
     w.ld = PB_VOCAB;
@@ -857,18 +911,20 @@ static uint32_t run_single_row(pb_context* ctx, const uint32_t* logits, const ui
     w.hist_ld = ctx->hist_cap;
     w.hist_len = ctx->d_small;
     w.seen = seen_dev;
-    w.token = ctx->d_token;
-    w.gather = ctx->d_gather;
+    w.token = token;
+    w.gather = reinterpret_cast<uint32_t*>(out + kOutGather);
     if ((e = pb::launch_writeback(w, s)) != hipSuccess) return device_error(err, e);
     if (seen_dirty &&
         (e = hipMemcpyAsync(ctx->h_seen, ctx->d_seen, PB_SEEN_BYTES, hipMemcpyDeviceToHost, s)) !=
             hipSuccess)
       return device_error(err, e);
   }
-  const size_t out_bytes = kOutGather + (with_hist ? history_len * 4 : 0);
-  if ((e = hipMemcpyAsync(ctx->h_out, ctx->d_out, out_bytes, hipMemcpyDeviceToHost, s)) !=
-      hipSuccess)
-    return device_error(err, e);
+  if (!mapped) {
+    const size_t out_bytes = kOutGather + (with_hist ? history_len * 4 : 0);
+    if ((e = hipMemcpyAsync(ctx->h_out, ctx->d_out, out_bytes, hipMemcpyDeviceToHost, s)) !=
+        hipSuccess)
+      return device_error(err, e);
+  }
   if ((e = hipStreamSynchronize(s)) != hipSuccess) return device_error(err, e);
   return PB_OK;
 }

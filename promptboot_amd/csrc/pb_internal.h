@@ -37,6 +37,9 @@ struct RowParams {
   uint32_t* hist_out;
   uint32_t* hist_len_out;
   const uint32_t* max_len; // per-row context cap, or null (hist_ld)
+  // Select kernel only (null otherwise; no `excl`): rows x hist_ld, the
+  // penalised logit at each history id, for q < the row's history length.
+  uint32_t* gather;
 };
 
 struct WritebackParams {
@@ -70,6 +73,14 @@ struct LmParams {
   uint32_t* tilesec;        // rows x 2,374 second words (narrow GEMM only, else null):
                             // a bound above every other logit's order word of the tile
                             // (a multiple of 64) plus the maximum's index in the tile
+  // tile_words_kernel only (null / 0 otherwise): the logits it reads are also
+  // stored at logits_copy (same ld), and stage_v4 16-byte groups are copied
+  // from stage_src to stage_dst on the way, so that logits and small inputs
+  // read from pinned host memory reach the device in the same launch.
+  uint32_t* logits_copy;
+  const uint32_t* stage_src;
+  uint32_t* stage_dst;
+  uint32_t stage_v4;
 };
 
 // Batches up to this size take the narrow GEMM.

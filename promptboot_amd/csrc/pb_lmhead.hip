@@ -1024,7 +1024,11 @@ __device__ __forceinline__ uint32_t collect_range(uint64_t* cand, const uint64_t
 // 4n .. 4n+3 of the tile (one 16-byte load each, read once).  A workgroup
 // takes 64 consecutive tiles of one row, each 16-lane row four of them (tiles
 // g, g + 16, g + 32, g + 48: every load instruction covers 16 whole tiles),
-// all four loads in flight together; the grid's y runs over the rows.
+// all four loads in flight together; the grid's y runs over the rows.  For a
+// single-row drop-in the logits are in mapped pinned host memory: the launch
+// also stores them at logits_copy and copies the staged scalars and history,
+// so that the selection reads device memory (on MI355X the PCIe read of the
+// 608 KB row takes about 15 us, at 128 to 1,024 threads per workgroup alike).
 constexpr uint32_t kTilesPerGroup = 64;
 __global__ __launch_bounds__(256) void tile_words_kernel(LmParams p) {
   const uint32_t n = threadIdx.x & 15u;
@@ -1038,9 +1042,17 @@ __global__ __launch_bounds__(256) void tile_words_kernel(LmParams p) {
     const uint32_t t = min(blockIdx.x * kTilesPerGroup + g + 16u * k, kTilesPerRow - 1u);
     x[k] = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(lrow + t * kTileIds + 4u * n));
   }
+  // the staged inputs beside the logits, spread over the whole grid
+  const uint32_t stride = gridDim.x * gridDim.y * 256u;
+  for (uint32_t i = (blockIdx.y * gridDim.x + blockIdx.x) * 256u + threadIdx.x; i < p.stage_v4;
+       i += stride)
+    reinterpret_cast<v4u*>(p.stage_dst)[i] = reinterpret_cast<const v4u*>(p.stage_src)[i];
 #pragma unroll
   for (uint32_t k = 0; k < 4; ++k) {
     const uint32_t tile = blockIdx.x * kTilesPerGroup + g + 16u * k;
+    if (p.logits_copy != nullptr && tile < kTilesPerRow)
+      *reinterpret_cast<v4u*>(p.logits_copy + (size_t)row * p.logits_ld + tile * kTileIds + 4u * n) =
+          x[k];
     const float y[4] = {f_of(x[k].x), f_of(x[k].y), f_of(x[k].z), f_of(x[k].w)};
     const uint32_t word = row16_max_u32(lane_tile_word(y));
     const uint32_t ow[4] = {order_word(y[0]), order_word(y[1]), order_word(y[2]), order_word(y[3])};
@@ -1519,10 +1531,26 @@ __global__ __launch_bounds__(kSelectThreads) void lm_select_kernel(LmParams p, R
     finalize_row(rp, row, lane < (uint32_t)kTopK ? sorted : 0, kNone, kNone, lane, r24);
     return;
   }
+  // The penalised logits at the history ids, for a caller that applies the
+  // penalty to its own copy of the row when no id is excluded (then every id
+  // is penalised once): written by the waves other than wave 0 once they have
+  // no other work.  They do not depend on the draw; the caller applies them
+  // only when the row succeeded.  Ids out of range are skipped (the row fails).
+  auto gather_history = [&]() {
+    if (rp.gather == nullptr || len == 0) return;
+    uint32_t* out = rp.gather + (size_t)row * rp.hist_ld;
+    for (uint32_t q = tid - 64u; q < len; q += kSelectThreads - 64u) {
+      const uint32_t id = hrow[q];
+      if (id < kVocab) out[q] = penalize_bits(lrow[id]);
+    }
+  };
   if (uniform(round2) != 0u) {
     if (tile_wave) tile_round(uniform(round2_thr));
     __syncthreads();  // (5) the second round's candidates
-    if (wave != 0) return;
+    if (wave != 0) {
+      gather_history();
+      return;
+    }
     const uint32_t elems = uniform(first_elems);
     if (uniform(first_fail) == 0u && elems <= kFirstElems) {
       sorted = key_candidates(elems);
@@ -1530,7 +1558,10 @@ __global__ __launch_bounds__(kSelectThreads) void lm_select_kernel(LmParams p, R
       return;
     }
   }
-  if (wave != 0) return;
+  if (wave != 0) {
+    gather_history();
+    return;
+  }
 
   // ---- wave 0: the general selection, best-first over the 64-bit tile keys ----
   if (lane < (uint32_t)kTopK) top[lane] = 0;
@@ -1762,7 +1793,14 @@ hipError_t launch_tile_select(const LmParams& p, const RowParams& rp, hipStream_
   hipLaunchKernelGGL(tile_words_kernel,
                      dim3((kTilesPerRow + kTilesPerGroup - 1) / kTilesPerGroup, p.rows), dim3(256), 0,
                      stream, p);
-  hipLaunchKernelGGL(lm_select_kernel, dim3(p.rows), dim3(kSelectThreads), 0, stream, p, rp);
+  // logits read from pinned host memory: the selection reads the device copy
+  // the first launch leaves
+  LmParams sp = p;
+  if (p.logits_copy != nullptr) {
+    sp.logits = p.logits_copy;
+    sp.logits_copy = nullptr;
+  }
+  hipLaunchKernelGGL(lm_select_kernel, dim3(p.rows), dim3(kSelectThreads), 0, stream, sp, rp);
   return hipGetLastError();
 }
 

@@ -223,3 +223,27 @@ def test_staging_grows_then_shorter_and_empty_histories():
         assert t == rt and (g == r).all() and (gseen == rseen).all()
         assert gs.state() == rs.state() and gs.draws() == rs.draws()
     assert (gseen == seen0).all()
+
+
+def test_mapped_and_copied_staging_alternate():
+    """Calls with a clear scratch (the row, scalars and history read from the
+    mapped pinned staging, the token, records and penalised values written
+    back into it) alternate with calls whose scratch has bits set (one copy
+    each way and a write-back launch), on histories that grow the staging
+    between them.  Every call matches the oracle."""
+    rng = np.random.default_rng(23)
+    gs, rs = s.SamplingState(5), o.SamplingState(5)
+    for i, n in enumerate((300, 300, 70_000, 70_000, 17, 0, 1, 1)):
+        base = rng.normal(0, 2.5, V).astype(np.float32).view(np.uint32)
+        top = np.argsort(-base.view(np.float32))[:20].astype(np.uint32)
+        hist = np.concatenate([rng.integers(0, V, n).astype(np.uint32), top[:min(n, 20)]])
+        seen0 = np.zeros(s.SEEN_BYTES, np.uint8)
+        if i % 2:
+            for tok in list(top[::3]) + [5]:
+                seen0[tok // 8] |= 1 << (tok % 8)
+        g, r = base.copy(), base.copy()
+        gseen, rseen = seen0.copy(), seen0.copy()
+        t = s.sample_token_with_repetition(g, hist, gseen, gs)
+        _, rt, _ = o.sample_token_with_repetition(r, hist, rseen, rs)
+        assert t == rt and (g == r).all() and (gseen == rseen).all(), (i, n)
+        assert gs.state() == rs.state() and gs.draws() == rs.draws()
