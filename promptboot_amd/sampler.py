@@ -224,7 +224,9 @@ def _words(a) -> np.ndarray:
 
 
 def _ptr(a):
-    return None if a is None else a.ctypes.data_as(vp)
+    # the address as an int (the void* parameters take it): the cheapest of
+    # numpy's routes, about 1 us against 2 us for ctypes.data_as
+    return None if a is None else a.ctypes.data
 
 
 def _check(status: int, err: _Error):
@@ -243,32 +245,32 @@ def sample_token_with_repetition(logits: np.ndarray, tokens, seen: np.ndarray,
     assert logits.dtype == np.uint32 and logits.flags.c_contiguous and logits.flags.writeable
     assert seen.dtype == np.uint8 and seen.flags.c_contiguous
     t = _words(tokens)
-    out = np.zeros(1, np.uint32)
+    out = u32()
     err = _Error()
     st = lib().pb_sample_token_with_repetition(
         _ptr(logits), logits.size, _ptr(t), t.size, _ptr(seen), seen.size,
-        ctypes.byref(state._s), _ptr(out), ctypes.byref(err))
+        ctypes.byref(state._s), ctypes.byref(out), ctypes.byref(err))
     _check(st, err)
-    return int(out[0])
+    return out.value
 
 
 def sample_token(logits, state: SamplingState) -> int:
     row = _words(logits)
-    out = np.zeros(1, np.uint32)
+    out = u32()
     err = _Error()
-    st = lib().pb_sample_token(_ptr(row), row.size, ctypes.byref(state._s), _ptr(out),
+    st = lib().pb_sample_token(_ptr(row), row.size, ctypes.byref(state._s), ctypes.byref(out),
                                ctypes.byref(err))
     _check(st, err)
-    return int(out[0])
+    return out.value
 
 
 def greedy_token(logits) -> int:
     row = _words(logits)
-    out = np.zeros(1, np.uint32)
+    out = u32()
     err = _Error()
-    st = lib().pb_greedy_token(_ptr(row), row.size, _ptr(out), ctypes.byref(err))
+    st = lib().pb_greedy_token(_ptr(row), row.size, ctypes.byref(out), ctypes.byref(err))
     _check(st, err)
-    return int(out[0])
+    return out.value
 
 
 def top_logits_8(logits, output: np.ndarray | None = None) -> np.ndarray:
