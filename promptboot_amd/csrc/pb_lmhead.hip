@@ -1022,22 +1022,23 @@ __device__ __forceinline__ uint32_t collect_range(uint64_t* cand, const uint64_t
 // The same tile and second words as the narrow GEMM writes, from logits in
 // memory: one 16-lane row per (row, 64-id tile), lane n reading ids
 // 4n .. 4n+3 of the tile (one 16-byte load each, read once).  A workgroup
-// takes 64 consecutive tiles of one row, each 16-lane row four of them (tiles
-// g, g + 16, g + 32, g + 48: every load instruction covers 16 whole tiles),
-// all four loads in flight together; the grid's y runs over the rows.  For a
+// takes 16 x kLoads consecutive tiles of one row, each 16-lane row kLoads of
+// them (tiles g, g + 16, ...: every load instruction covers 16 whole tiles),
+// all loads in flight together; the grid's y runs over the rows.  For a
 // single-row drop-in the logits are in mapped pinned host memory: the launch
 // also stores them at logits_copy and copies the staged scalars and history,
 // so that the selection reads device memory (on MI355X the PCIe read of the
 // 608 KB row takes about 15 us, at 128 to 1,024 threads per workgroup alike).
-constexpr uint32_t kTilesPerGroup = 64;
+template <uint32_t kLoads>
 __global__ __launch_bounds__(256) void tile_words_kernel(LmParams p) {
+  constexpr uint32_t kTilesPerGroup = 16u * kLoads;
   const uint32_t n = threadIdx.x & 15u;
   const uint32_t g = threadIdx.x >> 4;
   const uint32_t row = blockIdx.y;
   const uint32_t* lrow = p.logits + (size_t)row * p.logits_ld;
-  v4u x[4];
+  v4u x[kLoads];
 #pragma unroll
-  for (uint32_t k = 0; k < 4; ++k) {
+  for (uint32_t k = 0; k < kLoads; ++k) {
     // past the last tile the row's last tile is read again (and not stored)
     const uint32_t t = min(blockIdx.x * kTilesPerGroup + g + 16u * k, kTilesPerRow - 1u);
     x[k] = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(lrow + t * kTileIds + 4u * n));
@@ -1048,7 +1049,7 @@ __global__ __launch_bounds__(256) void tile_words_kernel(LmParams p) {
        i += stride)
     reinterpret_cast<v4u*>(p.stage_dst)[i] = reinterpret_cast<const v4u*>(p.stage_src)[i];
 #pragma unroll
-  for (uint32_t k = 0; k < 4; ++k) {
+  for (uint32_t k = 0; k < kLoads; ++k) {
     const uint32_t tile = blockIdx.x * kTilesPerGroup + g + 16u * k;
     if (p.logits_copy != nullptr && tile < kTilesPerRow)
       *reinterpret_cast<v4u*>(p.logits_copy + (size_t)row * p.logits_ld + tile * kTileIds + 4u * n) =
@@ -1790,9 +1791,20 @@ hipError_t launch_lm_sample(const LmParams& p, const RowParams& rp, hipStream_t 
 
 hipError_t launch_tile_select(const LmParams& p, const RowParams& rp, hipStream_t stream) {
   (void)hipGetLastError();  // report only this call's launch errors
-  hipLaunchKernelGGL(tile_words_kernel,
-                     dim3((kTilesPerRow + kTilesPerGroup - 1) / kTilesPerGroup, p.rows), dim3(256), 0,
-                     stream, p);
+  // Logits in HBM: two loads per thread, 75 workgroups per row (B = 1, 16,
+  // 64, 192 steps 0.6, 0.6, 0.4, 0.2 us shorter than with four; one load or
+  // eight were slower).  Logits in pinned host memory: four, 38 workgroups.
+  if (p.logits_copy == nullptr) {
+    constexpr uint32_t kGroupTiles = 16u * 2u;
+    hipLaunchKernelGGL(tile_words_kernel<2>,
+                       dim3((kTilesPerRow + kGroupTiles - 1) / kGroupTiles, p.rows), dim3(256), 0,
+                       stream, p);
+  } else {
+    constexpr uint32_t kGroupTiles = 16u * 4u;
+    hipLaunchKernelGGL(tile_words_kernel<4>,
+                       dim3((kTilesPerRow + kGroupTiles - 1) / kGroupTiles, p.rows), dim3(256), 0,
+                       stream, p);
+  }
   // logits read from pinned host memory: the selection reads the device copy
   // the first launch leaves
   LmParams sp = p;
