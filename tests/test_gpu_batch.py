@@ -161,3 +161,32 @@ def test_sample_rows_is_transactional_per_row(sampler):
     assert states[2] == s.SamplingState(int(w["seeds"][2]))
     rtok, _, _, _ = o.sample_batch(w["logits"], w["hist"], w["hist_len"], w["random_24"])
     assert (tok == rtok).all()
+
+
+def test_best_logits_in_the_last_tiles_of_the_row(sampler):
+    """The row's last six 64-id tiles fall in the last tile-words workgroup,
+    whose other lanes read the row's last tile again (clamped) and store
+    nothing.  Rows whose maximum is the last id, whose whole top-20 is the
+    last tile, or whose maximum sits just inside or just before those six
+    tiles: through the batch (logits in HBM) and through the drop-in (logits
+    read from host memory), both bit-exact against the oracle."""
+    w = workloads.make("small", rows=4)
+    lg = w["logits"].view(np.float32)
+    V = lg.shape[1]
+    lg[0, V - 1] = 60.0
+    lg[1, V - 64:V - 44] = 50.0 + np.arange(20, dtype=np.float32)
+    lg[2, V - 6 * 64] = 55.0
+    lg[3, V - 6 * 64 - 1] = 55.0
+    got = run_gpu(sampler, w)
+    want = run_oracle(w)
+    assert_rows_equal(*got, *want)
+    for r in range(4):
+        hist = np.ascontiguousarray(w["hist"][r, :w["hist_len"][r]])
+        g = lg[r].view(np.uint32).copy()
+        ref = g.copy()
+        gseen = np.zeros(s.SEEN_BYTES, np.uint8)
+        rseen = gseen.copy()
+        gs, rs = s.SamplingState(100 + r), o.SamplingState(100 + r)
+        t = s.sample_token_with_repetition(g, hist, gseen, gs)
+        _, rt, _ = o.sample_token_with_repetition(ref, hist, rseen, rs)
+        assert t == rt and (g == ref).all() and not gseen.any(), r
