@@ -225,7 +225,62 @@ def settle(step, per_round: int = 8) -> None:
         hip.synchronize()
 
 
-def time_batch(smp, w: dict, steps: int, warmup: int, stream) -> dict:
+class DevView:
+    """A view of part of a device buffer: shape and dtype over base + offset."""
+
+    def __init__(self, base, offset_bytes: int, shape, dtype=np.uint32):
+        self._ptr = base.data_ptr() + offset_bytes
+        self.shape = tuple(shape)
+        self.dtype = np.dtype(dtype)
+
+    def data_ptr(self) -> int:
+        return self._ptr
+
+
+def cold_pass(smp, bufs: dict, sets: int, steps: int, warmup: int, stream) -> tuple:
+    """The step rotated over `sets` copies of its inputs at different
+    addresses (together larger than MI355X's 256 MB last-level cache), so no
+    step finds its logits or histories in a cache: the reference times each
+    call on a freshly copied logits row (validate_inference.rs:780-794).
+    Returns (HIP-event ms per step, wall seconds for `steps` steps)."""
+    from promptboot_amd import hip
+
+    copies = {}
+    for k in ("logits", "hist", "hl", "r24"):
+        src = bufs[k]
+        big = hip.DeviceArray((sets,) + tuple(src.shape), src.dtype)
+        for i in range(sets):
+            hip.copy_async(big.data_ptr() + i * src.nbytes, src, src.nbytes, hip.D2D, stream)
+        copies[k] = big
+    hip.synchronize()
+    calls = []
+    for i in range(sets):
+        v = {k: DevView(copies[k], i * bufs[k].nbytes, bufs[k].shape, bufs[k].dtype)
+             for k in copies}
+        calls.append(smp.bind_sample(v["logits"], v["r24"], v["hist"], v["hl"],
+                                     token=bufs["token"], stream=stream))
+    at = [0]
+
+    def step():
+        calls[at[0] % sets]()
+        at[0] += 1
+
+    settle(step)
+    for _ in range(warmup):
+        step()
+    kernel_ms = event_pass(step, steps, stream)
+    wall = wall_pass(step, steps)
+    for big in copies.values():
+        big.free()
+    return kernel_ms, wall
+
+
+# Input sets rotated through by the cold passes of the small batches: over
+# 600 MB of logits each, against the 256 MB last-level cache.
+COLD_SETS = {1: 1024, 64: 16}
+
+
+def time_batch(smp, w: dict, steps: int, warmup: int, stream, cold_sets: int = 0) -> dict:
     from promptboot_amd import hip
     from promptboot_amd import sampler as s
     from promptboot_amd import workloads
@@ -251,22 +306,40 @@ def time_batch(smp, w: dict, steps: int, warmup: int, stream) -> dict:
     wall = wall_pass(step, steps)
     ms_per_step = wall / steps * 1e3
     alg = workloads.algorithmic_bytes(w["hist_len"])
-    return {"rows": B, "ms_per_step": ms_per_step, "rows_per_s": B / (ms_per_step / 1e3),
-            "launch_ms": kernel_ms, "alg_bytes": alg,
-            "achieved_gbs": alg / (kernel_ms / 1e3) / 1e9,
-            "segments": int(smp.segments or s.lib().pb_segments_for_rows(B)),
-            "path": ("tile selection" if not smp.segments and B <= s.TILE_SELECT_ROWS
-                     else "slices"),
-            "_tokens": tokens, "_detail": detail}
+    out = {"rows": B, "ms_per_step": ms_per_step, "rows_per_s": B / (ms_per_step / 1e3),
+           "launch_ms": kernel_ms, "alg_bytes": alg,
+           "achieved_gbs": alg / (kernel_ms / 1e3) / 1e9,
+           "segments": int(smp.segments or s.lib().pb_segments_for_rows(B)),
+           "path": ("tile selection" if not smp.segments and B <= s.TILE_SELECT_ROWS
+                    else "slices"),
+           "_tokens": tokens, "_detail": detail}
+    if cold_sets:
+        bufs = dict(logits=logits, hist=hist, hl=hl, r24=r24, token=token)
+        cold_ms, cold_wall = cold_pass(smp, bufs, cold_sets, steps, warmup, stream)
+        assert (token.numpy() == tokens).all()  # every copy draws the same tokens
+        out["cold"] = {"sets": cold_sets,
+                       "set_bytes": int(logits.nbytes + hist.nbytes + hl.nbytes + r24.nbytes),
+                       "ms_per_step": cold_wall / steps * 1e3,
+                       "rows_per_s": B / (cold_wall / steps), "launch_ms": cold_ms,
+                       "achieved_gbs": alg / (cold_ms / 1e3) / 1e9}
+    for a in (logits, hist, hl, r24, token, det):
+        a.free()
+    return out
+
+
+# Plain-read shapes timed for the read ceiling: (entry point, workgroups).
+READ_SHAPES = (("rows", 4096), ("ranges", 32768), ("grid_stride", 2048), ("grid_stride", 4096))
 
 
 def read_ceiling(nbytes: int, stream, steps: int = 20) -> dict:
-    """Read bandwidth of a plain streaming read (pb_device_read_probe:
-    non-temporal 16-byte loads, one contiguous range per workgroup) over a
-    buffer of `nbytes`, in two shapes: 4096 workgroups (the B=4096 launch's
-    grid) and 32,768 (ranges of a few tens of KB, so the workgroups resident
-    at once read a compact window of the buffer).  The faster shape is the
-    ceiling; both are reported."""
+    """Read bandwidth of a plain streaming read of `nbytes` (non-temporal
+    16-byte loads, eight per thread in flight) in the shapes of READ_SHAPES:
+    one contiguous range per workgroup over 4096 workgroups (the B=4096
+    launch's grid) and over 32,768 (ranges of a few tens of KB, so the
+    workgroups resident at once read a compact window of the buffer), and a
+    grid-stride read (pb_device_read_probe_grid_stride: 32 KiB chunks, chunk
+    g + k x workgroups for workgroup g) over 2048 and 4096 workgroups.  The
+    fastest shape is the ceiling; every shape is reported."""
     import ctypes
 
     from promptboot_amd import hip
@@ -277,24 +350,28 @@ def read_ceiling(nbytes: int, stream, steps: int = 20) -> dict:
     out = hip.DeviceArray.zeros(32768, np.uint32)
     h = ctypes.c_void_p(hip.stream_handle(stream))
     shapes = {}
-    for blocks in (4096, 32768):
+    for kind, blocks in READ_SHAPES:
+        fn = (s.lib().pb_device_read_probe_grid_stride if kind == "grid_stride"
+              else s.lib().pb_device_read_probe)
+
         def step():
-            st = s.lib().pb_device_read_probe(ctypes.c_void_p(buf.data_ptr()), words,
-                                              ctypes.c_void_p(out.data_ptr()), blocks, h)
+            st = fn(ctypes.c_void_p(buf.data_ptr()), words, ctypes.c_void_p(out.data_ptr()),
+                    blocks, h)
             assert st == s.OK
 
         settle(step)
-        shapes[blocks] = event_pass(step, steps, stream)
+        shapes[f"{kind}_{blocks}"] = event_pass(step, steps, stream)
     buf.free()
     out.free()
     best = min(shapes, key=shapes.get)
     ms = shapes[best]
     return {"read_gbs": round(words * 4 / (ms / 1e3) / 1e9, 1), "bytes": words * 4,
-            "launch_ms": round(ms, 4), "workgroups": best,
-            "by_workgroups": {str(b): {"launch_ms": round(m, 4),
-                                       "read_gbs": round(words * 4 / (m / 1e3) / 1e9, 1)}
-                              for b, m in shapes.items()},
-            "kernel": "pb::read_probe_kernel (pb_device_read_probe)"}
+            "launch_ms": round(ms, 4), "shape": best,
+            "by_shape": {k: {"launch_ms": round(m, 4),
+                             "read_gbs": round(words * 4 / (m / 1e3) / 1e9, 1)}
+                         for k, m in shapes.items()},
+            "kernel": "pb::read_probe_kernel / pb::read_probe_stride_kernel "
+                      "(pb_device_read_probe, pb_device_read_probe_grid_stride)"}
 
 
 def time_production(stream) -> dict:
@@ -435,7 +512,7 @@ def time_lmhead(smp, steps: int, warmup: int, stream, q8: bool = False, rows: in
     n_check = min(PARITY_LMHEAD_ROWS, B)
     g_logits = logits.numpy()[:n_check].copy()
     g_tokens = token.numpy()[:n_check].copy()
-    g_flags = det.numpy().view(s.DETAIL_DTYPE).reshape(B)["flags"][:n_check].copy()
+    g_det = det.numpy().view(s.DETAIL_DTYPE).reshape(B)[:n_check].copy()
     logits.free()
     settle(step, 4)
     for _ in range(warmup):
@@ -451,18 +528,14 @@ def time_lmhead(smp, steps: int, warmup: int, stream, q8: bool = False, rows: in
     threads = min(16, len(os.sched_getaffinity(0)))
     r_logits = o.lmhead_logits(w["hidden"][:n_check], head, workloads.VOCAB,
                                workloads.HIDDEN, threads=threads, q8=q8)
-    r_tok, _, _, _ = o.sample_batch(r_logits, w["hist"][:n_check], w["hist_len"][:n_check],
-                                    w["random_24"][:n_check], threads=threads)
+    r_tok, r_det, _, _ = o.sample_batch(r_logits, w["hist"][:n_check], w["hist_len"][:n_check],
+                                        w["random_24"][:n_check], threads=threads)
     rl = r_logits.view(np.float32).astype(np.float64)
     gl = g_logits.view(np.float32).astype(np.float64)
-    boundary = g_flags != 0
     parity = {"rows": n_check,
               "logits_bit_exact": float((g_logits == r_logits).mean()),
               "logits_max_rel_err": float(np.max(np.abs(gl - rl) / np.maximum(np.abs(rl), 1e-30))),
-              "token_agreement": float((g_tokens == r_tok).mean()),
-              "token_agreement_non_boundary": float((g_tokens == r_tok)[~boundary].mean())
-              if (~boundary).any() else None,
-              "boundary_rows": int(boundary.sum())}
+              **agreement(g_tokens, g_det, r_tok, r_det)}
     ops = 2.0 * B * workloads.VOCAB * workloads.HIDDEN
     # VALU ops per (row, id, block).  Q4_0: three IEEE roundings, f32(dot) *
     # w_scale, * a_scale, + total (the conversion folds into the first).  Q8_0:
@@ -496,13 +569,47 @@ def time_lmhead(smp, steps: int, warmup: int, stream, q8: bool = False, rows: in
                          "reference Q4 head")}
 
 
-ADVERSARIAL = ("flat", "ties", "dominant", "half")
+ADVERSARIAL = ("flat", "ties", "dominant", "half", "boundary")
+
+
+def probs_max_rel_err(det, rdet) -> float:
+    """Largest relative difference of the kept survivors' probabilities, device
+    against the oracle, over rows where both succeeded."""
+    keep = np.arange(20)[None, :] < rdet["kept"][:, None]
+    a = det["probs"].astype(np.float64)[keep]
+    b = rdet["probs"].astype(np.float64)[keep]
+    ok = np.isfinite(b)
+    if not ok.any():
+        return 0.0
+    return float(np.max(np.abs(a[ok] - b[ok]) / np.abs(b[ok])))
+
+
+def agreement(tokens, detail, rtok, rdet) -> dict:
+    """Token agreement overall, on rows flagged near a CDF step or near the
+    top-p cutoff (PB_FLAG_DRAW_BOUNDARY / PB_FLAG_CUTOFF_BOUNDARY) and on the
+    others, top-20 set agreement and the probabilities' relative error."""
+    flags = detail["flags"]
+    boundary = flags != 0
+    agree = tokens == rtok
+    return {"token_agreement": float(agree.mean()),
+            "token_agreement_non_boundary": float(agree[~boundary].mean())
+            if (~boundary).any() else None,
+            "token_agreement_boundary": float(agree[boundary].mean()) if boundary.any() else None,
+            "boundary_rows": int(boundary.sum()),
+            "draw_boundary_rows": int(((flags & 1) != 0).sum()),
+            "cutoff_boundary_rows": int(((flags & 2) != 0).sum()),
+            "top20_set_agreement": float((detail["ids"] == rdet["ids"]).all(axis=1).mean()),
+            "probs_bit_exact": bool((detail["probs"].view(np.uint32)
+                                     == rdet["probs"].view(np.uint32)).all()),
+            "probs_max_rel_err": probs_max_rel_err(detail, rdet)}
 
 
 def time_adversarial(smp, steps: int, warmup: int, threads: int, stream) -> dict:
     """The adversarial B=1024 sub-cases (flat logits, ties at the rank-20
-    boundary, one dominant token, a history over half the vocabulary), each
-    timed and checked row by row against the oracle."""
+    boundary, one dominant token, a history over half the vocabulary) and the
+    boundary batch (draws exactly on and one uniform step beside a step of the
+    cumulative distribution, with the top-p cutoff on a prefix), each timed
+    and checked row by row against the oracle."""
     from oracle import oracle as o
     from promptboot_amd import workloads
 
@@ -514,19 +621,14 @@ def time_adversarial(smp, steps: int, warmup: int, threads: int, stream) -> dict
         ceiling = read_ceiling(r["alg_bytes"], stream)
         rtok, rdet, _, _ = o.sample_batch(w["logits"], w["hist"], w["hist_len"],
                                           w["random_24"], threads=threads)
-        boundary = r["_detail"]["flags"] != 0
-        agree = r["_tokens"] == rtok
         out[name] = {"rows": int(len(rtok)), "rows_per_s": round(r["rows_per_s"], 1),
                      "launch_ms": round(r["launch_ms"], 4),
                      "hbm_frac": round(r["achieved_gbs"] / PEAK_HBM_GBS, 4),
                      "read_ceiling_gbs": ceiling["read_gbs"],
+                     "read_ceiling_shape": ceiling["shape"],
                      "frac_of_read_ceiling": round(r["achieved_gbs"] / ceiling["read_gbs"], 4),
                      "segments_per_row": r["segments"],
-                     "token_agreement": float(agree.mean()),
-                     "token_agreement_non_boundary": float(agree[~boundary].mean())
-                     if (~boundary).any() else None,
-                     "boundary_rows": int(boundary.sum()),
-                     "top20_set_agreement": float((r["_detail"]["ids"] == rdet["ids"]).all(axis=1).mean())}
+                     **agreement(r["_tokens"], r["_detail"], rtok, rdet)}
         del w
     return out
 
@@ -695,6 +797,9 @@ def main() -> int:
     ap.add_argument("--no-production", action="store_true",
                     help="skip the reference's own timed case (hello row, seed 0x0123456789abcdef)")
     ap.add_argument("--batches", default="1,64,4096")
+    ap.add_argument("--no-cold", action="store_true",
+                    help="skip the cold passes of B=1 and B=64 (inputs rotated over more "
+                         "than the last-level cache)")
     ap.add_argument("--segments", type=int, default=0,
                     help="force the slices per row (0 = the library's choice)")
     ap.add_argument("--calibration-copy-mib", type=int, default=0,
@@ -754,7 +859,8 @@ def main() -> int:
     results = {}
     for B in batches:
         log(f"timing B={B}")
-        results[B] = time_batch(smp, work[B], args.steps, args.warmup, stream)
+        results[B] = time_batch(smp, work[B], args.steps, args.warmup, stream,
+                                cold_sets=COLD_SETS.get(B, 0) if not args.no_cold else 0)
     main_res = results[head]
     log("timing the read ceiling of the sampler's load pattern")
     ceiling = read_ceiling(main_res["alg_bytes"], stream)
@@ -786,13 +892,8 @@ def main() -> int:
     log("checking tokens against the oracle")
     rtok, rdet, _, _ = o.sample_batch(w["logits"], w["hist"], w["hist_len"], w["random_24"],
                                       threads=threads)
-    boundary = (main_res["_detail"]["flags"] != 0)
-    agree = main_res["_tokens"] == rtok
-    topk_agree = (main_res["_detail"]["ids"] == rdet["ids"]).all(axis=1)
-    parity = {"rows": int(len(rtok)), "token_agreement": float(agree.mean()),
-              "token_agreement_non_boundary": float(agree[~boundary].mean()),
-              "boundary_rows": int(boundary.sum()),
-              "top20_set_agreement": float(topk_agree.mean())}
+    parity = {"rows": int(len(rtok)), **agreement(main_res["_tokens"], main_res["_detail"],
+                                                   rtok, rdet)}
     if cpu is not None:
         n = len(cpu["_tokens"])
         parity["cpu_baseline_tokens_agree"] = bool((cpu["_tokens"] == main_res["_tokens"][:n]).all())
@@ -814,13 +915,28 @@ def main() -> int:
             "frac_of_read_ceiling": round(main_res["achieved_gbs"] / ceiling["read_gbs"], 4)}
     by_batch = {}
     for B, r in results.items():
-        by_batch[str(B)] = {"rows_per_s": round(r["rows_per_s"], 1),
-                            "ms_per_step": round(r["ms_per_step"], 4),
-                            "launch_ms": round(r["launch_ms"], 4),
-                            "achieved_gbs": round(r["achieved_gbs"], 1),
-                            "hbm_frac": round(r["achieved_gbs"] / PEAK_HBM_GBS, 4),
-                            "segments_per_row": r["segments"] if r["path"] == "slices" else None,
-                            "path": r["path"]}
+        # the small batches' figures are their cold passes (inputs rotated over
+        # more than the last-level cache); the same inputs re-read every step
+        # are reported under "warm"
+        c = r.get("cold", r)
+        entry = {"rows_per_s": round(c["rows_per_s"], 1),
+                 "ms_per_step": round(c["ms_per_step"], 4),
+                 "launch_ms": round(c["launch_ms"], 4),
+                 "achieved_gbs": round(c["achieved_gbs"], 1),
+                 "hbm_frac": round(c["achieved_gbs"] / PEAK_HBM_GBS, 4),
+                 "segments_per_row": r["segments"] if r["path"] == "slices" else None,
+                 "path": r["path"]}
+        if "cold" in r:
+            entry["inputs"] = (f"cold: {c['sets']} input sets of {c['set_bytes']} bytes at "
+                               "different addresses in rotation, one per step")
+            entry["warm"] = {"rows_per_s": round(r["rows_per_s"], 1),
+                             "ms_per_step": round(r["ms_per_step"], 4),
+                             "launch_ms": round(r["launch_ms"], 4),
+                             "hbm_frac": round(r["achieved_gbs"] / PEAK_HBM_GBS, 4),
+                             "inputs": "the same inputs every step (cache-resident)"}
+        else:
+            entry["inputs"] = "one input set, larger than the 256 MB last-level cache"
+        by_batch[str(B)] = entry
     out = {
         "metric": METRIC,
         "value": round(main_res["rows_per_s"], 1),

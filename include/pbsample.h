@@ -184,11 +184,14 @@ void pb_context_destroy(pb_context *ctx);
  * the sampler's slice workspace under the context's current slice plan
  * (pb_context_set_segments), and, when cols > 0, the fused LM head's
  * workspace for hidden states of up to `cols` columns (either head format,
- * logits included).  Allocates (and waits for the device) only when the
- * workspace grows; never shrinks it.  Call it at set-up: the batched entry
- * points below never allocate, never wait, and return PB_CAPACITY
- * (needed/available = workspace bytes) when a call needs more than was
- * reserved, so a reserved context's calls can be captured in a HIP graph. */
+ * logits included).  Allocates only when the workspace grows; never shrinks
+ * it.  A workspace it outgrows stays allocated until pb_context_destroy, so
+ * launches already enqueued and HIP graphs captured before the growth keep
+ * valid memory (they keep using the old workspace).  Call it at set-up: the
+ * batched entry points below never allocate, never wait, and return
+ * PB_CAPACITY (needed/available = workspace bytes) when a call needs more
+ * than was reserved, so a reserved context's calls can be captured in a HIP
+ * graph. */
 uint32_t pb_context_reserve(pb_context *ctx, uint32_t rows, size_t cols, pb_inference_error *err);
 
 /* Threading and streams: one context's batched calls share its workspace.
@@ -226,15 +229,17 @@ uint32_t pb_sample_batch(pb_context *ctx, const uint32_t *d_logits, size_t vocab
 
 /* pb_sample_batch without any allocation, for callers that cannot allocate
  * (code under HIP graph capture, tight serving loops, harnesses that forbid
- * hipMalloc).  No counterpart in the reference.  The slice workspace of the
- * multi-slice plan lives in a static device array of 172,032 bytes (1,024
- * row x slice records) per device, held until the process ends, instead of
- * the context's workspace.  The automatic slice plan fits it for every batch
- * size; a slice plan forced on the context (pb_context_set_segments) that
- * needs more is refused with PB_CAPACITY (needed/available = bytes) before
- * anything is enqueued.  Every call on one device shares that device's
- * array: calls that overlap on the device race on it.  The context supplies
- * the device and the slice plan; its own workspace is not used. */
+ * hipMalloc).  No counterpart in the reference.  Its workspace is a static
+ * device array of 3,646,464 bytes per device, held until the process ends,
+ * instead of the context's workspace: the tile words of PB_TILE_SELECT_ROWS
+ * rows, which also hold the slice records of every batch of the automatic
+ * slice plan, so every batch takes the path pb_sample_batch takes.  A slice
+ * plan forced on the context (pb_context_set_segments) that needs more than
+ * the array (over 21,705 row x slice records) is refused with PB_CAPACITY
+ * (needed/available = bytes) before anything is enqueued.  Every context on
+ * one device shares that device's array: calls that overlap on the device,
+ * from any context or stream, race on it.  The context supplies the device
+ * and the slice plan; its own workspace is not used. */
 uint32_t pb_sample_batch_noalloc(pb_context *ctx, const uint32_t *d_logits, size_t vocab,
                                  size_t ld, uint32_t rows, const uint32_t *d_hist,
                                  size_t hist_ld, const uint32_t *d_hist_len,
@@ -436,6 +441,13 @@ uint32_t pb_device_mfma_selftest(int32_t *d_out, void *stream);
  * Timing it gives the read bandwidth the sampler's stream can reach. */
 uint32_t pb_device_read_probe(const uint32_t *d_in, size_t n_words, uint32_t *d_out,
                               uint32_t blocks, void *stream);
+/* The same read in grid-stride order (diagnostic, no reference counterpart):
+ * the buffer is cut into 32 KiB chunks and workgroup g reads chunks g,
+ * g + blocks, ..., so the workgroups resident at once read one compact
+ * window that moves through the buffer (the fastest plain read pattern
+ * measured on MI355X). */
+uint32_t pb_device_read_probe_grid_stride(const uint32_t *d_in, size_t n_words, uint32_t *d_out,
+                                          uint32_t blocks, void *stream);
 
 /* Library version string: "pbsample <version> src:<hash of the sources it was
  * built from> gfx950". */

@@ -10,6 +10,7 @@
 
 #include <map>
 #include <mutex>
+#include <vector>
 
 #include "pb_internal.h"
 #include "pbsample.h"
@@ -67,6 +68,10 @@ struct pb_context {
 
   void* d_lm = nullptr;  // fused LM head workspace
   size_t lm_bytes = 0;
+  // Workspaces that pb_context_reserve outgrew.  A HIP graph captured before
+  // the growth still launches kernels on them, so they stay allocated until
+  // pb_context_destroy.
+  std::vector<void*> retired;
 
   // Single-row staging: one input region, pinned on the host and mirrored on
   // the device ([row][history length, uniform, -, -][history ids]), and one
@@ -111,18 +116,17 @@ static_assert(kOutErr + sizeof(pb_inference_error) <= kOutDetail, "error record 
 static_assert(kInSmall % 16 == 0 && kInHist % 16 == 0, "history ids must stay 16-byte aligned");
 
 // Grows a device workspace to `bytes` (never shrinks it).  Only set-up calls
-// (pb_context_create, pb_context_reserve) use it: hipFree waits for the
-// device, so no launch still reads the old buffer.
-static hipError_t grow_device(void** buf, size_t* have, size_t bytes) {
+// (pb_context_create, pb_context_reserve) use it.  The outgrown buffer is not
+// freed but kept on `retired` until the context is destroyed: launches
+// already enqueued, and HIP graphs captured earlier, keep its address.
+static hipError_t grow_device(void** buf, size_t* have, size_t bytes,
+                              std::vector<void*>* retired) {
   if (bytes <= *have) return hipSuccess;
-  if (*buf) {
-    hipError_t e = hipFree(*buf);
-    *buf = nullptr;
-    *have = 0;
-    if (e != hipSuccess) return e;
-  }
-  hipError_t e = hipMalloc(buf, bytes);
+  void* fresh = nullptr;
+  hipError_t e = hipMalloc(&fresh, bytes);
   if (e != hipSuccess) return e;
+  if (*buf) retired->push_back(*buf);
+  *buf = fresh;
   *have = bytes;
   return hipSuccess;
 }
@@ -236,6 +240,7 @@ static void release(pb_context* ctx) {
   void* dev[] = {ctx->d_work, ctx->d_lm, ctx->d_seen};
   for (void* p : dev)
     if (p) (void)hipFree(p);
+  for (void* p : ctx->retired) (void)hipFree(p);
   if (ctx->h_seen) (void)hipHostFree(ctx->h_seen);
   if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
   delete ctx;
@@ -303,8 +308,17 @@ uint32_t pb_device_wave_selftest(uint32_t* d_out, void* stream) {
 uint32_t pb_device_read_probe(const uint32_t* d_in, size_t n_words, uint32_t* d_out,
                               uint32_t blocks, void* stream) {
   if (((uintptr_t)d_in & 15u) != 0) return PB_ALIGNMENT;
-  return pb::launch_read_probe(d_in, n_words, d_out, blocks, static_cast<hipStream_t>(stream)) ==
-                 hipSuccess
+  return pb::launch_read_probe(d_in, n_words, d_out, blocks, false,
+                               static_cast<hipStream_t>(stream)) == hipSuccess
+             ? PB_OK
+             : PB_DEVICE;
+}
+
+uint32_t pb_device_read_probe_grid_stride(const uint32_t* d_in, size_t n_words, uint32_t* d_out,
+                                          uint32_t blocks, void* stream) {
+  if (((uintptr_t)d_in & 15u) != 0) return PB_ALIGNMENT;
+  return pb::launch_read_probe(d_in, n_words, d_out, blocks, true,
+                               static_cast<hipStream_t>(stream)) == hipSuccess
              ? PB_OK
              : PB_DEVICE;
 }
@@ -323,7 +337,8 @@ uint32_t pb_context_create(int device, pb_context** out) {
   // the automatic plan for any batch
   if (e == hipSuccess) e = ensure_staging(ctx, PB_CONTEXT_IDS);
   if (e == hipSuccess)
-    e = grow_device(&ctx->d_work, &ctx->list_bytes, sample_workspace_bytes(255, 0));
+    e = grow_device(&ctx->d_work, &ctx->list_bytes, sample_workspace_bytes(255, 0),
+                    &ctx->retired);
   // the device address of pb_sample_batch_noalloc's static scratch, once per device
   void* scratch = nullptr;
   if (e == hipSuccess) e = pb::static_scratch_address(device, &scratch);
@@ -346,9 +361,10 @@ uint32_t pb_context_reserve(pb_context* ctx, uint32_t rows, size_t cols, pb_infe
   std::lock_guard<std::mutex> lock(ctx->mu);
   DeviceGuard guard(ctx->device);
   hipError_t e = grow_device(&ctx->d_work, &ctx->list_bytes,
-                             sample_workspace_bytes(rows, ctx->forced_segments));
+                             sample_workspace_bytes(rows, ctx->forced_segments), &ctx->retired);
   if (e == hipSuccess && cols != 0 && rows != 0)
-    e = grow_device(&ctx->d_lm, &ctx->lm_bytes, lm_workspace_bytes(rows, cols, true));
+    e = grow_device(&ctx->d_lm, &ctx->lm_bytes, lm_workspace_bytes(rows, cols, true),
+                    &ctx->retired);
   return e == hipSuccess ? PB_OK : device_error(err, e);
 }
 
@@ -560,12 +576,16 @@ uint32_t pb_sample_batch_inplace(pb_context* ctx, uint32_t* d_logits, size_t voc
                                  pb_sample_detail* d_detail, pb_inference_error* d_err,
                                  void* stream, pb_inference_error* err) {
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (ctx == nullptr)  // the arguments are checked first, then the context is refused
+    return enqueue_sample(nullptr, d_logits, vocab, ld, rows, d_hist, hist_ld, d_hist_len,
+                          d_random_24, d_seen, d_token, d_detail, d_err, s, err);
+  // Both launches go out under one hold of the context's lock: no other
+  // call on this context lands between them.
+  std::lock_guard<std::mutex> lock(ctx->mu);
   uint32_t st = enqueue_sample(ctx, d_logits, vocab, ld, rows, d_hist, hist_ld, d_hist_len,
-                               d_random_24, d_seen, d_token, d_detail, d_err, s, err);
+                               d_random_24, d_seen, d_token, d_detail, d_err, s, err, nullptr,
+                               true);
   if (st != PB_OK || rows == 0 || d_hist_len == nullptr) return st;
-  // Both launches go out under one hold of the lock: no other call on this
-  // context lands between them.  (The sample launch above took and released
-  // it; the write-back uses no context workspace.)
   pb::WritebackParams w;
   w.logits = d_logits;
   w.ld = ld;

@@ -25,6 +25,8 @@ constexpr uint32_t kTemperatureBits = 0x3f333333u;  // 0.7f
 constexpr uint32_t kTopPBits = 0x3f4ccccdu;         // 0.8f
 constexpr uint32_t kPenaltyBits = 0x3f8ccccdu;      // 1.1f
 constexpr uint32_t kTwoPow24Bits = 0x4b800000u;
+// The quiet NaN x86 SSE produces for an invalid operation (inf - inf).
+constexpr uint32_t kX86DefaultNaN = 0xffc00000u;
 
 // Row flags (not part of the reference; reported beside each draw).
 constexpr uint32_t kFlagDrawBoundary = 1u;

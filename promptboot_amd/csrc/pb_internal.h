@@ -115,7 +115,7 @@ hipError_t launch_probe(int which, const uint32_t* in, uint32_t* out, size_t n,
                         hipStream_t stream);
 hipError_t launch_wave_selftest(uint32_t* out, hipStream_t stream);
 hipError_t launch_read_probe(const uint32_t* in, size_t n_words, uint32_t* out, uint32_t blocks,
-                             hipStream_t stream);
+                             bool grid_stride, hipStream_t stream);
 
 // The context's device (pb_api.cpp).
 int context_device(const pb_context* ctx);

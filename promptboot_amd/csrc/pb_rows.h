@@ -126,6 +126,12 @@ __device__ __forceinline__ void finalize_row(const RowParams& p, uint32_t row, u
   if (lane < (uint32_t)kTopK) {
     const float shifted = f_of(vbits) - maximum;
     w = expf_ref(shifted / f_of(kTemperatureBits));
+    // The only NaN here is -inf - -inf (every top-20 value penalised to
+    // -inf): x86 SSE returns its default NaN 0xffc00000 for that invalid
+    // operation and passes it through the divide and expf unchanged, while
+    // the GPU's default NaN is positive.  The weights and probabilities
+    // reported carry the reference's bits.
+    if (w != w) w = f_of(kX86DefaultNaN);
   }
   double running = 0.0, mine = 0.0;
 #pragma unroll
@@ -165,7 +171,9 @@ __device__ __forceinline__ void finalize_row(const RowParams& p, uint32_t row, u
       d->ids[lane] = id;
       d->value_bits[lane] = vbits;
       d->weight_bits[lane] = b_of(w);
-      d->probs[lane] = lane < kept ? (float)((double)w / kept_total) : 0.0f;
+      float prob = lane < kept ? (float)((double)w / kept_total) : 0.0f;
+      if (prob != prob) prob = f_of(kX86DefaultNaN);  // NaN weights: x86's NaN, as above
+      d->probs[lane] = prob;
     }
     if (lane == 0) {
       d->kept = kept;

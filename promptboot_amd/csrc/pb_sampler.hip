@@ -680,14 +680,41 @@ __global__ __launch_bounds__(kBlock) void read_probe_kernel(const v4u* __restric
   if ((threadIdx.x & 63u) == 0) atomicXor(out + blockIdx.x, acc);
 }
 
+// The same loads in grid-stride order: the buffer is cut into chunks of
+// kBlock x kChunkF4 float4 (32 KiB) and workgroup g reads chunks g,
+// g + blocks, g + 2 blocks, ..., so the workgroups resident at once read one
+// compact window of the buffer that moves through it.
+__global__ __launch_bounds__(kBlock) void read_probe_stride_kernel(const v4u* __restrict__ in,
+                                                                   size_t n4, uint32_t* out) {
+  constexpr size_t kChunk = (size_t)kBlock * kChunkF4;
+  uint32_t acc = 0;
+  for (size_t base = (size_t)blockIdx.x * kChunk; base < n4; base += (size_t)gridDim.x * kChunk) {
+    v4u x[kChunkF4];
+#pragma unroll
+    for (int j = 0; j < kChunkF4; ++j) {
+      const size_t f = base + (size_t)j * kBlock + threadIdx.x;
+      x[j] = f < n4 ? __builtin_nontemporal_load(in + f) : v4u{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int j = 0; j < kChunkF4; ++j) acc ^= x[j].x ^ x[j].y ^ x[j].z ^ x[j].w;
+  }
+  acc = wave_min_u32(acc) ^ acc;  // every lane's value reaches the store
+  if ((threadIdx.x & 63u) == 0) atomicXor(out + blockIdx.x, acc);
+}
+
 hipError_t launch_read_probe(const uint32_t* in, size_t n_words, uint32_t* out, uint32_t blocks,
-                             hipStream_t stream) {
+                             bool grid_stride, hipStream_t stream) {
   (void)hipGetLastError();  // report only this call's launch errors
   const size_t n4 = n_words / 4;
   if (n4 == 0 || blocks == 0) return hipSuccess;
-  const size_t per_block = (n4 + blocks - 1) / blocks;
-  hipLaunchKernelGGL(read_probe_kernel, dim3(blocks), dim3(kBlock), 0, stream,
-                     reinterpret_cast<const v4u*>(in), n4, per_block, out);
+  if (grid_stride) {
+    hipLaunchKernelGGL(read_probe_stride_kernel, dim3(blocks), dim3(kBlock), 0, stream,
+                       reinterpret_cast<const v4u*>(in), n4, out);
+  } else {
+    const size_t per_block = (n4 + blocks - 1) / blocks;
+    hipLaunchKernelGGL(read_probe_kernel, dim3(blocks), dim3(kBlock), 0, stream,
+                       reinterpret_cast<const v4u*>(in), n4, per_block, out);
+  }
   return hipGetLastError();
 }
 

@@ -1,16 +1,20 @@
 // pb_static.hip -- pb_sample_batch_noalloc: the batched sampler with its
-// slice workspace in a file-scope device array instead of memory the
-// library allocates.
+// workspace in a file-scope device array instead of memory the library
+// allocates.
 //
-// The multi-slice sampler (segment_kernel + finish_kernel) passes each
-// slice's top-20 keys and first-bad positions from the first launch to the
-// second through a workspace of rows x slices records.  This file keeps one
-// such workspace per device in `scratch`, sized for every batch of the
-// automatic slice plan, so a caller that cannot allocate (code under HIP
-// graph capture, a tight serving loop) can still sample.  No record has to
-// start at zero: segment_kernel writes every record a launch uses before
-// finish_kernel reads it.  Every call on one device shares that device's
-// array, so calls that overlap on the device race on it.
+// The batched sampler passes intermediate results from its first launch to
+// its second through a workspace: for batches of up to PB_TILE_SELECT_ROWS
+// rows the tile words of every (row, 64-id tile) (tile_words_kernel, then
+// lm_select_kernel), for the slice plan rows x slices records of each
+// slice's top-20 keys and first-bad positions (segment_kernel, then
+// finish_kernel).  This file keeps one such workspace per device in
+// `scratch`, sized for the tile words of PB_TILE_SELECT_ROWS rows, which also
+// holds the records of every batch of the automatic slice plan, so a caller
+// that cannot allocate (code under HIP graph capture, a tight serving loop)
+// takes the same paths as pb_sample_batch.  Nothing in it has to start at
+// zero: the first launch writes every word the second reads.  Every call on
+// one device, from any context, shares that device's array, so calls that
+// overlap on the device race on it.
 #include <hip/hip_runtime.h>
 
 #include <mutex>
@@ -20,12 +24,14 @@
 
 namespace {
 
-// (row, slice) records the array holds: the automatic plan cuts a batch of
-// up to 64 rows into at most 1,024 / rows slices, one of up to 255 rows into
-// at most 512 / rows, and from 256 rows on uses one slice per row and no
-// workspace, so 1,024 records cover every batch.  20 keys + 2 words each.
-constexpr size_t kScratchSlots = 1024;
-constexpr size_t kScratchBytes = kScratchSlots * (PB_TOP_K * 8 + 8);  // 172,032 bytes
+// The tile words of PB_TILE_SELECT_ROWS rows: 192 x 2,374 x 8 = 3,646,464
+// bytes.  The automatic slice plan cuts a batch of up to 255 rows into at
+// most 1,024 (row, slice) records of 20 keys + 2 words (172,032 bytes) and
+// from 256 rows on uses one slice per row and no workspace, so the array
+// also holds every batch of the automatic plan; a forced plan may hold up to
+// 21,705 records.
+constexpr size_t kScratchBytes = (size_t)pb::kTileSelectRows * pb::kTileSelectBytesPerRow;
+static_assert(kScratchBytes >= 1024 * (PB_TOP_K * 8 + 8), "the automatic slice plan fits");
 constexpr int kMaxDevices = 64;
 
 std::mutex g_mu;

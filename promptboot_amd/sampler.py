@@ -120,6 +120,7 @@ EXPORTS = {
     "pb_device_penalize_bits": (u32, [vp, vp, size_t, vp]),
     "pb_device_wave_selftest": (u32, [vp, vp]),
     "pb_device_read_probe": (u32, [vp, size_t, vp, u32, vp]),
+    "pb_device_read_probe_grid_stride": (u32, [vp, size_t, vp, u32, vp]),
     "pb_device_mfma_selftest": (u32, [vp, vp]),
     "pb_lmhead_packed_bytes": (size_t, [size_t, size_t]),
     "pb_lmhead_pack_q4_0": (u32, [vp, size_t, size_t, vp, vp, ctypes.POINTER(_Error)]),

@@ -17,6 +17,16 @@ next_24; inference.rs:779-810).  Row r uses seed_r = base_seed + r.
     dominant  B=1024: N(0, 2.5^2) with one id at +40.
     half      B=1024: the `small` logits; each history is a shuffled set of
               V/2 distinct ids (penalty on half the vocabulary).
+    boundary  B=1024: the `small` logits and histories, with rows whose draw
+              lands exactly on, or one 2^-24 step of the uniform beside, a
+              step of the cumulative distribution (the strict `>` of
+              fp32_sse2.rs:1838-1844 decides them), cycling over four kinds:
+              24 ids tied at +40 (kept 16, steps at the integers, the top-p
+              cutoff exactly on the 16th prefix) with a uniform k/16; the
+              same with k/16 +- 2^-24; two ids tied at +40 with a uniform of
+              1/2 (or 1/2 +- 2^-24); an ordinary `small` row.  The uniform of
+              a constructed row is the first next_24 of a seed chosen for it
+              (seed_for_draw), so every row still draws from the repo PRNG.
 
 Generation is numpy with a fixed PCG64 seed, so every machine builds the
 same bytes.
@@ -40,6 +50,29 @@ def next_24_stream(seeds: np.ndarray) -> np.ndarray:
         s ^= s >> np.uint64(27)
         out = (s * np.uint64(0x2545F4914F6CDD1D)) >> np.uint64(40)
     return out.astype(np.uint32)
+
+
+_MUL = 0x2545F4914F6CDD1D
+_MASK64 = (1 << 64) - 1
+
+
+def _undo_xorshift(v: int) -> int:
+    """Inverse of next_24's state step (v ^= v >> 12; v ^= v << 25; v ^= v >> 27)."""
+    v ^= (v >> 27) ^ (v >> 54)
+    v = (v ^ (v << 25) ^ (v << 50)) & _MASK64
+    v ^= (v >> 12) ^ (v >> 24) ^ (v >> 36) ^ (v >> 48) ^ (v >> 60)
+    return v
+
+
+def seed_for_draw(value_24: int, salt: int = 0) -> int:
+    """A seed whose SamplingState's first next_24 is value_24: the scrambled
+    state (s * 0x2545F4914F6CDD1D mod 2^64) must have value_24 in its top 24
+    bits; the multiplier is odd, so s follows, and the state step is undone."""
+    scrambled = ((value_24 & 0xFFFFFF) << 40) | (0x5DEECE66D * (salt + 1) & ((1 << 40) - 1))
+    stepped = scrambled * pow(_MUL, -1, 1 << 64) & _MASK64
+    seed = _undo_xorshift(stepped)
+    assert seed != 0 and seed != 0x9E3779B97F4A7C15
+    return seed
 
 
 def zipf_ids(rng: np.random.Generator, n: int) -> np.ndarray:
@@ -83,6 +116,7 @@ CONFIGS = {
     "ties": dict(rows=1024),
     "dominant": dict(rows=1024),
     "half": dict(rows=1024),
+    "boundary": dict(rows=1024),
 }
 
 
@@ -124,6 +158,24 @@ def make(name: str, rows: int | None = None, seed: int = 20240601, base_seed: in
         lengths = rng.integers(16, 1025, B).astype(np.uint32)
         hist = zipf_history(rng, lengths, 1024)
     seeds = np.uint64(base_seed) + np.arange(B, dtype=np.uint64)
+    if name == "boundary":
+        logits = boosted_normal(rng, B)
+        lengths = rng.integers(16, 1025, B).astype(np.uint32)
+        hist = zipf_history(rng, lengths, 1024)
+        for r in range(B):
+            kind, k = r % 4, (r // 4) % 16
+            if kind == 3:
+                continue
+            tied = rng.choice(np.arange(VOCAB // 2, VOCAB), 24 if kind < 2 else 2, replace=False)
+            logits[r, tied] = np.float32(40.0)
+            hist[r][np.isin(hist[r], tied)] = 1  # the tied ids stay unpenalised
+            if kind == 0:
+                value = k << 20
+            elif kind == 1:
+                value = (k << 20) + (1 if k == 0 or (r // 64) % 2 == 0 else -1)
+            else:
+                value = (1 << 23) + (0, 1, -1)[(r // 4) % 3]
+            seeds[r] = np.uint64(seed_for_draw(value, r))
     return dict(name=name, logits=logits, hist=hist, hist_len=lengths.astype(np.uint32),
                 random_24=next_24_stream(seeds), seeds=seeds)
 

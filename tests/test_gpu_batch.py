@@ -190,3 +190,21 @@ def test_best_logits_in_the_last_tiles_of_the_row(sampler):
         t = s.sample_token_with_repetition(g, hist, gseen, gs)
         _, rt, _ = o.sample_token_with_repetition(ref, hist, rseen, rs)
         assert t == rt and (g == ref).all() and not gseen.any(), r
+
+
+@pytest.mark.parametrize("rows", [1, 64, 192])
+def test_tile_selection_on_padded_rows_and_an_odd_history_stride(sampler, rows):
+    """The tile selection (up to 192 rows) on logits rows padded to ld = V + 4,
+    whose padding holds NaN that must never be read, and on a history matrix
+    whose stride of 1,023 ids is not a multiple of 4 (the scalar history
+    loads), bit-exact against the oracle."""
+    w = workloads.make("small", rows=rows)
+    lg = np.full((rows, V + 4), np.nan, np.float32)
+    lg[:, :V] = w["logits"]
+    hl = np.minimum(w["hist_len"], 1023).astype(np.uint32)
+    hl[0] = 1023
+    padded = dict(logits=lg, hist=np.ascontiguousarray(w["hist"][:, :1023]), hist_len=hl,
+                  random_24=w["random_24"])
+    got = run_gpu(sampler, padded)
+    assert_rows_equal(*got, *run_oracle(padded))
+    assert (got[2]["status"] == 0).all()

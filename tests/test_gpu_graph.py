@@ -33,34 +33,73 @@ def smp():
     b.close()
 
 
-def test_sample_batch_replays(smp):
-    w = workloads.make("small")              # 64 rows: the two-launch slice plan
-    rows = 64
+def capture_sample(smp, w, rows):
     d = hip.DeviceArray.from_numpy
-    logits, hist, hl = d(w["logits"]), d(w["hist"]), d(w["hist_len"])
-    r24 = d(w["random_24"])
-    token = hip.DeviceArray(rows, np.uint32)
-    det = hip.DeviceArray((rows, DW), np.uint32)
-    err = hip.DeviceArray((rows, EW), np.uint32)
+    bufs = dict(logits=d(w["logits"][:rows]), hist=d(w["hist"][:rows]),
+                hl=d(w["hist_len"][:rows]), r24=d(w["random_24"][:rows]),
+                token=hip.DeviceArray(rows, np.uint32), det=hip.DeviceArray((rows, DW), np.uint32),
+                err=hip.DeviceArray((rows, EW), np.uint32))
     stream = hip.Stream()
     graph = hip.Graph(stream)
     graph.begin()
-    smp.sample(logits, r24, hist, hl, token=token, detail=det, err=err, stream=stream)
+    smp.sample(bufs["logits"], bufs["r24"], bufs["hist"], bufs["hl"], token=bufs["token"],
+               detail=bufs["det"], err=bufs["err"], stream=stream)
     graph.end()
+    return graph, stream, bufs
+
+
+def replay_and_check(smp, graph, stream, bufs, w, rows, replay):
+    u = workloads.next_24_stream(np.arange(rows, dtype=np.uint64) * 977 + replay)
+    bufs["r24"].upload(u)
+    graph.launch()
+    stream.synchronize()
+    got = (bufs["token"].numpy(), bufs["det"].numpy().view(s.DETAIL_DTYPE).reshape(rows),
+           bufs["err"].numpy().view(s.ERROR_DTYPE).reshape(rows))
+    want = o.sample_batch(w["logits"][:rows], w["hist"][:rows], w["hist_len"][:rows], u,
+                          threads=16)[:3]
+    assert_rows_equal(*got, *want)
+    # eager work of the library between replays, on the null stream
     other = hip.DeviceArray(rows, np.uint32)
-    for replay in range(4):
-        u = workloads.next_24_stream(np.arange(rows, dtype=np.uint64) * 977 + replay)
-        r24.upload(u)
-        graph.launch()
-        stream.synchronize()
-        got = (token.numpy(), det.numpy().view(s.DETAIL_DTYPE).reshape(rows),
-               err.numpy().view(s.ERROR_DTYPE).reshape(rows))
-        want = o.sample_batch(w["logits"], w["hist"], w["hist_len"], u, threads=16)[:3]
-        assert_rows_equal(*got, *want)
-        # eager work of the library between replays, on the null stream
-        smp.sample(logits, r24, hist, hl, token=other)
-        assert (other.numpy() == got[0]).all()
-    graph.close()
+    smp.sample(bufs["logits"], bufs["r24"], bufs["hist"], bufs["hl"], token=other)
+    assert (other.numpy() == got[0]).all()
+    other.free()
+
+
+# 64 rows take the tile selection (tile words, then the selection); a forced
+# plan of seven slices per row and 200 rows (two slices per row) the slice
+# plan (segment_kernel, then finish_kernel through the slice records)
+@pytest.mark.parametrize("rows,segments", [(64, 0), (64, 7), (200, 0)])
+def test_sample_batch_replays(smp, rows, segments):
+    w = workloads.make("small", rows=rows)
+    smp.set_segments(segments)
+    try:
+        smp.reserve(rows)
+        graph, stream, bufs = capture_sample(smp, w, rows)
+        for replay in range(4):
+            replay_and_check(smp, graph, stream, bufs, w, rows, replay)
+        graph.close()
+    finally:
+        smp.set_segments(0)
+
+
+def test_replays_survive_a_growing_reserve():
+    """A graph captured on a context's slice workspace replays correctly after
+    pb_context_reserve has outgrown that workspace: the old one stays
+    allocated until the context is destroyed."""
+    rows = 16
+    w = workloads.make("small", rows=rows)
+    b = s.BatchSampler(0, segments=5)
+    try:
+        b.reserve(rows)
+        graph, stream, bufs = capture_sample(b, w, rows)
+        replay_and_check(b, graph, stream, bufs, w, rows, 0)
+        b.reserve(64)                    # a larger slice workspace
+        b.reserve(64, workloads.HIDDEN)  # and the LM head's
+        for replay in range(1, 4):
+            replay_and_check(b, graph, stream, bufs, w, rows, replay)
+        graph.close()
+    finally:
+        b.close()
 
 
 def test_lmhead_q8_replays(smp):
