@@ -694,7 +694,13 @@ static uint32_t enqueue_lmhead(pb_context* ctx, const uint8_t* d_packed, size_t 
   }
   const uint32_t rows_pad = (rows + 63u) & ~63u;
   std::lock_guard<std::mutex> lock(ctx->mu);
-  const LmLayout lay = lm_layout(rows, cols, d_logits == nullptr);
+  // Above kNarrowRows rows without a logits buffer the step is one pass: the
+  // wide GEMM writes only the tile and second words, and the selection
+  // recomputes the few tiles it reads from the packed head.  Narrow batches
+  // keep their logits in the workspace (0.6 MB per row against the head's
+  // 76.6 MB) and the selection reads them.
+  const bool one_pass = d_logits == nullptr && rows > pb::kNarrowRows;
+  const LmLayout lay = lm_layout(rows, cols, d_logits == nullptr && !one_pass);
   const size_t need = lay.total;
   if (need > ctx->lm_bytes) {
     set_error(err, PB_CAPACITY, PB_DOMAIN_NONE, need, ctx->lm_bytes, PB_FIELD_BYTES, 6);
@@ -713,8 +719,9 @@ static uint32_t enqueue_lmhead(pb_context* ctx, const uint8_t* d_packed, size_t 
   p.act_q = reinterpret_cast<int8_t*>(base + lay.act_q);
   p.act_s = reinterpret_cast<float*>(base + lay.act_s);
   p.tilemax = reinterpret_cast<uint32_t*>(base + lay.tilemax);
-  p.tilesec = rows <= pb::kNarrowRows ? reinterpret_cast<uint32_t*>(base + lay.tilesec) : nullptr;
-  p.logits = d_logits ? d_logits : reinterpret_cast<uint32_t*>(base + lay.logits);
+  p.tilesec = rows <= pb::kNarrowRows || one_pass ? reinterpret_cast<uint32_t*>(base + lay.tilesec)
+                                                 : nullptr;
+  p.logits = d_logits ? d_logits : one_pass ? nullptr : reinterpret_cast<uint32_t*>(base + lay.logits);
   p.logits_ld = PB_VOCAB;
 
   pb::RowParams rp;

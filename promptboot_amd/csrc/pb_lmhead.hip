@@ -440,6 +440,72 @@ __device__ __forceinline__ void write_tile(const LmParams& p, const float (&tota
   }
 }
 
+// ---- the wide GEMM's tail when the caller keeps no logits (one pass) ----
+// Per (row, 64-id tile) the tile word as write_tile gives it and the second
+// word (kSecondIndexMask), with no logits written: the selection recomputes
+// the few tiles whose second word reaches its threshold from the packed head.
+// A lane takes the largest m and second largest s of its four values
+// (v_max3 / v_med3), and the index c of m (the lowest, among ties); across
+// the 16 lanes the tile word is the largest order word, the maximum's index
+// the lowest 4 n + c among the lanes holding it, and the bound on the other
+// logits the largest of the other lanes' maxima and that lane's s (a tie at
+// the maximum, in a lane or across lanes, makes the bound reach the tile
+// word).  The sign of a zero maximum is not kept: the selection reads a tile
+// whose word is the order word of zero.  Stores through resources over the
+// group's real rows, as write_tile's.
+template <int kRT, int kI>
+__device__ __forceinline__ void write_tile_words(const LmParams& p,
+                                                 const float (&total)[kRT][4][4],
+                                                 uint32_t base_row, uint32_t group_rows,
+                                                 uint32_t lane_row, uint32_t tile, uint32_t n) {
+  constexpr int kSteps = kRT * kI;
+  uint32_t o[kSteps], sw[kSteps], at[kSteps];
+#pragma unroll
+  for (int st = 0; st < kSteps; ++st) {
+    const int rt = st / kI, i = st % kI;
+    const float y0 = total[rt][0][i], y1 = total[rt][1][i], y2 = total[rt][2][i],
+                y3 = total[rt][3][i];
+    const float probe = __builtin_fmaf(
+        y0, 0.0f, __builtin_fmaf(y1, 0.0f, __builtin_fmaf(y2, 0.0f, y3 * 0.0f)));
+    // (the finite case is the only one used: no quietening of NaN operands)
+    float m3, md, lo, m, s2;
+    __asm__("v_max3_f32 %0, %1, %2, %3" : "=v"(m3) : "v"(y0), "v"(y1), "v"(y2));
+    __asm__("v_med3_f32 %0, %1, %2, %3" : "=v"(md) : "v"(y0), "v"(y1), "v"(y2));
+    __asm__("v_min_f32 %0, %1, %2" : "=v"(lo) : "v"(m3), "v"(y3));
+    __asm__("v_max_f32 %0, %1, %2" : "=v"(m) : "v"(m3), "v"(y3));
+    __asm__("v_max_f32 %0, %1, %2" : "=v"(s2) : "v"(md), "v"(lo));
+    uint32_t c = y2 == m ? 2u : 3u;
+    c = y1 == m ? 1u : c;
+    c = y0 == m ? 0u : c;
+    o[st] = probe != probe ? kNonFiniteTile : order_word(m);
+    sw[st] = order_word(s2);
+    at[st] = 4u * n + c;
+  }
+  uint32_t word[kSteps], sec[kSteps];
+#pragma unroll
+  for (int st = 0; st < kSteps; ++st) word[st] = row16_max_u32(o[st]);
+#pragma unroll
+  for (int st = 0; st < kSteps; ++st) {
+    const uint32_t idx = row16_min_u32(o[st] == word[st] ? at[st] : 0xffu);
+    const uint32_t other = row16_max_u32(at[st] == idx ? sw[st] : o[st]);
+    sec[st] = ((other & ~kSecondIndexMask) + 64u) | idx;
+  }
+  if (n != 0u) return;
+  const uint32_t real = p.rows > base_row ? min(p.rows - base_row, group_rows) : 0u;
+  const __amdgpu_buffer_rsrc_t tm = __builtin_amdgcn_make_buffer_rsrc(
+      p.tilemax + (size_t)base_row * kTilesPerRow, (short)0, (int)(real * kTilesPerRow * 4u),
+      kBufferFlags);
+  const __amdgpu_buffer_rsrc_t ts = __builtin_amdgcn_make_buffer_rsrc(
+      p.tilesec + (size_t)base_row * kTilesPerRow, (short)0, (int)(real * kTilesPerRow * 4u),
+      kBufferFlags);
+#pragma unroll
+  for (int st = 0; st < kSteps; ++st) {
+    const uint32_t row = lane_row + 16u * (uint32_t)(st / kI) + (uint32_t)(st % kI);
+    __builtin_amdgcn_raw_buffer_store_b32(word[st], tm, (row * kTilesPerRow + tile) * 4u, 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b32(sec[st], ts, (row * kTilesPerRow + tile) * 4u, 0, 0);
+  }
+}
+
 // ---- the head: int8 MFMA per block + the reference's binary32 epilogue ----
 // Fragment layout of v_mfma_i32_16x16x32_i8 (A and B alike, so only the
 // contraction index has to agree between them): lane l holds row (A) /
@@ -470,7 +536,7 @@ __device__ __forceinline__ void write_tile(const LmParams& p, const float (&tota
 // scales are both fp16 values, so ws * a_scale is exact, with at most 22
 // significant bits.  Folding the conversion into an FMA as above would work,
 // but it needs -M * ws * a_scale per value: one op either way.)
-template <bool kQ8>
+template <bool kQ8, bool kLogits>
 __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(4))) void lm_gemm_kernel(LmParams p) {
   // Dynamic LDS: the activation scales / 16 of every block for the group's
   // 256 rows, then this tile's weight scales and -M * weight scales by block.
@@ -726,7 +792,10 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(4)
     gemm(std::false_type{});
   }
 
-  write_tile<2, 4, false>(p, total, group0, kRowsPerGroup, lrow0 + 4u * q, tile, n);
+  if constexpr (kLogits)
+    write_tile<2, 4, false>(p, total, group0, kRowsPerGroup, lrow0 + 4u * q, tile, n);
+  else
+    write_tile_words<2, 4>(p, total, group0, kRowsPerGroup, lrow0 + 4u * q, tile, n);
 }
 
 // ---- the head for narrow batches (up to 64 rows) ----
@@ -1073,6 +1142,12 @@ __global__ __launch_bounds__(256) void tile_words_kernel(LmParams p) {
 // lowest low bits any element can have with the tile's lowest id
 // (tile_bound): the penalty never raises a value, so the raw maximum bounds
 // the penalised ones.
+// Where the selection takes the logits of the tiles it reads: from the logits
+// the GEMM or tile_words_kernel wrote, or recomputed from the packed Q4_0 or
+// Q8_0 head (the wide GEMM's one-pass mode keeps no logits).
+constexpr int kFromLogits = 0;
+constexpr int kRecomputeQ4 = 1;
+constexpr int kRecomputeQ8 = 2;
 constexpr uint32_t kTileWaves = 4;                      // waves that read the tile words
 constexpr uint32_t kHistWaves = 4;                      // waves that build the history bitmap
 constexpr uint32_t kSelectThreads = 64u * (kTileWaves + kHistWaves);
@@ -1160,8 +1235,15 @@ __device__ __forceinline__ uint64_t tile_bound(uint64_t key) {
 // read.  Error rows: the lowest tile flagged kNonFiniteTile holds the first
 // non-finite logit (NONFINITE_OUTPUT, which takes precedence), else the first
 // history id >= vocab (TOKEN_ID).  The row is finished with finalize_row.
+template <int kSrc>
 __global__ __launch_bounds__(kSelectThreads) void lm_select_kernel(LmParams p, RowParams rp) {
+  constexpr bool kRecompute = kSrc != kFromLogits;
   __shared__ __align__(16) uint32_t bm[kWordsPerRow];
+  // recomputing tiles: the row's Q8_0 activations and scales, and the
+  // recomputed logits of up to kWaveTiles tiles per tile wave
+  __shared__ __align__(16) uint32_t act_row[kRecompute ? kMaxBlocks * 8 : 4];
+  __shared__ float act_sc[kRecompute ? kMaxBlocks : 1];
+  __shared__ uint32_t xbuf[kRecompute ? kTileWaves * kWaveTiles * 64 : 1];
   __shared__ uint32_t tcand[kTileCap];
   __shared__ uint64_t ecand[kElemCap];
   __shared__ uint64_t top[kTopK];
@@ -1178,9 +1260,10 @@ __global__ __launch_bounds__(kSelectThreads) void lm_select_kernel(LmParams p, R
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = tid & 63u;
   const uint32_t wave = tid >> 6;
-  const uint32_t* lrow = p.logits + (size_t)row * p.logits_ld;
+  const uint32_t* lrow = kRecompute ? nullptr : p.logits + (size_t)row * p.logits_ld;
   const uint32_t* tm = p.tilemax + (size_t)row * kTilesPerRow;
   const bool tile_wave = wave < kTileWaves;
+  const uint32_t blocks = p.cols / 32u;
 
   // The loads that need only the kernel's arguments go out first, before the
   // row's state and length are read (each of those is a memory round trip
@@ -1220,6 +1303,15 @@ __global__ __launch_bounds__(kSelectThreads) void lm_select_kernel(LmParams p, R
       hv[0] = reinterpret_cast<const v4u*>(hbase)[min(ht, (uint32_t)(rp.hist_ld / 4u) - 1u)];
     else
       hs[0] = hbase[min(ht, (uint32_t)min(rp.hist_ld, (size_t)kHistThreads) - 1u)];
+  }
+  // recomputing tiles: the row's activations (one word per thread)
+  uint32_t act_word = 0;
+  float act_scale = 0.0f;
+  if constexpr (kRecompute) {
+    if (tid < blocks * 8u)
+      act_word = reinterpret_cast<const uint32_t*>(
+          p.act_q + ((size_t)(tid >> 3) * p.rows_pad + row) * 32u)[tid & 7u];
+    if (tid < blocks) act_scale = p.act_s[(size_t)tid * p.rows_pad + row];
   }
   __builtin_amdgcn_sched_barrier(0);
 
@@ -1268,7 +1360,78 @@ __global__ __launch_bounds__(kSelectThreads) void lm_select_kernel(LmParams p, R
     first_fail = 0;
   }
   if (tid < (uint32_t)kTopK) top[tid] = 0;
-  __syncthreads();  // (1) the bitmap is clear
+  if constexpr (kRecompute) {
+    if (tid < blocks * 8u) act_row[tid] = act_word;
+    if (tid < blocks) act_sc[tid] = act_scale;
+  }
+  __syncthreads();  // (1) the bitmap is clear, the activations staged
+
+  // The lane's logit of `tile` (id 64 tile + lane): read from the logits the
+  // GEMM wrote, or recomputed from the packed head and the staged
+  // activations with the head's arithmetic -- the exact int32 block dots
+  // (v_dot4c_i32_i8 over the nibbles expanded as in the GEMM, so a Q4_0 dot
+  // comes out as 16 dot), then the reference's binary32 epilogue over the
+  // blocks in order: total + mul(mul(f32(dot), w_scale), a_scale) for Q4_0
+  // (a_scale / 16 staged, 16 dot: the same products, scaled by exact powers
+  // of two), total + mul(f32(dot), mul(w_scale, a_scale)) for Q8_0.  The
+  // loads of kBatch blocks are in flight together.  `tile` is wave-uniform.
+  auto tile_logit = [&](uint32_t tile) __attribute__((always_inline)) -> uint32_t {
+    if constexpr (!kRecompute) {
+      return lrow[tile * kTileIds + lane];
+    } else {
+      constexpr bool kQ8 = kSrc == kRecomputeQ8;
+      constexpr uint32_t kTileB = kQ8 ? kTileBytesQ8 : kTileBytes;
+      constexpr uint32_t kWordsB = kQ8 ? 8u : 4u;  // a lane's weight words per block
+      constexpr uint32_t kBatch = kQ8 ? 7u : 14u;
+      const uint32_t last = blocks - 1u;
+      const uint8_t* wt = p.weights + (size_t)tile * kTileB + (kQ8 ? 8u : 4u) * lane;
+      const uint16_t* ws16 =
+          reinterpret_cast<const uint16_t*>(p.weights + (size_t)blocks * kVocab * (kQ8 ? 32 : 16)) +
+          tile * kTileIds + lane;
+      float total = 0.0f;
+      for (uint32_t b0 = 0; b0 < blocks; b0 += kBatch) {
+        uint32_t w[kBatch][kWordsB];
+        uint32_t sc[kBatch];
+#pragma unroll
+        for (uint32_t k = 0; k < kBatch; ++k) {
+          const uint32_t b = min(b0 + k, last);
+          const uint8_t* wb = wt + (size_t)b * kTilesPerRow * kTileB;
+#pragma unroll
+          for (uint32_t q = 0; q < 4; ++q) {
+            if constexpr (kQ8) {
+              const v2u x = *reinterpret_cast<const v2u*>(wb + 512u * q);
+              w[k][2 * q] = x.x;
+              w[k][2 * q + 1] = x.y;
+            } else {
+              w[k][q] = *reinterpret_cast<const uint32_t*>(wb + 256u * q);
+            }
+          }
+          sc[k] = ws16[(size_t)b * kVocab];
+        }
+#pragma unroll
+        for (uint32_t k = 0; k < kBatch; ++k) {
+          const uint32_t b = b0 + k;
+          if (b < blocks) {
+            const v4u a0 = *reinterpret_cast<const v4u*>(&act_row[b * 8u]);
+            const v4u a1 = *reinterpret_cast<const v4u*>(&act_row[b * 8u + 4u]);
+            const uint32_t a[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+            int dot = 0;
+#pragma unroll
+            for (uint32_t q = 0; q < 4; ++q) {
+              const uint32_t lo = kQ8 ? w[k][2 * q] : (w[k][q] << 4) & 0xf0f0f0f0u;
+              const uint32_t hi = kQ8 ? w[k][2 * q + 1] : w[k][q] & 0xf0f0f0f0u;
+              dot = __builtin_amdgcn_sdot4((int)lo, (int)a[2 * q], dot, false);
+              dot = __builtin_amdgcn_sdot4((int)hi, (int)a[2 * q + 1], dot, false);
+            }
+            const float ws = __half2float(__ushort_as_half((unsigned short)sc[k]));
+            const float term = kQ8 ? (float)dot * (ws * act_sc[b]) : ((float)dot * ws) * act_sc[b];
+            total = total + term;
+          }
+        }
+      }
+      return b_of(total);
+    }
+  };
 
   if (tile_wave) {
 #pragma unroll
@@ -1317,7 +1480,8 @@ __global__ __launch_bounds__(kSelectThreads) void lm_select_kernel(LmParams p, R
     for (int j = 0; j < kWaveKeys; ++j) {
       const bool take = words[j] >= thr;
       m |= (take ? 1u : 0u) << j;
-      d |= (take && (secs[j] & ~kSecondIndexMask) <= thr ? 1u : 0u) << j;
+      d |= (take && (secs[j] & ~kSecondIndexMask) <= thr && words[j] != 0x80000000u ? 1u : 0u)
+           << j;
     }
     m &= ~d;
     for (uint64_t mask = __ballot(d != 0); mask != 0; mask = __ballot(d != 0)) {
@@ -1348,10 +1512,20 @@ __global__ __launch_bounds__(kSelectThreads) void lm_select_kernel(LmParams p, R
       // their logits (tile i of the wave is wave-uniform: readlane; past the
       // list the row's tile 0 is read again), then the elements whose raw
       // value reaches thr, as (id, raw bits)
-      const uint32_t tl = lane < ntiles ? wave_tiles[wave][lane] : 0u;
       uint32_t xb[kWaveTiles];
+      if constexpr (!kRecompute) {
+        const uint32_t tl = lane < ntiles ? wave_tiles[wave][lane] : 0u;
 #pragma unroll
-      for (int i = 0; i < (int)kWaveTiles; ++i) xb[i] = lrow[bcast32(tl, (uint32_t)i) * kTileIds + lane];
+        for (int i = 0; i < (int)kWaveTiles; ++i) xb[i] = lrow[bcast32(tl, (uint32_t)i) * kTileIds + lane];
+      } else {
+        // one tile at a time into this wave's part of xbuf, then back into
+        // registers (past ntiles the values are not used)
+        uint32_t* xw = xbuf + wave * kWaveTiles * 64u;
+        for (uint32_t i = 0; i < ntiles; ++i) xw[i * 64u + lane] = tile_logit(uniform(wave_tiles[wave][i]));
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int i = 0; i < (int)kWaveTiles; ++i) xb[i] = xw[(uint32_t)i * 64u + lane];
+      }
       const float floor_value = f_of(key_value_bits((uint64_t)thr << 32));
       uint32_t e = 0;
 #pragma unroll
@@ -1521,15 +1695,16 @@ __global__ __launch_bounds__(kSelectThreads) void lm_select_kernel(LmParams p, R
   if (wave == 0 && action == kError) {
     if (nf != kNone) {
       const uint32_t id = nf * kTileIds + lane;
-      const uint32_t first = (lrow[id] & 0x7f800000u) == 0x7f800000u ? id : kNone;
-      finalize_row(rp, row, 0, wave_min_u32(first), first_bad_hist, lane, r24);
+      const uint32_t x = tile_logit(nf);
+      const uint32_t first = wave_min_u32((x & 0x7f800000u) == 0x7f800000u ? id : kNone);
+      finalize_row(rp, row, 0, first, bcast32(x, first & 63u), first_bad_hist, lane, r24);
     } else {
-      finalize_row(rp, row, 0, kNone, first_bad_hist, lane, r24);
+      finalize_row(rp, row, 0, kNone, 0u, first_bad_hist, lane, r24);
     }
     return;
   }
   if (wave == 0 && action == kDone) {
-    finalize_row(rp, row, lane < (uint32_t)kTopK ? sorted : 0, kNone, kNone, lane, r24);
+    finalize_row(rp, row, lane < (uint32_t)kTopK ? sorted : 0, kNone, 0u, kNone, lane, r24);
     return;
   }
   // The penalised logits at the history ids, for a caller that applies the
@@ -1538,7 +1713,7 @@ __global__ __launch_bounds__(kSelectThreads) void lm_select_kernel(LmParams p, R
   // no other work.  They do not depend on the draw; the caller applies them
   // only when the row succeeded.  Ids out of range are skipped (the row fails).
   auto gather_history = [&]() {
-    if (rp.gather == nullptr || len == 0) return;
+    if (kRecompute || rp.gather == nullptr || len == 0) return;
     uint32_t* out = rp.gather + (size_t)row * rp.hist_ld;
     for (uint32_t q = tid - 64u; q < len; q += kSelectThreads - 64u) {
       const uint32_t id = hrow[q];
@@ -1555,7 +1730,7 @@ __global__ __launch_bounds__(kSelectThreads) void lm_select_kernel(LmParams p, R
     const uint32_t elems = uniform(first_elems);
     if (uniform(first_fail) == 0u && elems <= kFirstElems) {
       sorted = key_candidates(elems);
-      finalize_row(rp, row, lane < (uint32_t)kTopK ? sorted : 0, kNone, kNone, lane, r24);
+      finalize_row(rp, row, lane < (uint32_t)kTopK ? sorted : 0, kNone, 0u, kNone, lane, r24);
       return;
     }
   }
@@ -1616,8 +1791,16 @@ __global__ __launch_bounds__(kSelectThreads) void lm_select_kernel(LmParams p, R
       // a scalar base plus the lane's offset
       const uint32_t tl = tcand[base + (lane < nt ? lane : 0u)];
       uint32_t xb[kChunkTiles];
+      if constexpr (!kRecompute) {
 #pragma unroll
-      for (int i = 0; i < kChunkTiles; ++i) xb[i] = lrow[bcast32(tl, (uint32_t)i) * kTileIds + lane];
+        for (int i = 0; i < kChunkTiles; ++i) xb[i] = lrow[bcast32(tl, (uint32_t)i) * kTileIds + lane];
+      } else {
+        static_assert(kChunkTiles * 64 <= kTileWaves * kWaveTiles * 64, "a pass fits xbuf");
+        for (uint32_t i = 0; i < nt; ++i) xbuf[i * 64u + lane] = tile_logit(uniform(tcand[base + i]));
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int i = 0; i < kChunkTiles; ++i) xb[i] = xbuf[(uint32_t)i * 64u + lane];
+      }
       // history bits of the lane's element of each tile, all requested first
       // (element 64 t + lane sits in bitmap word 2 t + lane / 32, bit lane % 32)
       uint32_t hw[kChunkTiles];
@@ -1652,7 +1835,7 @@ __global__ __launch_bounds__(kSelectThreads) void lm_select_kernel(LmParams p, R
     hi = thr;
   }
   const uint64_t key = top[lane < (uint32_t)kTopK ? lane : 0];
-  finalize_row(rp, row, lane < (uint32_t)kTopK ? key : 0, kNone, kNone, lane, r24);
+  finalize_row(rp, row, lane < (uint32_t)kTopK ? key : 0, kNone, 0u, kNone, lane, r24);
 }
 
 // MFMA layout self-test (one wave): A[i][k] = (7i + 3k) % 17 - 8 and
@@ -1778,14 +1961,33 @@ hipError_t launch_lm_sample(const LmParams& p, const RowParams& rp, hipStream_t 
     }
   } else {
     const dim3 gemm_grid(kTilesPerRow, (p.rows_pad + kRowsPerGroup - 1) / kRowsPerGroup);
-    if (p.q8)
-      hipLaunchKernelGGL(lm_gemm_kernel<true>, gemm_grid, dim3(kGemmThreads),
-                         gemm_lds_bytes(p.cols), stream, p);
-    else
-      hipLaunchKernelGGL(lm_gemm_kernel<false>, gemm_grid, dim3(kGemmThreads),
-                         gemm_lds_bytes(p.cols), stream, p);
+    const size_t lds = gemm_lds_bytes(p.cols);
+    if (p.logits == nullptr) {  // one pass: tile and second words, no logits
+      if (p.q8)
+        hipLaunchKernelGGL((lm_gemm_kernel<true, false>), gemm_grid, dim3(kGemmThreads), lds,
+                           stream, p);
+      else
+        hipLaunchKernelGGL((lm_gemm_kernel<false, false>), gemm_grid, dim3(kGemmThreads), lds,
+                           stream, p);
+    } else if (p.q8) {
+      hipLaunchKernelGGL((lm_gemm_kernel<true, true>), gemm_grid, dim3(kGemmThreads), lds, stream,
+                         p);
+    } else {
+      hipLaunchKernelGGL((lm_gemm_kernel<false, true>), gemm_grid, dim3(kGemmThreads), lds,
+                         stream, p);
+    }
   }
-  hipLaunchKernelGGL(lm_select_kernel, dim3(p.rows), dim3(kSelectThreads), 0, stream, p, rp);
+  if (p.logits == nullptr) {  // one pass: no logits kept, the selection recomputes tiles
+    if (p.q8)
+      hipLaunchKernelGGL(lm_select_kernel<kRecomputeQ8>, dim3(p.rows), dim3(kSelectThreads), 0,
+                         stream, p, rp);
+    else
+      hipLaunchKernelGGL(lm_select_kernel<kRecomputeQ4>, dim3(p.rows), dim3(kSelectThreads), 0,
+                         stream, p, rp);
+  } else {
+    hipLaunchKernelGGL(lm_select_kernel<kFromLogits>, dim3(p.rows), dim3(kSelectThreads), 0,
+                       stream, p, rp);
+  }
   return hipGetLastError();
 }
 
@@ -1812,7 +2014,8 @@ hipError_t launch_tile_select(const LmParams& p, const RowParams& rp, hipStream_
     sp.logits = p.logits_copy;
     sp.logits_copy = nullptr;
   }
-  hipLaunchKernelGGL(lm_select_kernel, dim3(p.rows), dim3(kSelectThreads), 0, stream, sp, rp);
+  hipLaunchKernelGGL(lm_select_kernel<kFromLogits>, dim3(p.rows), dim3(kSelectThreads), 0, stream,
+                     sp, rp);
   return hipGetLastError();
 }
 

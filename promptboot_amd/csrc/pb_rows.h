@@ -87,8 +87,11 @@ __device__ __forceinline__ void decode_commit(const RowParams& p, uint32_t row, 
 // fp32_sse2.rs:1818-1845 operation for operation; the binary64 sums run as a
 // lane-serial chain in rank order, so every partial sum is the reference's.
 // `r24` is the row's uniform (random_24[row]), which callers request early.
-__device__ __forceinline__ void finalize_row(const RowParams& p, uint32_t row, uint64_t key, uint32_t bad_logit,
-                             uint32_t bad_hist, uint32_t lane, uint32_t r24) {
+// An error row: bad_logit is the first non-finite index (bad_bits its bits)
+// or kNone, bad_hist the first history position holding an id >= vocab.
+__device__ __forceinline__ void finalize_row(const RowParams& p, uint32_t row, uint64_t key,
+                                             uint32_t bad_logit, uint32_t bad_bits,
+                                             uint32_t bad_hist, uint32_t lane, uint32_t r24) {
   if (bad_logit != kNone || bad_hist != kNone) {
     pb_inference_error e;
     e.layer = PB_NO_LAYER;
@@ -99,7 +102,7 @@ __device__ __forceinline__ void finalize_row(const RowParams& p, uint32_t row, u
     if (bad_logit != kNone) {
       e.status = PB_NONFINITE_OUTPUT;
       e.needed = 0;
-      e.available = p.logits[(size_t)row * p.ld + bad_logit];
+      e.available = bad_bits;
       e.detail = kErrDetailFinite | bad_logit;
     } else {
       e.status = PB_TOKEN_ID;

@@ -465,7 +465,10 @@ __global__ __launch_bounds__(kBlock) void segment_kernel(RowParams p) {
   if (kFinalize) {
     if (wave == 0) {
       const uint64_t key = merge_two_lists(top[0], top[1], lane);
-      finalize_row(p, row, lane < (uint32_t)kTopK ? key : 0, bad_logit, bad_hist, lane, r24);
+      const uint32_t bad_bits =
+          bad_logit != kNone ? p.logits[(size_t)row * p.ld + bad_logit] : 0u;
+      finalize_row(p, row, lane < (uint32_t)kTopK ? key : 0, bad_logit, bad_bits, bad_hist, lane,
+                   r24);
     }
     return;
   }
@@ -521,7 +524,9 @@ __global__ __launch_bounds__(64 * kFinishWaves) void finish_kernel(RowParams p) 
   __builtin_amdgcn_wave_barrier();
   const uint64_t merged = merge_lists_by_threshold(st, p.segs, st + kMaxSegments * kTopK, lane);
   const uint32_t first_bad = wave_min_u32(b);
-  finalize_row(p, row, lane < (uint32_t)kTopK ? merged : 0, first_bad, hist_bad, lane, r24);
+  const uint32_t bad_bits = first_bad != kNone ? p.logits[(size_t)row * p.ld + first_bad] : 0u;
+  finalize_row(p, row, lane < (uint32_t)kTopK ? merged : 0, first_bad, bad_bits, hist_bad, lane,
+               r24);
 }
 
 // In-place penalty for successful rows (fp32_sse2.rs:1848-1876): the first

@@ -1,0 +1,230 @@
+"""The fused LM head in one pass (GPU): above 64 rows, with no logits buffer
+from the caller, the wide GEMM writes only its tile and second words and the
+selection recomputes the few tiles it has to read from the packed head.
+
+Every construction of the two-pass tests is run both ways on the same inputs
+and compared field by field -- token, top-20 ids and values, weights,
+probabilities, kept, rank, flags and the error record, including the bits
+of a non-finite logit -- and against the oracle's head and sampler:
+
+* the standard workload (65, 129 and 300 rows; both head formats);
+* all-zero hidden states (every logit ties: the general selection reads and
+  recomputes tile after tile);
+* error rows (an infinite hidden value makes every logit non-finite, bad
+  history ids) and edge weight and activation scales (NaN and infinite
+  logits in their own tiles);
+* histories of each row's best ids (second rounds and the general path);
+* one tile holding 64 copies of the best row (20 tied ids in one tile);
+* a head whose logits are all negative; the widest hidden state (2,048);
+* 24 identical vocabulary rows with draws exactly on the steps of the
+  cumulative distribution.
+"""
+import numpy as np
+import pytest
+
+from oracle import oracle as o
+from promptboot_amd import sampler as s
+from promptboot_amd import workloads
+from tests.conftest import assert_rows_equal, to_dev
+from tests.test_gpu_boundary import step_uniforms, tied_head
+from tests.test_gpu_lmhead import _set_scales, _top_histories
+
+pytestmark = pytest.mark.gpu
+
+V = s.VOCAB
+HID = workloads.HIDDEN
+
+
+@pytest.fixture(scope="module")
+def smp():
+    b = s.BatchSampler(0)
+    b.reserve(300, 2048)
+    yield b
+    b.close()
+
+
+@pytest.fixture(scope="module")
+def base():
+    return workloads.make_lmhead(rows=300)
+
+
+def pack(smp, head, cols=HID, q8=False):
+    import torch
+
+    packed = smp.pack_lmhead(torch.from_numpy(head).to("cuda:0"), cols=cols, q8=q8)
+    torch.cuda.synchronize()
+    return packed
+
+
+def run(smp, packed, hidden, hist, hl, r24, keep, q8=False):
+    import torch
+
+    B, cols = hidden.shape
+    token = torch.empty(B, dtype=torch.int32, device="cuda:0")
+    det = torch.empty((B, s.DETAIL_DTYPE.itemsize // 4), dtype=torch.int32, device="cuda:0")
+    err = torch.empty((B, s.ERROR_DTYPE.itemsize // 4), dtype=torch.int32, device="cuda:0")
+    logits = torch.empty((B, V), dtype=torch.int32, device="cuda:0") if keep else None
+    smp.lmhead_sample(packed, to_dev(hidden), to_dev(r24), to_dev(hist), to_dev(hl), token=token,
+                      detail=det, err=err, logits=logits, q8=q8, cols=cols)
+    torch.cuda.synchronize()
+    return (token.cpu().numpy().view(np.uint32),
+            det.cpu().numpy().view(s.DETAIL_DTYPE).reshape(B),
+            err.cpu().numpy().view(s.ERROR_DTYPE).reshape(B),
+            logits.cpu().numpy().view(np.uint32) if keep else None)
+
+
+def check(smp, head, hidden, hist, hl, r24, q8=False, nan_rows_ok=False):
+    """One pass against two passes on the device (bit for bit, error records
+    included), and both against the oracle."""
+    cols = hidden.shape[1]
+    packed = pack(smp, head, cols, q8)
+    one = run(smp, packed, hidden, hist, hl, r24, keep=False, q8=q8)
+    two = run(smp, packed, hidden, hist, hl, r24, keep=True, q8=q8)
+    packed.free()
+    assert_rows_equal(*one[:3], *two[:3])
+    rlog = o.lmhead_logits(hidden, head, V, cols, threads=16, q8=q8)
+    glog = two[3]
+    rnan = np.isnan(rlog.view(np.float32))
+    assert (np.isnan(glog.view(np.float32)) == rnan).all()
+    assert (glog[~rnan] == rlog[~rnan]).all()
+    rtok, rdet, rerr, _ = o.sample_batch(rlog, hist, hl, r24, threads=16)
+    if nan_rows_ok:  # a NaN made on the device is not x86's: compare the rest
+        ok = ~(rerr["status"] == s.NONFINITE_OUTPUT)
+        assert (one[2]["status"] == rerr["status"]).all()
+        assert (one[2]["detail"] == rerr["detail"]).all()
+        if ok.any():
+            assert_rows_equal(one[0][ok], one[1][ok], one[2][ok], rtok[ok], rdet[ok], rerr[ok])
+    else:
+        assert_rows_equal(*one[:3], rtok, rdet, rerr)
+    return one, rdet
+
+
+@pytest.mark.parametrize("rows", [65, 129, 300])
+def test_workload_rows(smp, base, rows):
+    w = base
+    check(smp, w["q4"], w["hidden"][:rows], w["hist"][:rows], w["hist_len"][:rows],
+          w["random_24"][:rows])
+
+
+def test_workload_rows_q8(smp, base):
+    rows = 200
+    w = base
+    check(smp, workloads.make_q8_head(), w["hidden"][:rows], w["hist"][:rows],
+          w["hist_len"][:rows], w["random_24"][:rows], q8=True)
+
+
+def test_zero_hidden_states(smp, base):
+    rows = 70
+    w = base
+    check(smp, w["q4"], np.zeros((rows, HID), np.float32), w["hist"][:rows],
+          w["hist_len"][:rows], w["random_24"][:rows])
+
+
+def test_special_scales_put_non_finite_logits_in_every_row(smp, base):
+    """Edge weight scales (signed zeros, fp16 subnormals, +-65504; +-inf and
+    NaN in tiles 100 .. 102) and activation scales that are fp16-subnormal or
+    infinite: every row holds a non-finite logit, so every row takes the
+    error path, which recomputes the first flagged tile to find the index."""
+    w = base
+    rows = 80
+    blocks = HID // 32
+    q4 = w["q4"].reshape(V, blocks, 18).copy()
+    edits = {}
+    for j, bits in enumerate([0x0000, 0x8000, 0x3C00, 0x0001, 0x03FF, 0x7BFF, 0xFBFF]):
+        edits[(64 * (10 + j) + 5 * j + 1, (3 * j) % blocks)] = bits
+    for j, bits in enumerate([0x7C00, 0xFC00, 0x7E00]):
+        edits[(64 * (100 + j) + 7 * j, j)] = bits
+    _set_scales(q4, edits)
+    rng = np.random.default_rng(5)
+    hidden = w["hidden"][:rows].copy()
+    hidden[1::4] *= np.float32(1e-4)                                        # subnormal scales
+    hidden[2::4] = rng.standard_normal((rows // 4, HID)) * np.float32(1e7)  # infinite scales
+    one, _ = check(smp, q4.reshape(-1), hidden, w["hist"][:rows], w["hist_len"][:rows],
+                   w["random_24"][:rows], nan_rows_ok=True)
+    assert (one[2]["status"] == s.NONFINITE_OUTPUT).all()
+
+
+def test_error_rows(smp, base):
+    """An infinite hidden value (every logit of the row non-finite: the
+    first flagged tile is tile 0) and bad history ids, among ordinary rows."""
+    w = base
+    rows = 80
+    hidden = w["hidden"][:rows].copy()
+    hidden[1::8, 100] = np.inf
+    hist = w["hist"][:rows].copy()
+    hist[4::8, 3] = V + 7
+    one, _ = check(smp, w["q4"], hidden, hist, w["hist_len"][:rows], w["random_24"][:rows],
+                   nan_rows_ok=True)
+    assert (one[2]["status"][1::8] == s.NONFINITE_OUTPUT).all()
+    assert (one[2]["status"][4::8] == s.TOKEN_ID).all()
+    assert (one[2]["status"][0::8] == s.OK).all()
+
+
+def test_histories_of_the_best_ids(smp, base):
+    w = base
+    rows = 80
+    hidden = w["hidden"][:rows]
+    rlog = o.lmhead_logits(hidden, w["q4"], V, HID, threads=16)
+    hist, hl = _top_histories(rlog, rows)
+    check(smp, w["q4"], hidden, hist, hl, w["random_24"][:rows])
+
+
+def test_one_tile_holds_the_best_ids(smp, base):
+    w = base
+    rows = 140
+    hidden = w["hidden"][:rows]
+    q4 = w["q4"].reshape(V, HID // 32, 18).copy()
+    rlog0 = o.lmhead_logits(hidden[:1], w["q4"], V, HID, threads=16)
+    best = int(np.argmax(rlog0[0].view(np.float32)))
+    tile = (best // 64 + 1000) % (V // 64)
+    q4[tile * 64:(tile + 1) * 64] = q4[best]
+    _, rdet = check(smp, q4.reshape(-1), hidden, w["hist"][:rows], w["hist_len"][:rows],
+                    w["random_24"][:rows])
+    top = rdet[0]["ids"]
+    assert ((top >= tile * 64) & (top < tile * 64 + 64)).sum() >= 10
+
+
+def test_every_logit_negative(smp):
+    rows = 70
+    rng = np.random.default_rng(23)
+    blocks = HID // 32
+    lo = rng.integers(0, 8, (V, blocks, 16), dtype=np.uint8)
+    hi = rng.integers(0, 8, (V, blocks, 16), dtype=np.uint8)
+    q4 = np.zeros((V, blocks, 18), np.uint8)
+    q4[:, :, 2:] = lo | (hi << 4)
+    sc = rng.uniform(0.001, 0.02, (V, blocks)).astype(np.float16).view(np.uint16)
+    q4[:, :, 0] = sc & 0xFF
+    q4[:, :, 1] = sc >> 8
+    hidden = rng.uniform(0.5, 2.0, (rows, HID)).astype(np.float32)
+    rlog = o.lmhead_logits(hidden, q4.reshape(-1), V, HID, threads=16)
+    hist, hl = _top_histories(rlog, rows)
+    r24 = (np.arange(rows, dtype=np.uint32) * 1_234_567) & 0xFFFFFF
+    check(smp, q4.reshape(-1), hidden, hist, hl, r24)
+
+
+def test_widest_hidden_state(smp, base):
+    rows, cols = 140, 2048
+    rng = np.random.default_rng(11)
+    blocks = cols // 32
+    q4 = rng.integers(0, 256, (V, blocks, 18), dtype=np.uint8)
+    sc = rng.uniform(0.001, 0.02, (V, blocks)).astype(np.float16).view(np.uint16)
+    q4[:, :, 0] = sc & 0xFF
+    q4[:, :, 1] = sc >> 8
+    hidden = rng.standard_normal((rows, cols)).astype(np.float32)
+    w = base
+    check(smp, q4.reshape(-1), hidden, w["hist"][:rows], w["hist_len"][:rows],
+          w["random_24"][:rows])
+
+
+def test_exact_steps_through_tied_rows(smp):
+    rows = 72
+    w = workloads.make_lmhead(rows=rows)
+    tied = np.sort(np.random.default_rng(rows).choice(np.arange(V // 2, V), 24, replace=False))
+    hist = w["hist"].copy()
+    hist[np.isin(hist, tied)] = 1
+    pairs = step_uniforms()
+    r24 = np.array([pairs[i % len(pairs)][0] for i in range(rows)], np.uint32)
+    _, rdet = check(smp, tied_head(w, tied), np.abs(w["hidden"]) + np.float32(1.0), hist,
+                    w["hist_len"], r24)
+    assert (rdet["kept"] == 16).all()
+    assert (rdet["rank"] == [pairs[i % len(pairs)][1] for i in range(rows)]).all()
