@@ -1244,6 +1244,9 @@ __global__ __launch_bounds__(kSelectThreads) void lm_select_kernel(LmParams p, R
   __shared__ __align__(16) uint32_t act_row[kRecompute ? kMaxBlocks * 8 : 4];
   __shared__ float act_sc[kRecompute ? kMaxBlocks : 1];
   __shared__ uint32_t xbuf[kRecompute ? kTileWaves * kWaveTiles * 64 : 1];
+  __shared__ uint32_t mt_list[kRecompute ? kTileWaves * kWaveTiles : 1];  // tiles to recompute
+  __shared__ uint32_t mt_count;
+  __shared__ uint32_t mt_thr;  // the threshold word of the round that listed them
   __shared__ uint32_t tcand[kTileCap];
   __shared__ uint64_t ecand[kElemCap];
   __shared__ uint64_t top[kTopK];
@@ -1358,6 +1361,7 @@ __global__ __launch_bounds__(kSelectThreads) void lm_select_kernel(LmParams p, R
     nf_tile = kNone;
     first_elems = 0;
     first_fail = 0;
+    mt_count = 0;
   }
   if (tid < (uint32_t)kTopK) top[tid] = 0;
   if constexpr (kRecompute) {
@@ -1366,68 +1370,68 @@ __global__ __launch_bounds__(kSelectThreads) void lm_select_kernel(LmParams p, R
   }
   __syncthreads();  // (1) the bitmap is clear, the activations staged
 
-  // The lane's logit of `tile` (id 64 tile + lane): read from the logits the
-  // GEMM wrote, or recomputed from the packed head and the staged
-  // activations with the head's arithmetic -- the exact int32 block dots
+  // Recomputing a tile's logits from the packed head and the staged
+  // activations, with the head's arithmetic: the exact int32 block dots
   // (v_dot4c_i32_i8 over the nibbles expanded as in the GEMM, so a Q4_0 dot
   // comes out as 16 dot), then the reference's binary32 epilogue over the
   // blocks in order: total + mul(mul(f32(dot), w_scale), a_scale) for Q4_0
   // (a_scale / 16 staged, 16 dot: the same products, scaled by exact powers
-  // of two), total + mul(f32(dot), mul(w_scale, a_scale)) for Q8_0.  The
-  // loads of kBatch blocks are in flight together.  `tile` is wave-uniform.
+  // of two), total + mul(f32(dot), mul(w_scale, a_scale)) for Q8_0.  Lane l
+  // takes id 64 tile + l; `tile` is wave-uniform.
+  constexpr bool kQ8 = kSrc == kRecomputeQ8;
+  constexpr uint32_t kTileB = kQ8 ? kTileBytesQ8 : kTileBytes;
+  constexpr uint32_t kWordsB = kQ8 ? 8u : 4u;  // a lane's weight words per block
+  // the lane's weight words and fp16 weight scale of (tile, block b)
+  auto load_weights = [&](uint32_t tile, uint32_t b, uint32_t(&w)[kWordsB], uint32_t& sc)
+      __attribute__((always_inline)) {
+    const uint8_t* wb = p.weights + ((size_t)b * kTilesPerRow + tile) * kTileB + kWordsB * lane;
+#pragma unroll
+    for (uint32_t q = 0; q < 4; ++q) {
+      if constexpr (kQ8) {
+        const v2u x = *reinterpret_cast<const v2u*>(wb + 512u * q);
+        w[2 * q] = x.x;
+        w[2 * q + 1] = x.y;
+      } else {
+        w[q] = *reinterpret_cast<const uint32_t*>(wb + 256u * q);
+      }
+    }
+    sc = reinterpret_cast<const uint16_t*>(p.weights + (size_t)blocks * kVocab * (kQ8 ? 32 : 16))
+        [(size_t)b * kVocab + tile * kTileIds + lane];
+  };
+  // block b's term of the lane's logit
+  auto block_term = [&](uint32_t b, const uint32_t(&w)[kWordsB], uint32_t sc)
+      __attribute__((always_inline)) -> float {
+    const v4u a0 = *reinterpret_cast<const v4u*>(&act_row[b * 8u]);
+    const v4u a1 = *reinterpret_cast<const v4u*>(&act_row[b * 8u + 4u]);
+    const uint32_t a[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+    int dot = 0;
+#pragma unroll
+    for (uint32_t q = 0; q < 4; ++q) {
+      const uint32_t lo = kQ8 ? w[2 * q] : (w[q] << 4) & 0xf0f0f0f0u;
+      const uint32_t hi = kQ8 ? w[2 * q + 1] : w[q] & 0xf0f0f0f0u;
+      dot = __builtin_amdgcn_sdot4((int)lo, (int)a[2 * q], dot, false);
+      dot = __builtin_amdgcn_sdot4((int)hi, (int)a[2 * q + 1], dot, false);
+    }
+    const float ws = __half2float(__ushort_as_half((unsigned short)sc));
+    return kQ8 ? (float)dot * (ws * act_sc[b]) : ((float)dot * ws) * act_sc[b];
+  };
+  // One wave's whole tile, kBatch blocks' loads in flight at a time (the
+  // error path's first flagged tile, and the general selection's tiles).
   auto tile_logit = [&](uint32_t tile) __attribute__((always_inline)) -> uint32_t {
     if constexpr (!kRecompute) {
       return lrow[tile * kTileIds + lane];
     } else {
-      constexpr bool kQ8 = kSrc == kRecomputeQ8;
-      constexpr uint32_t kTileB = kQ8 ? kTileBytesQ8 : kTileBytes;
-      constexpr uint32_t kWordsB = kQ8 ? 8u : 4u;  // a lane's weight words per block
       constexpr uint32_t kBatch = kQ8 ? 7u : 14u;
       const uint32_t last = blocks - 1u;
-      const uint8_t* wt = p.weights + (size_t)tile * kTileB + (kQ8 ? 8u : 4u) * lane;
-      const uint16_t* ws16 =
-          reinterpret_cast<const uint16_t*>(p.weights + (size_t)blocks * kVocab * (kQ8 ? 32 : 16)) +
-          tile * kTileIds + lane;
       float total = 0.0f;
       for (uint32_t b0 = 0; b0 < blocks; b0 += kBatch) {
         uint32_t w[kBatch][kWordsB];
         uint32_t sc[kBatch];
 #pragma unroll
-        for (uint32_t k = 0; k < kBatch; ++k) {
-          const uint32_t b = min(b0 + k, last);
-          const uint8_t* wb = wt + (size_t)b * kTilesPerRow * kTileB;
+        for (uint32_t k = 0; k < kBatch; ++k) load_weights(tile, min(b0 + k, last), w[k], sc[k]);
 #pragma unroll
-          for (uint32_t q = 0; q < 4; ++q) {
-            if constexpr (kQ8) {
-              const v2u x = *reinterpret_cast<const v2u*>(wb + 512u * q);
-              w[k][2 * q] = x.x;
-              w[k][2 * q + 1] = x.y;
-            } else {
-              w[k][q] = *reinterpret_cast<const uint32_t*>(wb + 256u * q);
-            }
-          }
-          sc[k] = ws16[(size_t)b * kVocab];
-        }
-#pragma unroll
-        for (uint32_t k = 0; k < kBatch; ++k) {
-          const uint32_t b = b0 + k;
-          if (b < blocks) {
-            const v4u a0 = *reinterpret_cast<const v4u*>(&act_row[b * 8u]);
-            const v4u a1 = *reinterpret_cast<const v4u*>(&act_row[b * 8u + 4u]);
-            const uint32_t a[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-            int dot = 0;
-#pragma unroll
-            for (uint32_t q = 0; q < 4; ++q) {
-              const uint32_t lo = kQ8 ? w[k][2 * q] : (w[k][q] << 4) & 0xf0f0f0f0u;
-              const uint32_t hi = kQ8 ? w[k][2 * q + 1] : w[k][q] & 0xf0f0f0f0u;
-              dot = __builtin_amdgcn_sdot4((int)lo, (int)a[2 * q], dot, false);
-              dot = __builtin_amdgcn_sdot4((int)hi, (int)a[2 * q + 1], dot, false);
-            }
-            const float ws = __half2float(__ushort_as_half((unsigned short)sc[k]));
-            const float term = kQ8 ? (float)dot * (ws * act_sc[b]) : ((float)dot * ws) * act_sc[b];
-            total = total + term;
-          }
-        }
+        for (uint32_t k = 0; k < kBatch; ++k)
+          if (b0 + k < blocks) total = total + block_term(b0 + k, w[k], sc[k]);
       }
       return b_of(total);
     }
@@ -1466,15 +1470,15 @@ __global__ __launch_bounds__(kSelectThreads) void lm_select_kernel(LmParams p, R
   // value reaches thr kept.  Every element whose raw word reaches thr ends up
   // in ecand (up to kFirstElems of them; first_elems counts them all).  One
   // pass per bit taken (the lanes' lowest remaining bits).
+  // appends a pass's elements (mask: the lanes holding one): one LDS
+  // atomic reserves their slots past the other waves' elements
+  auto append = [&](uint64_t mask, bool mine, uint64_t e) {
+    uint32_t base = 0;
+    if (lane == 0) base = atomicAdd(&first_elems, (uint32_t)__popcll((unsigned long long)mask));
+    const uint32_t slot = bcast32(base, 0) + lanes_below(mask);
+    if (mine && slot < kFirstElems) ecand[slot] = e;
+  };
   auto tile_round = [&](uint32_t thr) __attribute__((always_inline)) {
-    // appends a pass's elements (mask: the lanes holding one): one LDS
-    // atomic reserves their slots past the other waves' elements
-    auto append = [&](uint64_t mask, bool mine, uint64_t e) {
-      uint32_t base = 0;
-      if (lane == 0) base = atomicAdd(&first_elems, (uint32_t)__popcll((unsigned long long)mask));
-      const uint32_t slot = bcast32(base, 0) + lanes_below(mask);
-      if (mine && slot < kFirstElems) ecand[slot] = e;
-    };
     uint32_t m = 0, d = 0;
 #pragma unroll
     for (int j = 0; j < kWaveKeys; ++j) {
@@ -1507,25 +1511,26 @@ __global__ __launch_bounds__(kSelectThreads) void lm_select_kernel(LmParams p, R
     }
     const uint32_t ntiles = uniform(count);
     if (ntiles > kWaveTiles && lane == 0) first_fail = 1u;
-    if (ntiles != 0 && ntiles <= kWaveTiles) {
+    if constexpr (kRecompute) {
+      // listed for recompute_listed, which all waves run after the next barrier
+      if (ntiles != 0 && ntiles <= kWaveTiles) {
+        __builtin_amdgcn_wave_barrier();
+        uint32_t base = 0;
+        if (lane == 0) {
+          base = atomicAdd(&mt_count, ntiles);
+          mt_thr = thr;
+        }
+        if (lane < ntiles) mt_list[bcast32(base, 0) + lane] = wave_tiles[wave][lane];
+      }
+    } else if (ntiles != 0 && ntiles <= kWaveTiles) {
       __builtin_amdgcn_wave_barrier();
       // their logits (tile i of the wave is wave-uniform: readlane; past the
       // list the row's tile 0 is read again), then the elements whose raw
       // value reaches thr, as (id, raw bits)
       uint32_t xb[kWaveTiles];
-      if constexpr (!kRecompute) {
-        const uint32_t tl = lane < ntiles ? wave_tiles[wave][lane] : 0u;
+      const uint32_t tl = lane < ntiles ? wave_tiles[wave][lane] : 0u;
 #pragma unroll
-        for (int i = 0; i < (int)kWaveTiles; ++i) xb[i] = lrow[bcast32(tl, (uint32_t)i) * kTileIds + lane];
-      } else {
-        // one tile at a time into this wave's part of xbuf, then back into
-        // registers (past ntiles the values are not used)
-        uint32_t* xw = xbuf + wave * kWaveTiles * 64u;
-        for (uint32_t i = 0; i < ntiles; ++i) xw[i * 64u + lane] = tile_logit(uniform(wave_tiles[wave][i]));
-        __builtin_amdgcn_wave_barrier();
-#pragma unroll
-        for (int i = 0; i < (int)kWaveTiles; ++i) xb[i] = xw[(uint32_t)i * 64u + lane];
-      }
+      for (int i = 0; i < (int)kWaveTiles; ++i) xb[i] = lrow[bcast32(tl, (uint32_t)i) * kTileIds + lane];
       const float floor_value = f_of(key_value_bits((uint64_t)thr << 32));
       uint32_t e = 0;
 #pragma unroll
@@ -1539,6 +1544,57 @@ __global__ __launch_bounds__(kSelectThreads) void lm_select_kernel(LmParams p, R
         }
         append(mask, e != 0, x);
         e &= e - 1u;
+      }
+    }
+  };
+
+  // Recomputing the listed tiles with all eight waves (recompute mode; every
+  // thread calls it, after the barrier that follows a round): G tiles at a
+  // time, each tile's blocks split over 8 / G waves whose per-block terms
+  // go through LDS (xbuf), then one wave per tile adds the terms in block
+  // order -- the reference's order -- and appends the elements whose value
+  // reaches the round's threshold, as the memory mode's read does.  One
+  // memory round trip per group of tiles instead of one per batch of blocks
+  // of one tile on one wave.
+  auto recompute_listed = [&]() __attribute__((always_inline)) {
+    if constexpr (kRecompute) {
+      const uint32_t count = uniform(mt_count);
+      if (count == 0u) return;
+      const float floor_value = f_of(key_value_bits((uint64_t)uniform(mt_thr) << 32));
+      constexpr uint32_t kWaves = kSelectThreads / 64u;
+      constexpr uint32_t kMaxPart = 8;  // blocks of one wave's part, at most
+      const uint32_t G = blocks <= 8u ? 8u : blocks <= 16u ? 4u : blocks <= 32u ? 2u : 1u;
+      const uint32_t wpt = kWaves / G;                  // waves per tile
+      const uint32_t bpw = (blocks + wpt - 1u) / wpt;   // blocks per wave, <= kMaxPart
+      const uint32_t slot = wave / wpt;
+      const uint32_t part = wave - slot * wpt;
+      const uint32_t b_lo = part * bpw;
+      const uint32_t b_hi = min(blocks, b_lo + bpw);
+      float* terms = reinterpret_cast<float*>(xbuf) + slot * blocks * 64u;
+      static_assert(kMaxBlocks * 64u <= kTileWaves * kWaveTiles * 64u, "the terms fit xbuf");
+      for (uint32_t g0 = 0; g0 < count; g0 += G) {
+        const uint32_t t = g0 + slot;
+        const uint32_t tile = t < count ? uniform(mt_list[t]) : 0u;
+        if (t < count && b_lo < b_hi) {
+          uint32_t w[kMaxPart][kWordsB];
+          uint32_t sc[kMaxPart];
+#pragma unroll
+          for (uint32_t k = 0; k < kMaxPart; ++k)
+            load_weights(tile, min(b_lo + k, b_hi - 1u), w[k], sc[k]);
+#pragma unroll
+          for (uint32_t k = 0; k < kMaxPart; ++k)
+            if (b_lo + k < b_hi) terms[(b_lo + k) * 64u + lane] = block_term(b_lo + k, w[k], sc[k]);
+        }
+        __syncthreads();
+        if (part == 0u && t < count) {
+          float total = 0.0f;
+          for (uint32_t b = 0; b < blocks; ++b) total = total + terms[b * 64u + lane];
+          const uint32_t x = b_of(total);
+          const bool take = f_of(x) >= floor_value;
+          const uint64_t mask = __ballot(take);
+          if (mask != 0) append(mask, take, ((uint64_t)(tile * kTileIds + lane) << 32) | x);
+        }
+        __syncthreads();
       }
     }
   };
@@ -1631,6 +1687,7 @@ __global__ __launch_bounds__(kSelectThreads) void lm_select_kernel(LmParams p, R
     if (lane == 0 && my_bad != kNone) atomicMin(&bad_hist, my_bad);
   }
   __syncthreads();  // (3) the bitmap, the first-round lists and the errors are done
+  recompute_listed();  // (recompute mode: the first round's listed tiles)
 
   // ---- wave 0: errors, then the first round's candidates ----
   // (every word read at once: one LDS round trip).  Keys the candidates:
@@ -1684,6 +1741,7 @@ __global__ __launch_bounds__(kSelectThreads) void lm_select_kernel(LmParams p, R
           round2_thr = k20_word;
           first_elems = 0;
           first_fail = 0;
+          mt_count = 0;
         }
       }
     } else {
@@ -1723,6 +1781,7 @@ __global__ __launch_bounds__(kSelectThreads) void lm_select_kernel(LmParams p, R
   if (uniform(round2) != 0u) {
     if (tile_wave) tile_round(uniform(round2_thr));
     __syncthreads();  // (5) the second round's candidates
+    recompute_listed();
     if (wave != 0) {
       gather_history();
       return;
