@@ -155,6 +155,46 @@ def test_lmhead_decode_steps_match_the_oracle_loop():
         smp.close()
 
 
+def test_lmhead_decode_steps_in_one_pass():
+    """Above 64 rows the head runs in one pass (no logits kept; the selection
+    recomputes the tiles it reads): 70 sequences in lockstep with the oracle's
+    loop, rows with limits of 2 to 5 tokens, the last rows starting with a bad
+    prompt id (an error on the first step, no draw)."""
+    import torch
+
+    w = workloads.make_lmhead(rows=4)
+    q4 = w["q4"]
+    smp = s.BatchSampler(0)
+    packed = smp.pack_lmhead(torch.from_numpy(q4).to("cuda:0"))
+    rng = np.random.default_rng(9)
+    n = 70
+    prompts = [workloads.zipf_ids(rng, int(k)) for k in rng.integers(1, 60, n)]
+    prompts[-1] = np.append(prompts[-1], np.uint32(V + 3))
+    seeds, limits = list(range(100, 100 + n)), [int(x) for x in rng.integers(2, 6, n)]
+    oracle_rows = [o.DecodeRow(p, sd, lim) for p, sd, lim in zip(prompts, seeds, limits)]
+    dec = s.DecodeBatch(prompts, seeds, limits, sampler=smp)
+    try:
+        for step in range(6):
+            hidden = np.stack([
+                np.random.default_rng([r, step, d.working[-1]]).normal(0, 1, workloads.HIDDEN)
+                for r, d in enumerate(oracle_rows)]).astype(np.float32)
+            logits = o.lmhead_logits(hidden, q4, V, workloads.HIDDEN, threads=16)
+            want = [d.step(logits[r]) for r, d in enumerate(oracle_rows)]
+            got = dec.lmhead_step(packed, torch.from_numpy(hidden.view(np.int32)).to("cuda:0"))
+            assert got.tolist() == [s.NO_TOKEN if t is None else t for t in want], step
+            if not dec.active():
+                break
+        assert not dec.active()
+        states = dec.sampling_states()
+        for r, d in enumerate(oracle_rows):
+            assert dec.contexts()[r].tolist() == d.working
+            assert (states[r].state(), states[r].draws()) == (d.state.state(), d.state.draws())
+        assert oracle_rows[-1].reason == "ERROR" and states[-1].draws() == 0
+    finally:
+        dec.close()
+        smp.close()
+
+
 def test_active_row_at_its_cap_is_not_sampled():
     """A row still marked active whose context is already at its cap is not
     sampled (the REPL stops before sampling when there is no room): it ends

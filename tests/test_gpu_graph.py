@@ -135,6 +135,38 @@ def test_lmhead_q8_replays(smp):
     graph.close()
 
 
+def test_lmhead_one_pass_replays(smp):
+    """70 rows through the Q4_0 head without a logits buffer (one pass: the
+    selection recomputes tiles from the head) under capture, replayed with
+    new hidden states."""
+    rows = 70
+    w = workloads.make_lmhead(rows=rows)
+    smp.reserve(rows, workloads.HIDDEN)
+    packed = smp.pack_lmhead(hip.DeviceArray.from_numpy(w["q4"]))
+    d = hip.DeviceArray.from_numpy
+    hidden, hist, hl, r24 = d(w["hidden"]), d(w["hist"]), d(w["hist_len"]), d(w["random_24"])
+    token = hip.DeviceArray(rows, np.uint32)
+    det = hip.DeviceArray((rows, DW), np.uint32)
+    stream = hip.Stream()
+    graph = hip.Graph(stream)
+    graph.begin()
+    smp.lmhead_sample(packed, hidden, r24, hist, hl, token=token, detail=det, stream=stream)
+    graph.end()
+    rng = np.random.default_rng(4)
+    for replay in range(3):
+        x = rng.standard_normal((rows, workloads.HIDDEN), dtype=np.float32)
+        hidden.upload(x)
+        graph.launch()
+        stream.synchronize()
+        rlog = o.lmhead_logits(x, w["q4"], V, workloads.HIDDEN, threads=16)
+        rtok, rdet, rerr, _ = o.sample_batch(rlog, w["hist"], w["hist_len"], w["random_24"],
+                                             threads=16)
+        assert_rows_equal(token.numpy(), det.numpy().view(s.DETAIL_DTYPE).reshape(rows),
+                          np.zeros(rows, s.ERROR_DTYPE), rtok, rdet, rerr)
+    graph.close()
+    packed.free()
+
+
 def test_decode_step_replays(smp):
     rng = np.random.default_rng(8)
     prompts = [workloads.zipf_ids(rng, n) for n in (30, 7, 120, 2)]
