@@ -288,10 +288,14 @@ uint32_t pb_lmhead_pack_q4_0(const uint8_t *d_q4, size_t vocab, size_t cols, uin
  * (896 for Qwen2.5-0.5B).  packed_bytes is the size of d_packed and must be
  * pb_lmhead_packed_bytes(vocab, cols): a head packed for another width or
  * format is refused (PB_CAPACITY) before anything is enqueued.  d_logits
- * (optional, rows x vocab words) receives the raw logits; without it they
- * live in the context's workspace.  Per-row outputs and error records as
- * pb_sample_batch (non-finite logit, bad history id).  Needs a context
- * reserved (pb_context_reserve) for at least `rows` rows and `cols` columns. */
+ * (optional, rows x vocab words) receives the raw logits.  Without it, a step
+ * of more than 64 rows runs in one pass: the head writes no logits at all,
+ * only two words per (row, 64-id tile), and the selection recomputes the few
+ * tiles it has to read from the packed head (same results, bit for bit); up
+ * to 64 rows the logits go through the context's workspace.  Per-row outputs
+ * and error records as pb_sample_batch (non-finite logit, bad history id).
+ * Needs a context reserved (pb_context_reserve) for at least `rows` rows and
+ * `cols` columns. */
 uint32_t pb_lmhead_sample_batch(pb_context *ctx, const uint8_t *d_packed, size_t packed_bytes,
                                 size_t vocab, size_t cols, const uint32_t *d_hidden, uint32_t rows,
                                 const uint32_t *d_hist, size_t hist_ld,

@@ -33,6 +33,16 @@ constexpr uint32_t kFlagDrawBoundary = 1u;
 constexpr uint32_t kFlagCutoffBoundary = 2u;
 
 __device__ __forceinline__ float f_of(uint32_t b) { return __uint_as_float(b); }
+
+// Linear workgroup index -> work item, so that each XCD takes one contiguous
+// range of the n items: the hardware hands workgroup L of a launch to XCD
+// L % 8, and the workgroups that XCD k receives (L = k, k + 8, ...) take the
+// items of its range in order.  A bijection of [0, n) for any n.
+__device__ __forceinline__ uint32_t xcd_contiguous_item(uint32_t linear, uint32_t n) {
+  const uint32_t k = linear & 7u, j = linear >> 3;
+  const uint32_t per = n >> 3, extra = n & 7u;
+  return k * per + (k < extra ? k : extra) + j;
+}
 __device__ __forceinline__ uint32_t b_of(float f) { return __float_as_uint(f); }
 
 // ---- scalbnf / expf: FreeBSD e_expf method as adapted in

@@ -66,11 +66,12 @@ struct LmParams {
   uint32_t cols;            // hidden width, multiple of 32
   int8_t* act_q;            // [blocks][rows_pad][32] Q8_0 quants
   float* act_s;             // [blocks][rows_pad] activation scales (a_scale / 16 for Q4_0, a_scale for Q8_0)
-  uint32_t* logits;         // rows x logits_ld raw logits (binary32 words)
+  uint32_t* logits;         // rows x logits_ld raw logits (binary32 words); null for
+                            // the wide GEMM's one pass (tilesec then set)
   size_t logits_ld;
   uint32_t* tilemax;        // rows x 2,374 order word of the largest raw logit per 64-id
                             // tile, 0xffffffff when the tile holds a non-finite logit
-  uint32_t* tilesec;        // rows x 2,374 second words (narrow GEMM only, else null):
+  uint32_t* tilesec;        // rows x 2,374 second words (narrow GEMM and one pass, else null):
                             // a bound above every other logit's order word of the tile
                             // (a multiple of 64) plus the maximum's index in the tile
   // tile_words_kernel only (null / 0 otherwise): the logits it reads are also

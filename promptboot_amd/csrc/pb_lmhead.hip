@@ -15,17 +15,26 @@
 //   lm_gemm_kernel     one workgroup per (64-id vocabulary tile, 256 rows):
 //                      v_mfma_i32_16x16x32_i8 gives each block's exact int32
 //                      dot; the reference's per-block binary32 epilogue runs on
-//                      the VALU.  Writes the raw logits and, per (row, tile),
-//                      the order word of the largest raw logit.
-//   lm_gemm_narrow_kernel  the same for up to 64 rows, one wave per tile;
-//                      with up to kFusedQuantRows rows each workgroup
-//                      quantises the activations itself (no lm_quant_kernel).
+//                      the VALU.  With a logits buffer it writes the raw logits
+//                      and, per (row, tile), the order word of the largest raw
+//                      logit; without one (kLogits false: one pass) it writes
+//                      no logits, only that word and the tile's second word (a
+//                      bound on its other logits and the maximum's index).
+//   lm_gemm_narrow_kernel  the same for up to 64 rows, one wave per tile,
+//                      logits always written (to the workspace if the caller
+//                      keeps none) with both words; with up to
+//                      kFusedQuantRows rows each workgroup quantises the
+//                      activations itself (no lm_quant_kernel).
 //   lm_select_kernel   one workgroup per row: the history bitmap in LDS, then
 //                      the exact top-20 of the penalised logits best-first
 //                      over the tiles (the penalty never raises a value, so a
 //                      tile's raw maximum bounds its penalised elements), and
 //                      the row's finish (softmax, top-p, draw) with the
-//                      sampler's finalize_row.
+//                      sampler's finalize_row.  A tile whose second word says
+//                      that only its maximum can reach the threshold gives
+//                      that element from its words; the other tiles it reads
+//                      are read from the logits, or in one pass recomputed from
+//                      the packed head with the head's own arithmetic.
 //
 // Weight nibbles are stored XOR 8 and expanded to int8 by masking them into
 // the high half of a byte: (n ^ 8) << 4 = 16 * (n - 8) as a signed byte.  The
@@ -550,9 +559,18 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(4)
   const uint32_t wave = tid >> 6;
   const uint32_t n = lane & 15u;  // MFMA row (A) / column (B)
   const uint32_t q = lane >> 4;   // contraction quarter; result rows 4q .. 4q+3
-  const uint32_t tile = blockIdx.x;
+  // Consecutive tiles run on the same XCD (xcd_contiguous_item): every
+  // (row, tile) gets one or two 4-byte words in row-major arrays, and the
+  // words of up to eight neighbouring tiles share a 32-byte sector, which
+  // leaves an XCD's L2 whole only when the neighbours were written through
+  // that L2.  With tile = block index the neighbours sat on eight different
+  // XCDs: 8 x the words' bytes written (39.7 MB instead of 4.9 MB per
+  // 256-row one-pass step, WRITE_SIZE).
+  const uint32_t item = xcd_contiguous_item(blockIdx.x + blockIdx.y * gridDim.x,
+                                            gridDim.x * gridDim.y);
+  const uint32_t tile = item % kTilesPerRow;
   const uint32_t v0 = tile * kTileIds;
-  const uint32_t group0 = blockIdx.y * kRowsPerGroup;
+  const uint32_t group0 = item / kTilesPerRow * kRowsPerGroup;
   const uint16_t* wscale16 =
       reinterpret_cast<const uint16_t*>(p.weights + (size_t)blocks * kVocab * (kQ8 ? 32 : 16));
 
