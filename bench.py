@@ -481,6 +481,49 @@ def time_host_buffers(smp, w1: dict, w: dict, stream, calls: int = 200, steps: i
                                      "h2d_gbs": round(h2d / sec / 1e9, 1), "steps": steps}}
 
 
+def trace_case(case: str, steps: int) -> None:
+    """One small-batch case alone, for a kernel trace of its launches:
+      warm    `steps` bound pb_sample_batch steps at B=1, then at B=64, on the
+              same inputs every step;
+      cold    the same through cold_pass, the inputs rotated over COLD_SETS
+              copies (its settle phase adds untimed steps);
+      dropin  `steps` + 10 pb_sample_token_with_repetition calls on host
+              buffers (row 0 of the B=1 workload, its 300-id history)."""
+    from promptboot_amd import hip
+    from promptboot_amd import sampler as s
+    from promptboot_amd import workloads
+
+    hip.set_device(0)
+    stream = hip.Stream()
+    if case == "dropin":
+        w = workloads.make("single")
+        row0 = np.ascontiguousarray(w["logits"][0]).view(np.uint32)
+        prompt = np.ascontiguousarray(w["hist"][0, :w["hist_len"][0]])
+        state = s.SamplingState(int(w["seeds"][0]))
+        for _ in range(steps + 10):
+            s.sample_token_with_repetition(row0.copy(), prompt, np.zeros(s.SEEN_BYTES, np.uint8),
+                                           state)
+        log(f"trace case dropin: {steps + 10} calls done")
+        return
+    smp = s.BatchSampler(0)
+    for B, name in ((1, "single"), (64, "small")):
+        w = workloads.make(name)
+        logits, hist, hl, r24 = dev(w["logits"]), dev(w["hist"]), dev(w["hist_len"]), dev(w["random_24"])
+        token = hip.DeviceArray(B, np.uint32)
+        if case == "warm":
+            step = smp.bind_sample(logits, r24, hist, hl, token=token, stream=stream)
+            for _ in range(steps):
+                step()
+            hip.synchronize()
+        else:
+            bufs = dict(logits=logits, hist=hist, hl=hl, r24=r24, token=token)
+            cold_pass(smp, bufs, COLD_SETS[B], steps, 0, stream)
+        for a in (logits, hist, hl, r24, token):
+            a.free()
+        log(f"trace case {case}: B={B}, {steps} steps done")
+    smp.close()
+
+
 MFMA_INT8_PEAK_TOPS = 5000.0     # dense int8 MFMA, MI355X
 VALU_LANE_OPS_PEAK = 256 * 4 * 16 * 2.4e9  # 32-bit VALU lane-ops/s, MI355X
 
@@ -824,6 +867,9 @@ def main() -> int:
                          "rocprofv3 --pmc run can scale FETCH_SIZE/WRITE_SIZE to bytes")
     ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="write the counter summary of two rocprofv3 --pmc runs and exit")
+    ap.add_argument("--trace-case", choices=("warm", "cold", "dropin"),
+                    help="run only this small-batch case for --steps steps (for a kernel "
+                         "trace of its launches) and exit")
     ap.add_argument("--cpu-worker", default=None, help=argparse.SUPPRESS)
     ap.add_argument("--production-worker", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
@@ -835,6 +881,9 @@ def main() -> int:
         return 0
     if args.traffic_summary:
         traffic_summary(*args.traffic_summary)
+        return 0
+    if args.trace_case:
+        trace_case(args.trace_case, args.steps)
         return 0
     if args.gpus != 1:
         print("bench.py measures one GPU only: the sampler shards rows across GPUs with no "
