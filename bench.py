@@ -15,8 +15,9 @@ The printed JSON line also carries:
                       over its average launch time (HIP events on the launch
                       stream) against the 8 TB/s MI355X peak; the read
                       bandwidth a plain streaming read of the same number of
-                      bytes reaches on this device (pb_device_read_probe, the
-                      faster of 4096 and 32,768 workgroups);
+                      bytes reaches on this device (the fastest shape of
+                      READ_SHAPES: contiguous ranges or grid-stride chunks,
+                      pb_device_read_probe / _grid_stride);
                       and the HBM traffic measured by rocprofv3 counters,
                       taken from the committed summary only when that summary
                       names this very build (pb_version);
@@ -29,9 +30,11 @@ The printed JSON line also carries:
                       pinned CPU oracle, min/median/max;
   parity              token agreement with the oracle over every row;
   adversarial_B1024   the flat / ties / dominant / half-vocabulary-history
-                      sub-cases, each timed and checked against the oracle,
+                      sub-cases and the boundary batch (draws exactly on a
+                      step of the cumulative distribution), each timed and
+                      checked against the oracle,
                       with the read ceiling of the same byte count
-                      (pb_device_read_probe, as above) beside it;
+                      (as above) beside it;
   lmhead_fused        the fused Q4_0 LM head + sampler step (B=256);
   lmhead_q8_fused     the same with the Q8_0 head (the model's output head);
   lmhead_B1           one conversation's step (B=1) through each head,
@@ -709,9 +712,10 @@ def measured_traffic(version: str) -> dict:
 # (The B=256 legs run one pass: the GEMM keeps no logits and the selection
 # recomputes the tiles it reads.)
 LM_STEP_KERNELS = {
-    ("q4_0", 256): [("pb::lm_quant_kernel", 57344), ("pb::lm_gemm_kernel<false, false>", 1215488),
+    ("q4_0", 256): [("pb::lm_quant_kernel", 57344),
+                    ("pb::lm_gemm_kernel<false, false, 28u>", 1215488),
                     ("pb::lm_select_kernel<1>", 131072)],
-    ("q8_0", 256): [("pb::lm_quant_kernel", 57344), ("pb::lm_gemm_kernel<true, false>", 1215488),
+    ("q8_0", 256): [("pb::lm_quant_kernel", 57344), ("pb::lm_gemm_kernel<true, false, 0u>", 1215488),
                     ("pb::lm_select_kernel<2>", 131072)],
     ("q4_0", 1): [("pb::lm_gemm_narrow_kernel<false", 152064), ("pb::lm_select_kernel<0>", 512)],
     ("q8_0", 1): [("pb::lm_gemm_narrow_kernel<true", 151936), ("pb::lm_select_kernel<0>", 512)],

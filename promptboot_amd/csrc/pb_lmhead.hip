@@ -12,7 +12,7 @@
 //                      (row, block): the Q8_0 activations in the head's
 //                      contraction order and the fp32 activation scales (for
 //                      the Q4_0 head divided by 16), zeros for padding rows.
-//   lm_gemm_kernel     one workgroup per (64-id vocabulary tile, 256 rows):
+//   lm_gemm_kernel     one workgroup per (64-id vocabulary tile, 128 rows):
 //                      v_mfma_i32_16x16x32_i8 gives each block's exact int32
 //                      dot; the reference's per-block binary32 epilogue runs on
 //                      the VALU.  With a logits buffer it writes the raw logits
@@ -63,12 +63,20 @@ typedef uint32_t v2u __attribute__((ext_vector_type(2)));
 constexpr uint32_t kBlockThreads = 256;
 constexpr uint32_t kTileIds = 64;        // vocabulary ids per tile and per workgroup
 constexpr uint32_t kRowsPerWave = 32;   // two 16-row MFMA row tiles per wave in the head
-constexpr uint32_t kGemmThreads = 512;  // eight waves
-constexpr uint32_t kRowsPerGroup = 256;
+constexpr uint32_t kGemmThreads = 256;  // four waves
+// Rows per workgroup of the wide GEMM.  Against 256 rows with eight waves the
+// 128-row, four-wave workgroups spread the launch's last workgroups over more
+// CUs: B = 256 Q4_0 one-pass GEMM 106.6 -> 103.7 us, Q8_0 116.5 -> 112.7 us
+// (same box, traced).  16 or 64 rows per wave were slower (+9 % and +2.5 %:
+// the nibble unpacking is shared by a wave's rows; 64 rows need 213 VGPRs).
+constexpr uint32_t kRowsPerGroup = 128;
 // Batches up to kNarrowRows take lm_gemm_narrow_kernel (measured per step,
 // Q4_0 / Q8_0: B = 64 74.8 / 73.7 us against 92.0 / 98.1 with the wide kernel;
 // B = 128 119.2 / 121.9 against 103.6 / 108.6).
 constexpr uint32_t kWordsPerRow = kVocab / 32;
+// Blocks of 32 in Qwen2.5-0.5B's hidden state of 896: the width whose block
+// loops are unrolled whole.
+constexpr uint32_t kModelBlocks = 28;
 constexpr uint32_t kTilesPerRow = kVocab / kTileIds;  // 2,374
 constexpr uint32_t kTileBytes = kTileIds * 16;    // packed Q4_0 nibbles of one (block, tile)
 constexpr uint32_t kTileBytesQ8 = kTileIds * 32;  // packed Q8_0 weights of one (block, tile)
@@ -383,7 +391,7 @@ __device__ __forceinline__ uint32_t tile_second_word(const uint32_t (&ow)[4], ui
 // row test, and each address is the lane's 32-bit offset plus the step's.
 // They are non-temporal: the selection reads a few
 // tiles of them, and ordinary stores of a 256-row step (155.6 MB) evict the
-// packed weights that a workgroup's eight waves share through the L2.
+// packed weights that a workgroup's waves share through the L2.
 // Measured per 256-row step: Q8_0 161.3-162.0 -> 142.1-149.8 us, Q4_0 about
 // even (128.9-130.0 -> 129.4-134.9 us, HIP events 129.0-131.5 ->
 // 129.4-130.4 us).
@@ -545,12 +553,17 @@ __device__ __forceinline__ void write_tile_words(const LmParams& p,
 // scales are both fp16 values, so ws * a_scale is exact, with at most 22
 // significant bits.  Folding the conversion into an FMA as above would work,
 // but it needs -M * ws * a_scale per value: one op either way.)
-template <bool kQ8, bool kLogits>
+//
+// kNB, when not 0, is the number of blocks (the hidden width / 32) known at
+// compile time: the Q4_0 block loop is then unrolled whole, so the LDS
+// addresses of the scales are immediate offsets (Q4_0 one-pass GEMM at the
+// model's width of 896: 102.5 -> 100.4 us, same box, traced).
+template <bool kQ8, bool kLogits, uint32_t kNB = 0>
 __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(4))) void lm_gemm_kernel(LmParams p) {
   // Dynamic LDS: the activation scales / 16 of every block for the group's
-  // 256 rows, then this tile's weight scales and -M * weight scales by block.
+  // 128 rows, then this tile's weight scales and -M * weight scales by block.
   extern __shared__ __align__(16) float lds[];
-  const uint32_t blocks = p.cols / 32u;
+  const uint32_t blocks = kNB != 0 ? kNB : p.cols / 32u;
   float* act_scale = lds;
   float* w_scale = lds + blocks * kRowsPerGroup;
   float* w_neg = w_scale + blocks * kTileIds;
@@ -565,12 +578,14 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(4)
   // leaves an XCD's L2 whole only when the neighbours were written through
   // that L2.  With tile = block index the neighbours sat on eight different
   // XCDs: 8 x the words' bytes written (39.7 MB instead of 4.9 MB per
-  // 256-row one-pass step, WRITE_SIZE).
+  // 256-row one-pass step, WRITE_SIZE).  The row groups of one tile are
+  // consecutive items, so they run on one XCD at about the same time and the
+  // head leaves HBM once (group-major items read it once per group).
   const uint32_t item = xcd_contiguous_item(blockIdx.x + blockIdx.y * gridDim.x,
                                             gridDim.x * gridDim.y);
-  const uint32_t tile = item % kTilesPerRow;
+  const uint32_t tile = item / gridDim.y;
   const uint32_t v0 = tile * kTileIds;
-  const uint32_t group0 = item / kTilesPerRow * kRowsPerGroup;
+  const uint32_t group0 = item % gridDim.y * kRowsPerGroup;
   const uint16_t* wscale16 =
       reinterpret_cast<const uint16_t*>(p.weights + (size_t)blocks * kVocab * (kQ8 ? 32 : 16));
 
@@ -754,8 +769,7 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(4)
     __builtin_amdgcn_sched_barrier(0);
     if (blocks > 1u) run(1u, odd_ops, odd_tag, kNext);
     __builtin_amdgcn_sched_barrier(0);
-#pragma unroll 1
-    for (uint32_t b = 2; b + 1u < blocks; b += 2) {
+    auto round = [&](uint32_t b) __attribute__((always_inline)) {
       load(b + 1u, odd_ops);
       __builtin_amdgcn_sched_barrier(0);
       run(b, even, odd_tag, kNext);
@@ -764,6 +778,13 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(4)
       __builtin_amdgcn_sched_barrier(0);
       run(b + 1u, odd_ops, odd_tag, kNext);
       __builtin_amdgcn_sched_barrier(0);
+    };
+    if constexpr (kNB != 0) {
+#pragma unroll
+      for (uint32_t b = 2; b + 1u < kNB; b += 2) round(b);
+    } else {
+#pragma unroll 1
+      for (uint32_t b = 2; b + 1u < blocks; b += 2) round(b);
     }
     if ((blocks & 1u) != 0u && blocks > 1u) run(last, even, odd_tag, kNext);
   };
@@ -817,7 +838,7 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(4)
 }
 
 // ---- the head for narrow batches (up to 64 rows) ----
-// The wide kernel stages the scales of 256 rows in LDS and gives each wave
+// The wide kernel stages the scales of 128 rows in LDS and gives each wave
 // 32 rows of one 64-id tile; with few rows most of that work is padding.
 // Here one wave takes one 64-id tile and 16 kRT rows (one MFMA row tile up
 // to 32 rows, two above), four waves per workgroup (two for the Q8_0 head
@@ -1986,8 +2007,8 @@ static void launch_narrow(uint32_t rows, hipStream_t stream, const LmParams& p) 
   constexpr int kNW = kQ8 && kRT == 1 ? 2 : 4;
   const dim3 grid((kTilesPerRow + kNW - 1) / kNW, (rows + 16u * kRT - 1) / (16u * kRT));
   if constexpr (!kQ8) {
-    if (p.cols == 896u) {
-      hipLaunchKernelGGL((lm_gemm_narrow_kernel<kQ8, kRT, kSets, kI, kFused, 28, kNW>), grid,
+    if (p.cols == kModelBlocks * 32u) {
+      hipLaunchKernelGGL((lm_gemm_narrow_kernel<kQ8, kRT, kSets, kI, kFused, kModelBlocks, kNW>), grid,
                          dim3(64 * kNW), 0, stream, p);
       return;
     }
@@ -2039,16 +2060,23 @@ hipError_t launch_lm_sample(const LmParams& p, const RowParams& rp, hipStream_t 
   } else {
     const dim3 gemm_grid(kTilesPerRow, (p.rows_pad + kRowsPerGroup - 1) / kRowsPerGroup);
     const size_t lds = gemm_lds_bytes(p.cols);
+    const bool model_width = p.cols == kModelBlocks * 32u;  // the Q4_0 loop unrolled whole
     if (p.logits == nullptr) {  // one pass: tile and second words, no logits
       if (p.q8)
         hipLaunchKernelGGL((lm_gemm_kernel<true, false>), gemm_grid, dim3(kGemmThreads), lds,
                            stream, p);
+      else if (model_width)
+        hipLaunchKernelGGL((lm_gemm_kernel<false, false, kModelBlocks>), gemm_grid,
+                           dim3(kGemmThreads), lds, stream, p);
       else
         hipLaunchKernelGGL((lm_gemm_kernel<false, false>), gemm_grid, dim3(kGemmThreads), lds,
                            stream, p);
     } else if (p.q8) {
       hipLaunchKernelGGL((lm_gemm_kernel<true, true>), gemm_grid, dim3(kGemmThreads), lds, stream,
                          p);
+    } else if (model_width) {
+      hipLaunchKernelGGL((lm_gemm_kernel<false, true, kModelBlocks>), gemm_grid,
+                         dim3(kGemmThreads), lds, stream, p);
     } else {
       hipLaunchKernelGGL((lm_gemm_kernel<false, true>), gemm_grid, dim3(kGemmThreads), lds,
                          stream, p);
