@@ -669,8 +669,10 @@ static uint32_t enqueue_lmhead(pb_context* ctx, const uint8_t* d_packed, size_t 
     set_error(err, PB_CAPACITY, PB_DOMAIN_LOGITS, PB_VOCAB, vocab, PB_FIELD_LOGITS, 0);
     return PB_CAPACITY;
   }
-  // The head keeps every block's activation scales for 256 rows in 64 KB of
-  // LDS: up to 2,048 columns (Qwen2.5-0.5B has 896).
+  // The wide head keeps every block's scales (a tile's weight scales and a
+  // 128-row group's activation scales) in 64 KB of LDS at 2,048 columns, and
+  // the selection stages a row's activations for up to 64 blocks: up to
+  // 2,048 columns (Qwen2.5-0.5B has 896).
   if (cols == 0 || cols % 32 != 0 || cols > 2048) {
     set_error(err, PB_CAPACITY, PB_DOMAIN_NONE, 32, cols, PB_FIELD_BYTES, 4);
     return PB_CAPACITY;
