@@ -819,8 +819,8 @@ def traffic_summary(fetch_dir: str, write_dir: str) -> None:
     w = workloads.make("large")
     alg = workloads.algorithmic_bytes(w["hist_len"])
     repo = "$REPO"
-    cmd = ("cd /tmp && export TMPDIR=/tmp && timeout -s KILL 300 rocprofv3 --pmc {c} -f csv -d "
-           f"{repo}/gpurun_out/pmc_{{c}} -o run -- python3 {repo}/bench.py --no-cpu-baseline "
+    cmd = ("cd /tmp && export TMPDIR=/tmp && timeout -s KILL 240 rocprofv3 --pmc {c} -f csv -d "
+           f"/tmp/pmc_{{c}} -o run -- python3 {repo}/bench.py --no-cpu-baseline "
            "--no-adversarial --no-host-buffers --no-production --batches 4096 "
            "--steps 2 --warmup 0 --calibration-copy-mib 1024")
     out = {"kernel": SEGMENT_KERNEL,
@@ -828,8 +828,8 @@ def traffic_summary(fetch_dir: str, write_dir: str) -> None:
            "workload": "B=4096 rows x 151936 fp32 logits, history lengths U[16,32768] "
                        "(promptboot_amd.workloads large)",
            "commands": [cmd.format(c="FETCH_SIZE"), cmd.format(c="WRITE_SIZE"),
-                        f"python3 {repo}/bench.py --traffic-summary {repo}/gpurun_out/pmc_FETCH_SIZE "
-                        f"{repo}/gpurun_out/pmc_WRITE_SIZE"],
+                        f"cd {repo} && python3 bench.py --traffic-summary /tmp/pmc_FETCH_SIZE "
+                        "/tmp/pmc_WRITE_SIZE"],
            "calibration": {"kernel": f"{CALIBRATION_KERNEL} (hipMemcpyAsync device to device, "
                                      "1024 MiB read + 1024 MiB written)",
                            "fetch_size_kib": round(f_cal, 2), "write_size_kib": round(w_cal, 2),
