@@ -228,3 +228,23 @@ def test_exact_steps_through_tied_rows(smp):
                     w["hist_len"], r24)
     assert (rdet["kept"] == 16).all()
     assert (rdet["rank"] == [pairs[i % len(pairs)][1] for i in range(rows)]).all()
+
+
+def test_eight_row_groups(smp):
+    """1000 rows: eight 128-row groups per tile (the last one partly padding),
+    one pass against two passes on the device for every row, the logits of the
+    first 128 rows against the oracle's head, and every row's draw against the
+    oracle sampler on those logits."""
+    rows = 1000
+    w = workloads.make_lmhead(rows=rows)
+    packed = pack(smp, w["q4"])
+    one = run(smp, packed, w["hidden"], w["hist"], w["hist_len"], w["random_24"], keep=False)
+    two = run(smp, packed, w["hidden"], w["hist"], w["hist_len"], w["random_24"], keep=True)
+    packed.free()
+    assert_rows_equal(*one[:3], *two[:3])
+    glog = two[3]
+    rlog = o.lmhead_logits(w["hidden"][:128], w["q4"], V, HID, threads=16)
+    assert (glog[:128] == rlog).all()
+    rtok, rdet, rerr, _ = o.sample_batch(glog, w["hist"], w["hist_len"], w["random_24"],
+                                         threads=16)
+    assert_rows_equal(*one[:3], rtok, rdet, rerr)
