@@ -180,18 +180,20 @@ typedef struct pb_context pb_context;
 uint32_t pb_context_create(int device, pb_context **out);
 void pb_context_destroy(pb_context *ctx);
 
-/* Sizes the context's workspace for batched calls of up to `rows` rows:
- * the sampler's slice workspace under the context's current slice plan
+/* Sizes the context's workspace for batched calls of up to `rows` rows: the
+ * sampler's slice workspace under the context's current slice plan
  * (pb_context_set_segments), and, when cols > 0, the fused LM head's
- * workspace for hidden states of up to `cols` columns (either head format,
- * logits included).  Allocates only when the workspace grows; never shrinks
- * it.  A workspace it outgrows stays allocated until pb_context_destroy, so
- * launches already enqueued and HIP graphs captured before the growth keep
- * valid memory (they keep using the old workspace).  Call it at set-up: the
- * batched entry points below never allocate, never wait, and return
- * PB_CAPACITY (needed/available = workspace bytes) when a call needs more
- * than was reserved, so a reserved context's calls can be captured in a HIP
- * graph. */
+ * workspace for hidden states of up to `cols` columns (either head format;
+ * logits only for the steps of up to 64 rows that keep them there, since a
+ * wider step without a logits buffer runs in one pass and keeps none: 40.2 MB
+ * at 256 rows of 896 columns).  Allocates only when the workspace grows; never
+ * shrinks it.  A workspace it outgrows stays allocated until
+ * pb_context_destroy, so launches already enqueued and HIP graphs captured
+ * before the growth keep valid memory (they keep using the old
+ * workspace).  Call it at set-up: the batched entry points below never
+ * allocate, never wait, and return PB_CAPACITY (needed/available = workspace
+ * bytes) when a call needs more than was reserved, so a reserved context's
+ * calls can be captured in a HIP graph. */
 uint32_t pb_context_reserve(pb_context *ctx, uint32_t rows, size_t cols, pb_inference_error *err);
 
 /* Threading and streams: one context's batched calls share its workspace.

@@ -182,6 +182,17 @@ static LmLayout lm_layout(uint32_t rows, size_t cols, bool with_logits) {
 static size_t lm_workspace_bytes(uint32_t rows, size_t cols, bool with_logits) {
   return lm_layout(rows, cols, with_logits).total;
 }
+// Workspace that every step of up to `rows` rows fits in: the logits only
+// for the narrow steps (up to kNarrowRows rows without a logits buffer from
+// the caller), which keep them there; a wider step keeps none (one pass) and
+// any step given a logits buffer writes the caller's.  At 256 rows of width
+// 896 that is 40.2 MB instead of 160.7 MB.
+static size_t lm_reserve_bytes(uint32_t rows, size_t cols) {
+  const size_t wide = lm_workspace_bytes(rows, cols, false);
+  const size_t narrow =
+      lm_workspace_bytes(rows < pb::kNarrowRows ? rows : pb::kNarrowRows, cols, true);
+  return wide > narrow ? wide : narrow;
+}
 
 static void free_staging(pb_context* ctx) {
   if (ctx->d_in) (void)hipFree(ctx->d_in);
@@ -363,8 +374,7 @@ uint32_t pb_context_reserve(pb_context* ctx, uint32_t rows, size_t cols, pb_infe
   hipError_t e = grow_device(&ctx->d_work, &ctx->list_bytes,
                              sample_workspace_bytes(rows, ctx->forced_segments), &ctx->retired);
   if (e == hipSuccess && cols != 0 && rows != 0)
-    e = grow_device(&ctx->d_lm, &ctx->lm_bytes, lm_workspace_bytes(rows, cols, true),
-                    &ctx->retired);
+    e = grow_device(&ctx->d_lm, &ctx->lm_bytes, lm_reserve_bytes(rows, cols), &ctx->retired);
   return e == hipSuccess ? PB_OK : device_error(err, e);
 }
 

@@ -248,3 +248,27 @@ def test_eight_row_groups(smp):
     rtok, rdet, rerr, _ = o.sample_batch(glog, w["hist"], w["hist_len"], w["random_24"],
                                          threads=16)
     assert_rows_equal(*one[:3], rtok, rdet, rerr)
+
+
+def test_reserve_keeps_logits_only_for_narrow_steps(base):
+    """A context reserved for 256 rows of width 896 holds workspace logits for
+    64 rows only, the narrow steps that keep them there: 40.2 MB for the LM
+    head rather than 160.7 MB with logits for every row.  Every step of up to
+    256 rows runs in it: 64 rows with the workspace's logits, 256 rows in one
+    pass and 256 rows with the caller's logits, each against the oracle."""
+    import torch
+
+    b = s.BatchSampler(0)
+    try:
+        torch.cuda.synchronize()
+        free0 = torch.cuda.mem_get_info(0)[0]
+        b.reserve(256, HID)
+        torch.cuda.synchronize()
+        used = free0 - torch.cuda.mem_get_info(0)[0]
+        assert used < 64 << 20, used
+        w = base
+        for rows in (64, 256):
+            check(b, w["q4"], w["hidden"][:rows], w["hist"][:rows], w["hist_len"][:rows],
+                  w["random_24"][:rows])
+    finally:
+        b.close()
