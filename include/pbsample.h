@@ -183,14 +183,14 @@ void pb_context_destroy(pb_context *ctx);
 /* Sizes the context's workspace for batched calls of up to `rows` rows: the
  * sampler's slice workspace under the context's current slice plan
  * (pb_context_set_segments), and, when cols > 0, the fused LM head's
- * workspace for hidden states of up to `cols` columns (either head format;
- * logits only for the steps of up to 64 rows that keep them there, since a
- * wider step without a logits buffer runs in one pass and keeps none: 40.2 MB
- * at 256 rows of 896 columns).  Allocates only when the workspace grows; never
- * shrinks it.  A workspace it outgrows stays allocated until
- * pb_context_destroy, so launches already enqueued and HIP graphs captured
- * before the growth keep valid memory (they keep using the old
- * workspace).  Call it at set-up: the batched entry points below never
+ * workspace for hidden states of up to `cols` columns (either head format,
+ * rows <= PB_LMHEAD_MAX_ROWS; logits only for the steps of up to 64 rows that
+ * keep them there, since a wider step without a logits buffer runs in one
+ * pass and keeps none: 40.2 MB at 256 rows of 896 columns).  Allocates only
+ * when the workspace grows; never shrinks it.  A workspace it outgrows stays
+ * allocated until pb_context_destroy, so launches already enqueued and HIP
+ * graphs captured before the growth keep valid memory (they keep using the
+ * old workspace).  Call it at set-up: the batched entry points below never
  * allocate, never wait, and return PB_CAPACITY (needed/available = workspace
  * bytes) when a call needs more than was reserved, so a reserved context's
  * calls can be captured in a HIP graph. */
@@ -270,6 +270,12 @@ uint32_t pb_sample_batch_inplace(pb_context *ctx, uint32_t *d_logits, size_t voc
  * The logits are bit-identical to the reference's Q4 head (int8 MFMA for the
  * exact block dots, the reference's per-block binary32 epilogue in order). */
 
+/* Largest batch of one LM-head call (either format) and of an LM-head
+ * reservation: the kernels address the quantised activations (at most
+ * 64 blocks x 32 bytes per row) with 32-bit offsets.  More rows are refused
+ * with PB_CAPACITY (needed = this limit, available = rows). */
+#define PB_LMHEAD_MAX_ROWS 262144u
+
 /* Bytes of the device layout of a Q4_0 head: the source size (rows * cols /
  * 32 blocks of 18 bytes) plus one flag word per 64-id tile. */
 size_t pb_lmhead_packed_bytes(size_t vocab, size_t cols);
@@ -297,7 +303,7 @@ uint32_t pb_lmhead_pack_q4_0(const uint8_t *d_q4, size_t vocab, size_t cols, uin
  * to 64 rows the logits go through the context's workspace.  Per-row outputs
  * and error records as pb_sample_batch (non-finite logit, bad history id).
  * Needs a context reserved (pb_context_reserve) for at least `rows` rows and
- * `cols` columns. */
+ * `cols` columns, and rows <= PB_LMHEAD_MAX_ROWS. */
 uint32_t pb_lmhead_sample_batch(pb_context *ctx, const uint8_t *d_packed, size_t packed_bytes,
                                 size_t vocab, size_t cols, const uint32_t *d_hidden, uint32_t rows,
                                 const uint32_t *d_hist, size_t hist_ld,

@@ -369,6 +369,10 @@ uint32_t pb_context_reserve(pb_context* ctx, uint32_t rows, size_t cols, pb_infe
     set_error(err, PB_CAPACITY, PB_DOMAIN_NONE, 32, cols, PB_FIELD_BYTES, 4);
     return PB_CAPACITY;
   }
+  if (cols != 0 && rows > PB_LMHEAD_MAX_ROWS) {
+    set_error(err, PB_CAPACITY, PB_DOMAIN_NONE, PB_LMHEAD_MAX_ROWS, rows, PB_FIELD_BYTES, 8);
+    return PB_CAPACITY;
+  }
   std::lock_guard<std::mutex> lock(ctx->mu);
   DeviceGuard guard(ctx->device);
   hipError_t e = grow_device(&ctx->d_work, &ctx->list_bytes,
@@ -699,6 +703,11 @@ static uint32_t enqueue_lmhead(pb_context* ctx, const uint8_t* d_packed, size_t 
     return PB_ALIGNMENT;
   }
   if (rows == 0) return PB_OK;
+  // the kernels' 32-bit offsets into the quantised activations
+  if (rows > PB_LMHEAD_MAX_ROWS) {
+    set_error(err, PB_CAPACITY, PB_DOMAIN_NONE, PB_LMHEAD_MAX_ROWS, rows, PB_FIELD_BYTES, 8);
+    return PB_CAPACITY;
+  }
   if (d_packed == nullptr || d_hidden == nullptr || d_random_24 == nullptr ||
       d_token == nullptr || (d_hist_len != nullptr && d_hist == nullptr)) {
     set_error(err, PB_CAPACITY, PB_DOMAIN_ARGMAX, 1, 0, PB_FIELD_BYTES, 3);
@@ -1020,7 +1029,9 @@ uint32_t pb_sample_token_with_repetition(uint32_t* logits, size_t logits_len,
     return row_err.status;
   }
   // success: publish the in-place penalty, the cleared scratch and the draw
-  for (size_t q = 0; q < tokens_len; ++q) logits[tokens[q]] = ctx->h_gather[q];
+  // (a NULL history is an empty one, as in run_single_row)
+  if (tokens != nullptr)
+    for (size_t q = 0; q < tokens_len; ++q) logits[tokens[q]] = ctx->h_gather[q];
   if (seen_dirty && tokens != nullptr && tokens_len > 0) memcpy(seen, ctx->h_seen, PB_SEEN_BYTES);
   *state = next;
   *out_token = *ctx->h_token;

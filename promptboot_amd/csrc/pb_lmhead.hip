@@ -597,8 +597,9 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(4)
   // The operands are buffer loads: a lane's byte offset is fixed, the block's
   // offset is a scalar, so a load costs no VALU address arithmetic (three to
   // five instructions per block otherwise).  Widths of at most 2048 keep the
-  // packed head under 330 MB, and the activations take blocks * rows_pad * 32
-  // bytes, far below 4 GB for any workspace that holds the rows' logits.
+  // packed head under 330 MB, and the activations of at most
+  // PB_LMHEAD_MAX_ROWS rows (the host refuses more) take blocks * rows_pad * 32
+  // <= 512 MB, so every offset and resource size fits in 31 bits.
   const uint32_t w_stride = kTilesPerRow * kTile;  // bytes per block
   const uint32_t w_off = tile * kTile + 16u * kWords * lane;
   const uint32_t a_stride = p.rows_pad * 32u;  // bytes per block

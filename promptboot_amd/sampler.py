@@ -35,6 +35,7 @@ from . import hip
 
 VOCAB = 151_936
 TILE_SELECT_ROWS = 192  # PB_TILE_SELECT_ROWS: batches up to it take the tile selection
+LMHEAD_MAX_ROWS = 262_144  # PB_LMHEAD_MAX_ROWS: largest batch of one LM-head call
 TOP_K = 20
 SEEN_BYTES = (VOCAB + 7) // 8
 NO_TOKEN = 0xFFFF_FFFF

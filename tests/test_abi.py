@@ -34,6 +34,18 @@ def test_library_exports_every_declared_function():
         assert getattr(lib, n) is not None
 
 
+def test_header_constants_match_the_binding():
+    """Every numeric #define of the header that the binding mirrors has the
+    same value there."""
+    defines = {m[0]: int(m[1], 0) for m in
+               re.findall(r"^#define PB_([A-Z0-9_]+) (0x[0-9a-fA-F]+|[0-9]+)u", HEADER.read_text(),
+                          flags=re.M)}
+    mirrored = {k: getattr(s, k) for k in defines if hasattr(s, k)}
+    assert {"VOCAB", "TOP_K", "TILE_SELECT_ROWS", "LMHEAD_MAX_ROWS", "IM_END",
+            "END_OF_TEXT"} <= set(mirrored)
+    assert mirrored == {k: defines[k] for k in mirrored}
+
+
 def test_one_hip_runtime_is_mapped():
     """The binding opens the library after torch, so torch's bundled
     libamdhip64 serves both and the process holds a single HIP runtime."""
@@ -193,8 +205,9 @@ def test_lmhead_pack_argument_errors_need_no_device():
 
 def test_lmhead_and_reserve_argument_errors_need_no_device():
     """A head packed for another width or format is refused by its size
-    before any device work (the C calls take the packed length), and so is a
-    reservation for a width the head cannot take."""
+    before any device work (the C calls take the packed length), and so are a
+    reservation for a width the head cannot take and a batch or reservation
+    above PB_LMHEAD_MAX_ROWS rows."""
     import ctypes
 
     e = s._Error()
@@ -215,3 +228,12 @@ def test_lmhead_and_reserve_argument_errors_need_no_device():
     assert st == s.CAPACITY and (e.needed, e.available) == (32, 900)
     st = s.lib().pb_context_reserve(None, 256, 4096, ctypes.byref(e))
     assert st == s.CAPACITY and e.available == 4096
+    # more rows than the LM head's 32-bit activation offsets allow
+    over = s.LMHEAD_MAX_ROWS + 1
+    want_err = (s.LMHEAD_MAX_ROWS, over, (4 << 32) | 8)
+    for fn, size in ((s.lib().pb_lmhead_sample_batch, q4), (s.lib().pb_lmhead_q8_sample_batch, q8)):
+        st = fn(None, fake, size, s.VOCAB, 896, fake, over, None, 0, None, fake, fake, None, None,
+                None, None, ctypes.byref(e))
+        assert st == s.CAPACITY and (e.needed, e.available, e.detail) == want_err
+    st = s.lib().pb_context_reserve(None, over, 896, ctypes.byref(e))
+    assert st == s.CAPACITY and (e.needed, e.available, e.detail) == want_err
