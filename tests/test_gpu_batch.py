@@ -208,3 +208,21 @@ def test_tile_selection_on_padded_rows_and_an_odd_history_stride(sampler, rows):
     got = run_gpu(sampler, padded)
     assert_rows_equal(*got, *run_oracle(padded))
     assert (got[2]["status"] == 0).all()
+
+
+@pytest.mark.parametrize("name,rows,segments", [("small", 64, 0), ("flat", 256, 0), ("small", 64, 7)])
+def test_history_lengths_past_the_stride_are_clamped(sampler, name, rows, segments):
+    """A history length above hist_ld counts as hist_ld ids (the header's
+    contract for every batched entry point): lengths of hist_ld + 1, far past
+    it and 0xffffffff give the oracle's results on the clamped lengths, on the
+    tile selection, the one-slice plan and a forced seven-slice plan."""
+    w = workloads.make(name, rows=rows)
+    ld = w["hist"].shape[1]
+    long = w["hist_len"].copy()
+    long[0::3] = ld + 1
+    long[1::3] = ld + 12345
+    long[2] = 0xFFFFFFFF
+    got = run_gpu(sampler, dict(w, hist_len=long), segments=segments)
+    want = run_oracle(dict(w, hist_len=np.minimum(long, ld).astype(np.uint32)))
+    assert_rows_equal(*got, *want)
+    assert (got[2]["status"] == 0).all()

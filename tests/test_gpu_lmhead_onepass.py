@@ -272,3 +272,24 @@ def test_reserve_keeps_logits_only_for_narrow_steps(base):
                   w["random_24"][:rows])
     finally:
         b.close()
+
+
+@pytest.mark.parametrize("rows", [8, 70])
+def test_history_lengths_past_the_stride_are_clamped(smp, base, rows):
+    """The LM head's selection clamps a history length above hist_ld to
+    hist_ld, as the batched sampler does: the narrow step (8 rows) and the
+    one-pass step (70 rows) with lengths past the stride give the same records
+    as with the clamped lengths, which match the oracle."""
+    w = base
+    ld = w["hist"].shape[1]
+    long = w["hist_len"][:rows].copy()
+    long[0::2] = ld + 7
+    long[1] = 0xFFFFFFFF
+    clamped = np.minimum(long, ld).astype(np.uint32)
+    one, _ = check(smp, w["q4"], w["hidden"][:rows], w["hist"][:rows], clamped,
+                   w["random_24"][:rows])
+    packed = pack(smp, w["q4"])
+    got = run(smp, packed, w["hidden"][:rows], w["hist"][:rows], long, w["random_24"][:rows],
+              keep=False)
+    packed.free()
+    assert_rows_equal(*got[:3], *one[:3])
