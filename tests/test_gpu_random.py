@@ -24,11 +24,13 @@ pytestmark = pytest.mark.gpu
 V = s.VOCAB
 
 
-def random_case(seed: int) -> dict:
+def random_case(seed: int, rows: int | None = None) -> dict:
     """One random batch (numpy, host side): logits [B, ld] float32, history
-    [B, hist_ld] uint32 or None, lengths, uniforms and the slice plan."""
+    [B, hist_ld] uint32 or None, lengths, uniforms and the slice plan.  `rows`
+    replaces the drawn batch size (the other draws follow from the seed)."""
     rng = np.random.default_rng(seed)
     B = int(rng.choice([1, 2, 7, 33, 64, 65, 127, 191, 192, 193, 256, 300]))
+    B = B if rows is None else rows
     ld = V + int(rng.choice([0, 0, 4, 12]))
     kind = int(rng.integers(0, 6))
     shape = (B, V)
