@@ -227,3 +227,23 @@ def test_active_row_at_its_cap_is_not_sampled():
         finally:
             dec.close()
             smp.close()
+
+
+@pytest.mark.parametrize("seed,n", [(0, 3), (1, 40), (2, 193), (3, 230)])
+def test_random_decode_loops_match_the_oracle(seed, n):
+    """Seeded random decode batches in lockstep with the oracle's loop: batch
+    sizes either side of the tile selection's 192 rows, prompt lengths of 1 to
+    2,000 ids (a bad id in some), limits of 0 to 12 tokens, end of sequence
+    on either id after a random step, a non-finite logit at a random step,
+    and the automatic or a forced slice plan."""
+    rng = np.random.default_rng([seed, 31])
+    prompts = [workloads.zipf_ids(rng, int(k)) for k in rng.integers(1, 2001, n)]
+    for r in rng.choice(n, max(1, n // 20), replace=False):
+        prompts[r] = np.append(prompts[r], np.uint32(V + int(rng.integers(0, 99))))
+    seeds = [int(x) for x in rng.integers(0, 2**63, n)]
+    limits = [int(x) for x in rng.integers(0, 13, n)]
+    eos_after = [int(x) if x < 12 else None for x in rng.integers(0, 24, n)]
+    eos_ids = [s.IM_END if x else s.END_OF_TEXT for x in rng.integers(0, 2, n)]
+    nan_at = {int(r): int(rng.integers(0, 8)) for r in rng.choice(n, max(1, n // 25), replace=False)}
+    segments = int(rng.choice([0, 0, 1, 3]))
+    run_lockstep(prompts, seeds, limits, eos_after, eos_ids, nan_at, 14, segments)
