@@ -14,10 +14,11 @@ The printed JSON line also carries:
   roofline            the segment kernel's algorithmic HBM bytes per launch
                       over its average launch time (HIP events on the launch
                       stream) against the 8 TB/s MI355X peak; the read
-                      bandwidth a plain streaming read of the same number of
-                      bytes reaches on this device (the fastest shape of
-                      READ_SHAPES: contiguous ranges or grid-stride chunks,
-                      pb_device_read_probe / _grid_stride);
+                      bandwidth a plain streaming read of the batch's own
+                      logits, where they lie, reaches on this device (the
+                      fastest shape of READ_SHAPES: contiguous ranges or
+                      grid-stride chunks, pb_device_read_probe /
+                      _grid_stride);
                       and the HBM traffic measured by rocprofv3 counters,
                       taken from the committed summary only when that summary
                       names this very build (pb_version);
@@ -33,12 +34,12 @@ The printed JSON line also carries:
                       sub-cases and the boundary batch (draws exactly on a
                       step of the cumulative distribution), each timed and
                       checked against the oracle,
-                      with the read ceiling of the same byte count
-                      (as above) beside it;
+                      with the read ceiling of its own logits (as above)
+                      beside it;
   lmhead_fused        the fused Q4_0 LM head + sampler step (B=256);
   lmhead_q8_fused     the same with the Q8_0 head (the model's output head);
   lmhead_B1           one conversation's step (B=1) through each head,
-                      with a plain read of the same byte count beside it
+                      with a plain read of the packed head beside it
                       (read_ceiling_ms; frac_of_read_ceiling = that read's
                       time over the step's);
                       each LM-head leg also gives its step's HBM traffic
@@ -283,7 +284,8 @@ def cold_pass(smp, bufs: dict, sets: int, steps: int, warmup: int, stream) -> tu
 COLD_SETS = {1: 1024, 64: 16}
 
 
-def time_batch(smp, w: dict, steps: int, warmup: int, stream, cold_sets: int = 0) -> dict:
+def time_batch(smp, w: dict, steps: int, warmup: int, stream, cold_sets: int = 0,
+               ceiling: bool = False) -> dict:
     from promptboot_amd import hip
     from promptboot_amd import sampler as s
     from promptboot_amd import workloads
@@ -316,6 +318,8 @@ def time_batch(smp, w: dict, steps: int, warmup: int, stream, cold_sets: int = 0
            "path": ("tile selection" if not smp.segments and B <= s.TILE_SELECT_ROWS
                     else "slices"),
            "_tokens": tokens, "_detail": detail}
+    if ceiling:  # a plain read of the logits the step reads, where they lie
+        out["_ceiling"] = read_ceiling(alg, stream, src=logits)
     if cold_sets:
         bufs = dict(logits=logits, hist=hist, hl=hl, r24=r24, token=token)
         cold_ms, cold_wall = cold_pass(smp, bufs, cold_sets, steps, warmup, stream)
@@ -331,25 +335,36 @@ def time_batch(smp, w: dict, steps: int, warmup: int, stream, cold_sets: int = 0
 
 
 # Plain-read shapes timed for the read ceiling: (entry point, workgroups).
-READ_SHAPES = (("rows", 4096), ("ranges", 32768), ("grid_stride", 2048), ("grid_stride", 4096))
+READ_SHAPES = (("rows", 4096), ("ranges", 32768), ("grid_stride", 2048), ("grid_stride", 4096),
+               ("grid_stride", 8192), ("grid_stride", 16384))
 
 
-def read_ceiling(nbytes: int, stream, steps: int = 20) -> dict:
+def read_ceiling(nbytes: int, stream, steps: int = 20, src=None) -> dict:
     """Read bandwidth of a plain streaming read of `nbytes` (non-temporal
     16-byte loads, eight per thread in flight) in the shapes of READ_SHAPES:
     one contiguous range per workgroup over 4096 workgroups (the B=4096
     launch's grid) and over 32,768 (ranges of a few tens of KB, so the
     workgroups resident at once read a compact window of the buffer), and a
     grid-stride read (pb_device_read_probe_grid_stride: 32 KiB chunks, chunk
-    g + k x workgroups for workgroup g) over 2048 and 4096 workgroups.  The
-    fastest shape is the ceiling; every shape is reported."""
+    g + k x workgroups for workgroup g) over 2048 to 16,384 workgroups (the
+    larger grids keep more 32 KiB chunks in flight over a narrower window and
+    read fastest on MI355X).  The fastest shape is the ceiling; every shape
+    is reported.  With `src` (a device buffer) the probes read that buffer's
+    first min(nbytes, its size) bytes where they lie, the step's own input
+    (the logits matrix, the packed head): a fresh buffer allocated late in a
+    process that holds several GB measured up to 10 % slower in some shapes
+    than the same read of the step's input on the same device."""
     import ctypes
 
     from promptboot_amd import hip
     from promptboot_amd import sampler as s
 
-    words = nbytes // 16 * 4
-    buf = hip.DeviceArray(words, np.uint32)
+    if src is not None:
+        words = min(nbytes, src.nbytes) // 16 * 4
+        buf = src
+    else:
+        words = nbytes // 16 * 4
+        buf = hip.DeviceArray(words, np.uint32)
     out = hip.DeviceArray.zeros(32768, np.uint32)
     h = ctypes.c_void_p(hip.stream_handle(stream))
     shapes = {}
@@ -364,11 +379,13 @@ def read_ceiling(nbytes: int, stream, steps: int = 20) -> dict:
 
         settle(step)
         shapes[f"{kind}_{blocks}"] = event_pass(step, steps, stream)
-    buf.free()
+    if src is None:
+        buf.free()
     out.free()
     best = min(shapes, key=shapes.get)
     ms = shapes[best]
     return {"read_gbs": round(words * 4 / (ms / 1e3) / 1e9, 1), "bytes": words * 4,
+            "buffer": "the step's own input" if src is not None else "a fresh buffer",
             "launch_ms": round(ms, 4), "shape": best,
             "by_shape": {k: {"launch_ms": round(m, 4),
                              "read_gbs": round(words * 4 / (m / 1e3) / 1e9, 1)}
@@ -577,6 +594,10 @@ def time_lmhead(smp, steps: int, warmup: int, stream, q8: bool = False, rows: in
         two_pass = {"launch_ms": round(event_pass(step2, steps, stream), 4),
                     "ms_per_step": round(wall_pass(step2, steps) / steps * 1e3, 4)}
         kept.free()
+    alg = workloads.lmhead_algorithmic_bytes(B, w["hist_len"], q8=q8)
+    # one conversation's step streams the head once: beside it, a plain read of
+    # the packed head where it lies
+    ceiling = read_ceiling(alg, stream, src=packed) if B == 1 else None
     packed.free()
     # parity on a bounded sample: the oracle's head and sampler on the first
     # rows (bit-exact logits; token agreement on non-boundary rows)
@@ -598,12 +619,8 @@ def time_lmhead(smp, steps: int, warmup: int, stream, q8: bool = False, rows: in
     # w_scale, * a_scale, + total (the conversion folds into the first).  Q8_0:
     # the conversion, w_scale * a_scale, the product and the sum.
     epilogue = (4.0 if q8 else 3.0) * B * workloads.VOCAB * (workloads.HIDDEN // 32)
-    alg = workloads.lmhead_algorithmic_bytes(B, w["hist_len"], q8=q8)
-    # one conversation's step streams the head once: beside it, a plain read of
-    # the same number of bytes on this device
     extra = {}
-    if B == 1:
-        ceiling = read_ceiling(alg, stream)
+    if ceiling is not None:
         extra = {"read_ceiling_gbs": ceiling["read_gbs"],
                  "read_ceiling_ms": ceiling["launch_ms"],
                  "frac_of_read_ceiling": round(ceiling["launch_ms"] / step_ms, 4)}
@@ -678,8 +695,8 @@ def time_adversarial(smp, steps: int, warmup: int, threads: int, stream) -> dict
     for name in ADVERSARIAL:
         log(f"adversarial {name}: generating, timing, checking")
         w = workloads.make(name)
-        r = time_batch(smp, w, steps, warmup, stream)
-        ceiling = read_ceiling(r["alg_bytes"], stream)
+        r = time_batch(smp, w, steps, warmup, stream, ceiling=True)
+        ceiling = r["_ceiling"]
         rtok, rdet, _, _ = o.sample_batch(w["logits"], w["hist"], w["hist_len"],
                                           w["random_24"], threads=threads)
         out[name] = {"rows": int(len(rtok)), "rows_per_s": round(r["rows_per_s"], 1),
@@ -930,10 +947,10 @@ def main() -> int:
     for B in batches:
         log(f"timing B={B}")
         results[B] = time_batch(smp, work[B], args.steps, args.warmup, stream,
-                                cold_sets=COLD_SETS.get(B, 0) if not args.no_cold else 0)
+                                cold_sets=COLD_SETS.get(B, 0) if not args.no_cold else 0,
+                                ceiling=B == head)
     main_res = results[head]
-    log("timing the read ceiling of the sampler's load pattern")
-    ceiling = read_ceiling(main_res["alg_bytes"], stream)
+    ceiling = main_res["_ceiling"]
     threads = min(16, len(os.sched_getaffinity(0)))
     adversarial = None
     if not args.no_adversarial:

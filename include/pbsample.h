@@ -449,15 +449,16 @@ uint32_t pb_device_mfma_selftest(int32_t *d_out, void *stream);
 
 /* Read-only stream probe (diagnostic, no reference counterpart): `blocks`
  * workgroups read the n_words words at d_in (16-byte aligned) with the
- * sampler's load pattern and XOR what they read into d_out[0 .. blocks).
- * Timing it gives the read bandwidth the sampler's stream can reach. */
+ * sampler's load pattern, workgroup g a contiguous run of ceil(n_words / 4 /
+ * blocks) 16-byte groups, and d_out[g] receives the XOR of the words it
+ * read.  Timing it gives the read bandwidth the sampler's stream can reach. */
 uint32_t pb_device_read_probe(const uint32_t *d_in, size_t n_words, uint32_t *d_out,
                               uint32_t blocks, void *stream);
 /* The same read in grid-stride order (diagnostic, no reference counterpart):
  * the buffer is cut into 32 KiB chunks and workgroup g reads chunks g,
- * g + blocks, ..., so the workgroups resident at once read one compact
- * window that moves through the buffer (the fastest plain read pattern
- * measured on MI355X). */
+ * g + blocks, ... (d_out[g] receives the XOR of their words), so the
+ * workgroups resident at once read one compact window that moves through the
+ * buffer (the fastest plain read pattern measured on MI355X). */
 uint32_t pb_device_read_probe_grid_stride(const uint32_t *d_in, size_t n_words, uint32_t *d_out,
                                           uint32_t blocks, void *stream);
 
