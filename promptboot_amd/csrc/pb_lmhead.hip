@@ -1820,12 +1820,27 @@ __global__ __launch_bounds__(kSelectThreads) void lm_select_kernel(LmParams p, R
   // is penalised once): written by the waves other than wave 0 once they have
   // no other work.  They do not depend on the draw; the caller applies them
   // only when the row succeeded.  Ids out of range are skipped (the row fails).
+  // Eight positions per thread go out per batch, their ids and values loaded
+  // first (clamped, unconditional): the caller's copy lives in mapped host
+  // memory, and each wait for a load also waits for the stores before it, so
+  // a store per position made every position wait for a write across PCIe
+  // (single-row drop-in with 32,000 history ids: 117 -> 92 us per call).
   auto gather_history = [&]() {
     if (kRecompute || rp.gather == nullptr || len == 0) return;
     uint32_t* out = rp.gather + (size_t)row * rp.hist_ld;
-    for (uint32_t q = tid - 64u; q < len; q += kSelectThreads - 64u) {
-      const uint32_t id = hrow[q];
-      if (id < kVocab) out[q] = penalize_bits(lrow[id]);
+    constexpr uint32_t kThreads = kSelectThreads - 64u;
+    constexpr uint32_t kBatch = 8;
+    for (uint32_t q0 = tid - 64u; q0 < len; q0 += kBatch * kThreads) {
+      uint32_t id[kBatch], x[kBatch];
+#pragma unroll
+      for (uint32_t u = 0; u < kBatch; ++u) id[u] = hrow[min(q0 + u * kThreads, len - 1u)];
+#pragma unroll
+      for (uint32_t u = 0; u < kBatch; ++u) x[u] = lrow[min(id[u], kVocab - 1u)];
+#pragma unroll
+      for (uint32_t u = 0; u < kBatch; ++u) {
+        const uint32_t q = q0 + u * kThreads;
+        if (q < len && id[u] < kVocab) out[q] = penalize_bits(x[u]);
+      }
     }
   };
   if (uniform(round2) != 0u) {
