@@ -439,13 +439,19 @@ def time_production(stream) -> dict:
             "token": 9707}
 
 
+# History lengths (Zipf(1.1) ids) of the drop-in's longer-history timings.
+DROPIN_HISTORIES = (1000, 3000, 10000, 32000)
+
+
 def time_host_buffers(smp, w1: dict, w: dict, stream, calls: int = 200, steps: int = 5) -> dict:
     """Rates with the inputs in host memory, so PCIe is included (never the
     headline value, which is timed with the inputs resident in HBM):
 
       dropin    pb_sample_token_with_repetition on host buffers, as the
                 reference's call sites pass them (one row, its history as the
-                token list): wall time per call;
+                token list): wall time per call; also with longer Zipf(1.1)
+                histories (the REPL passes its whole working context, up to
+                32,767 ids): DROPIN_HISTORIES;
       batch     the B=4096 batch copied from pinned host memory every step
                 (logits, the padded history matrix, lengths, uniforms), then
                 pb_sample_batch, then the tokens copied back.
@@ -465,6 +471,20 @@ def time_host_buffers(smp, w1: dict, w: dict, stream, calls: int = 200, steps: i
         if i >= 10:
             times.append(time.perf_counter() - t0)
     times = np.array(times) * 1e6
+    from promptboot_amd import workloads
+
+    rng = np.random.default_rng(5)
+    by_history = {}
+    for L in DROPIN_HISTORIES:
+        hist = workloads.zipf_ids(rng, L).astype(np.uint32)
+        t = []
+        for i in range(60):
+            row = row0.copy()
+            t0 = time.perf_counter()
+            s.sample_token_with_repetition(row, hist, seen, state)
+            if i >= 10:
+                t.append(time.perf_counter() - t0)
+        by_history[str(L)] = round(float(np.median(t)) * 1e6, 1)
 
     B = w["logits"].shape[0]
     names = ("logits", "hist", "hist_len", "random_24")
@@ -494,7 +514,8 @@ def time_host_buffers(smp, w1: dict, w: dict, stream, calls: int = 200, steps: i
                                    "p90": round(float(np.percentile(times, 90)), 1),
                                    "calls": calls,
                                    "row": "B=1 workload row 0, history of "
-                                          f"{int(w1['hist_len'][0])} ids"},
+                                          f"{int(w1['hist_len'][0])} ids",
+                                   "by_history_ids": by_history},
             "batch_pcie_inclusive": {"rows": B, "rows_per_s": round(B / sec, 1),
                                      "ms_per_step": round(sec * 1e3, 3),
                                      "h2d_bytes_per_step": h2d,
