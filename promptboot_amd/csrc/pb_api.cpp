@@ -353,6 +353,9 @@ uint32_t pb_context_create(int device, pb_context** out) {
   // the device address of pb_sample_batch_noalloc's static scratch, once per device
   void* scratch = nullptr;
   if (e == hipSuccess) e = pb::static_scratch_address(device, &scratch);
+  // the batch size from which rows run longest history first, once per device
+  uint32_t resident = 0;
+  if (e == hipSuccess) e = pb::resident_rows(device, &resident);
   if (e != hipSuccess) {
     release(ctx);
     return PB_DEVICE;
@@ -510,6 +513,7 @@ static uint32_t enqueue_sample_in(int device, uint32_t forced_segments, void* wo
     p.part_meta = reinterpret_cast<uint32_t*>(base + slots * PB_TOP_K * 8);
   }
   DeviceGuard guard(device);
+  pb::plan_row_order(device, &p);
   hipError_t e = pb::launch_sample(p, stream);
   if (e != hipSuccess) return device_error(err, e);
   return PB_OK;

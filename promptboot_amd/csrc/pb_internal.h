@@ -29,6 +29,11 @@ struct RowParams {
   uint32_t segs;           // slices per row
   uint32_t seg_f4;         // float4 per slice, multiple of 8
   uint32_t hist_vec4;      // history rows are 16-byte aligned: load 4 ids at a time
+  // One slice per row only (0: rows in batch order).  Workgroups from
+  // order_from on take the remaining rows longest history first, ranked in
+  // groups of kOrderGroup rows by min(length, hist_ld) >> order_shift.
+  uint32_t order_from;
+  uint32_t order_shift;
   // Decode-loop mode (null row_state: plain sampling).  Rows not in
   // PB_ROW_ACTIVE are skipped; a sampled token is appended to the row's
   // context (hist_out / hist_len_out alias hist / hist_len) and the row
@@ -110,6 +115,14 @@ hipError_t launch_mfma_selftest(int32_t* out, hipStream_t stream);
 uint32_t segments_for_rows(uint32_t rows);
 // forced_segments == 0 picks segments_for_rows(rows).
 void plan_segments(uint32_t rows, uint32_t forced_segments, uint32_t* segs, uint32_t* seg_f4);
+// Rows ranked together by history length (one slice per row).
+constexpr uint32_t kOrderGroup = 4096;
+// Workgroups of segment_kernel<.., true> that `device` holds at once, looked
+// up once per device (the first call on a device queries the runtime).
+hipError_t resident_rows(int device, uint32_t* out);
+// Sets p->order_from and p->order_shift for a one-slice plan on `device`:
+// rows past the first residency round run longest history first.
+void plan_row_order(int device, RowParams* p);
 hipError_t launch_sample(const RowParams& p, hipStream_t stream);
 hipError_t launch_writeback(const WritebackParams& p, hipStream_t stream);
 hipError_t launch_probe(int which, const uint32_t* in, uint32_t* out, size_t n,

@@ -72,6 +72,37 @@ def test_large_rows_with_full_context_histories(sampler):
     assert_rows_equal(*got, *want)
 
 
+def test_rows_past_the_first_residency_round_run_longest_history_first(sampler):
+    """Past the workgroups the GPU holds at once (1,024 on MI355X), one-slice
+    batches take the remaining rows longest history first, ranked in groups of
+    4,096 rows.  5,300 rows with lengths spread over 0..32,768 (some zero, some
+    past the stride and clamped) span two such groups; every row is sampled
+    exactly once and bit-exact against the oracle (the outputs start as 0xff
+    bytes, so a row left out or sampled into the wrong slot shows)."""
+    import torch
+
+    B, L = 5300, 32768
+    rng = np.random.default_rng(20260101)
+    logits = rng.standard_normal((B, V), dtype=np.float32) * np.float32(2.5)
+    hist = rng.integers(0, V, (B, L), dtype=np.uint32)
+    hl = rng.integers(0, L + 1, B).astype(np.uint32)
+    hl[::89] = 0
+    hl[5::97] = L + 7
+    r24 = rng.integers(0, 1 << 24, B).astype(np.uint32)
+    token = torch.full((B,), -1, dtype=torch.int32, device="cuda:0")
+    det = torch.full((B, s.DETAIL_DTYPE.itemsize // 4), -1, dtype=torch.int32, device="cuda:0")
+    err = torch.full((B, s.ERROR_DTYPE.itemsize // 4), -1, dtype=torch.int32, device="cuda:0")
+    sampler.sample(to_dev(logits), to_dev(r24), to_dev(hist), to_dev(hl), token=token, detail=det,
+                   err=err)
+    torch.cuda.synchronize()
+    got = (token.cpu().numpy().view(np.uint32), det.cpu().numpy().view(s.DETAIL_DTYPE).reshape(B),
+           err.cpu().numpy().view(s.ERROR_DTYPE).reshape(B))
+    tok, rdet, rerr, _ = o.sample_batch(logits, hist, np.minimum(hl, L).astype(np.uint32), r24,
+                                        threads=16)
+    assert_rows_equal(*got, tok, rdet, rerr)
+    assert (got[2]["status"] == 0).all()
+
+
 @pytest.mark.parametrize("name,rows", [("large", 192), ("ties", 128), ("flat", 128),
                                        ("dominant", 64)])
 def test_small_batches_take_the_tile_selection(sampler, name, rows):
