@@ -2126,8 +2126,17 @@ hipError_t launch_tile_select(const LmParams& p, const RowParams& rp, hipStream_
   (void)hipGetLastError();  // report only this call's launch errors
   // Logits in HBM: two loads per thread, 75 workgroups per row (B = 1, 16,
   // 64, 192 steps 0.6, 0.6, 0.4, 0.2 us shorter than with four; one load or
-  // eight were slower).  Logits in pinned host memory: four, 38 workgroups.
-  if (p.logits_copy == nullptr) {
+  // eight were slower from 16 rows up).  Up to three rows, where 75
+  // workgroups per row leave CUs idle, one load, 149 workgroups per row:
+  // B = 1, 2, 3 cold steps 7.8, 8.2, 8.3 -> 7.6, 7.9, 8.1 us (wall, one box;
+  // 64 or 128 threads per workgroup measured the same).  Logits in pinned
+  // host memory: four, 38 workgroups.
+  if (p.logits_copy == nullptr && p.rows <= 3u) {
+    constexpr uint32_t kGroupTiles = 16u;
+    hipLaunchKernelGGL(tile_words_kernel<1>,
+                       dim3((kTilesPerRow + kGroupTiles - 1) / kGroupTiles, p.rows), dim3(256), 0,
+                       stream, p);
+  } else if (p.logits_copy == nullptr) {
     constexpr uint32_t kGroupTiles = 16u * 2u;
     hipLaunchKernelGGL(tile_words_kernel<2>,
                        dim3((kTilesPerRow + kGroupTiles - 1) / kGroupTiles, p.rows), dim3(256), 0,
