@@ -45,6 +45,9 @@ The printed JSON line also carries:
                       each LM-head leg also gives its step's HBM traffic
                       (the per-kernel counter figures of the committed
                       summary, same-build only) over its algorithmic bytes;
+  by_batch.1.by_history_ids
+                      the B=1 step (inputs in HBM) with Zipf histories of
+                      1,000 to 32,000 ids, wall time per step;
   host_buffers        PCIe-inclusive rates: the single-row drop-in on host
                       buffers, and the B=4096 batch copied from pinned host
                       memory every step (not the headline value).
@@ -441,6 +444,37 @@ def time_production(stream) -> dict:
 
 # History lengths (Zipf(1.1) ids) of the drop-in's longer-history timings.
 DROPIN_HISTORIES = (1000, 3000, 10000, 32000)
+
+
+def time_device_histories(smp, w1: dict, stream, steps: int = 200) -> dict:
+    """One conversation's step with the inputs resident in HBM and longer
+    histories (the REPL passes its whole working context, up to 32,767 ids):
+    row 0 of the B=1 workload with a Zipf(1.1) history of L ids for each L in
+    DROPIN_HISTORIES, bound pb_sample_batch steps back to back (wall time per
+    step, after the settle phase), each token checked against the oracle."""
+    from oracle import oracle as o
+    from promptboot_amd import hip
+    from promptboot_amd import workloads
+
+    rng = np.random.default_rng(6)
+    logits = np.ascontiguousarray(w1["logits"][:1])
+    r24 = np.ascontiguousarray(w1["random_24"][:1])
+    out = {}
+    for L in DROPIN_HISTORIES:
+        hist = np.zeros((1, 32768), np.uint32)
+        hist[0, :L] = workloads.zipf_ids(rng, L)
+        hl = np.array([L], np.uint32)
+        d = [hip.DeviceArray.from_numpy(a) for a in (logits, hist, hl, r24)]
+        token = hip.DeviceArray(1, np.uint32)
+        step = smp.bind_sample(d[0], d[3], d[1], d[2], token=token, stream=stream)
+        settle(step)
+        us = wall_pass(step, steps) / steps * 1e6
+        want = o.sample_batch(logits, hist, hl, r24)[0]
+        out[str(L)] = {"us_per_step": round(us, 2),
+                       "token_agrees": bool((token.numpy() == want).all())}
+        for a in d + [token]:
+            a.free()
+    return out
 
 
 def time_host_buffers(smp, w1: dict, w: dict, stream, calls: int = 200, steps: int = 5) -> dict:
@@ -994,6 +1028,10 @@ def main() -> int:
     if not args.no_host_buffers and 1 in work and 4096 in work:
         log("timing with the inputs in host memory (PCIe included)")
         host_buffers = time_host_buffers(smp, work[1], work[4096], stream)
+    device_histories = None
+    if 1 in work:
+        log("timing one conversation's step with longer histories (inputs in HBM)")
+        device_histories = time_device_histories(smp, work[1], stream)
     smp.close()
 
     w = work[head]
@@ -1044,6 +1082,8 @@ def main() -> int:
                              "inputs": "the same inputs every step (cache-resident)"}
         else:
             entry["inputs"] = "one input set, larger than the 256 MB last-level cache"
+        if B == 1 and device_histories is not None:
+            entry["by_history_ids"] = device_histories
         by_batch[str(B)] = entry
     out = {
         "metric": METRIC,

@@ -1200,6 +1200,7 @@ constexpr int kRecomputeQ4 = 1;
 constexpr int kRecomputeQ8 = 2;
 constexpr uint32_t kTileWaves = 4;                      // waves that read the tile words
 constexpr uint32_t kHistWaves = 4;                      // waves that build the history bitmap
+constexpr uint32_t kHistGroup = 2;                      // later history batches requested together
 constexpr uint32_t kSelectThreads = 64u * (kTileWaves + kHistWaves);
 constexpr int kTileKeys = (kTilesPerRow + 63) / 64;    // 38 tile words per lane
 constexpr int kWaveKeys = (kTileKeys + (int)kTileWaves - 1) / (int)kTileWaves;  // 10 per tile wave
@@ -1343,13 +1344,14 @@ __global__ __launch_bounds__(kSelectThreads) void lm_select_kernel(LmParams p, R
   }
   // History threads: each requests its first uint4 (or word) of the row,
   // clamped to the row's capacity (hist_ld ids are readable per row); the
-  // other three (seven) follow once the length shows that the row needs
-  // them.
+  // other three (seven) of its first batch, and its second batch of four,
+  // follow once the length shows that the row needs them.
   const uint32_t ht = tid - 64u * kTileWaves;
   constexpr uint32_t kHistThreads = 64u * kHistWaves;
   const bool has_hist = rp.hist != nullptr && rp.hist_len != nullptr && rp.hist_ld != 0;
   const uint32_t* hbase = has_hist ? rp.hist + (size_t)row * rp.hist_ld : nullptr;
   v4u hv[4] = {};
+  v4u hb[4] = {};  // the second batch of a history longer than the first
   uint32_t hs[8] = {};
   if (!tile_wave && has_hist) {
     if (rp.hist_vec4)
@@ -1397,6 +1399,10 @@ __global__ __launch_bounds__(kSelectThreads) void lm_select_kernel(LmParams p, R
     if (rp.hist_vec4) {
 #pragma unroll
       for (uint32_t u = 1; u < 4; ++u) hv[u] = h4[min(ht + u * kHistThreads, n4 - 1u)];
+      if (uniform(n4) > 4u * kHistThreads) {
+#pragma unroll
+        for (uint32_t u = 0; u < 4; ++u) hb[u] = h4[min(ht + (4u + u) * kHistThreads, n4 - 1u)];
+      }
     } else {
 #pragma unroll
       for (uint32_t u = 1; u < 8; ++u) hs[u] = hrow[min(ht + u * kHistThreads, len - 1u)];
@@ -1663,53 +1669,90 @@ __global__ __launch_bounds__(kSelectThreads) void lm_select_kernel(LmParams p, R
     if (rp.hist_vec4) {
       // Sixteen ids (four uint4) per thread per batch: their bitmap words are
       // read together (one LDS round trip), then only the missing bits are
-      // set (Zipf histories repeat a few ids thousands of times).  Two batches
-      // alternate between register sets and the loads are unconditional
-      // (clamped inside the row; hist_ld is a multiple of 4), so no loaded
-      // register crosses the loop edge and the next batch is in flight while
-      // this one is used.
+      // set (Zipf histories repeat a few ids thousands of times).  A batch
+      // whose last position is inside the row is live throughout and takes
+      // no per-element tests; an id >= vocab is looked for once per batch
+      // (the largest id), and the rare batch that holds one records the first
+      // bad position and sets no bit for it.  Positions past the row read id 0
+      // and set nothing.
       auto batch = [&](uint32_t k0, const v4u (&h)[4]) {
-        uint32_t wi[16], bit[16];
+        uint32_t id[16], bit[16];
 #pragma unroll
         for (uint32_t u = 0; u < 4; ++u) {
-          const uint32_t k = k0 + u * kHistThreads;
-          const uint32_t ids[4] = {h[u].x, h[u].y, h[u].z, h[u].w};
+          id[4 * u] = h[u].x;
+          id[4 * u + 1] = h[u].y;
+          id[4 * u + 2] = h[u].z;
+          id[4 * u + 3] = h[u].w;
+        }
+        if (4u * (k0 + 3u * kHistThreads) + 3u < len) {
 #pragma unroll
-          for (uint32_t c = 0; c < 4; ++c) {
-            const uint32_t pos = 4u * k + c;
-            const uint32_t id = ids[c];
-            const bool live = k < n4 && pos < len;
-            if (live && id >= kVocab) my_bad = pos < my_bad ? pos : my_bad;
-            const bool set = live && id < kVocab;
-            wi[4 * u + c] = set ? id >> 5 : 0u;
-            bit[4 * u + c] = set ? 1u << (id & 31u) : 0u;
+          for (int e = 0; e < 16; ++e) bit[e] = 1u << (id[e] & 31u);
+        } else {
+#pragma unroll
+          for (uint32_t e = 0; e < 16; ++e) {
+            const bool live = 4u * (k0 + (e >> 2) * kHistThreads) + (e & 3u) < len;
+            id[e] = live ? id[e] : 0u;
+            bit[e] = live ? 1u << (id[e] & 31u) : 0u;
+          }
+        }
+        uint32_t top_id = 0;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) top_id = max(top_id, id[e]);
+        if (top_id >= kVocab) {
+#pragma unroll
+          for (uint32_t e = 0; e < 16; ++e) {
+            if (id[e] >= kVocab) {
+              const uint32_t pos = 4u * (k0 + (e >> 2) * kHistThreads) + (e & 3u);
+              my_bad = pos < my_bad ? pos : my_bad;
+              id[e] = 0u;
+              bit[e] = 0u;
+            }
           }
         }
         uint32_t cur[16];
 #pragma unroll
         for (int e = 0; e < 16; ++e)
-          cur[e] = __hip_atomic_load(&bm[wi[e]], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+          cur[e] = __hip_atomic_load(&bm[id[e] >> 5], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 #pragma unroll
-        for (int e = 0; e < 16; ++e)
-          if ((cur[e] & bit[e]) == 0u && bit[e] != 0u) atomicOr(&bm[wi[e]], bit[e]);
+        for (int e = 0; e < 16; ++e) {
+          const uint32_t need = bit[e] & ~cur[e];
+          if (need != 0u) atomicOr(&bm[id[e] >> 5], need);
+        }
       };
       auto load4 = [&](uint32_t k0, v4u (&h)[4]) {
 #pragma unroll
         for (uint32_t u = 0; u < 4; ++u) h[u] = h4[min(k0 + u * kHistThreads, n4 - 1u)];
       };
-      v4u hb[4];
       if (uniform(n4) <= 4u * kHistThreads) {
         // the loads made at entry hold the whole history: no batch is
         // requested ahead (a load nothing uses would still be waited for at
         // the next barrier)
         if (ht < n4) batch(ht, hv);
       } else {
-        for (uint32_t k0 = ht; k0 < n4; k0 += 8u * kHistThreads) {
-          load4(k0 + 4u * kHistThreads, hb);
-          batch(k0, hv);
-          if (k0 + 4u * kHistThreads >= n4) break;
-          load4(k0 + 8u * kHistThreads, hv);
-          batch(k0 + 4u * kHistThreads, hb);
+        // Longer histories: the second batch was requested at entry too; the
+        // rest come kHistGroup batches at a time (one memory round trip per
+        // group, the first group's behind the first two batches).  The loads
+        // are clamped inside the row; a batch past the row's end is not used.
+        constexpr uint32_t kStep = 4u * kHistThreads;
+        const bool groups = uniform(n4) > 2u * kStep;
+        v4u more[kHistGroup][4];
+        uint32_t k0 = ht + 2u * kStep;
+        if (groups) {
+#pragma unroll
+          for (uint32_t s = 0; s < kHistGroup; ++s) load4(k0 + s * kStep, more[s]);
+        }
+        batch(ht, hv);
+        if (ht + kStep < n4) batch(ht + kStep, hb);
+        if (groups) {
+          for (;; k0 += kHistGroup * kStep) {
+#pragma unroll
+            for (uint32_t s = 0; s < kHistGroup; ++s)
+              if (k0 + s * kStep < n4) batch(k0 + s * kStep, more[s]);
+            if (k0 + kHistGroup * kStep >= n4) break;
+#pragma unroll
+            for (uint32_t s = 0; s < kHistGroup; ++s)
+              load4(k0 + (kHistGroup + s) * kStep, more[s]);
+          }
         }
       }
     } else {
