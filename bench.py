@@ -933,6 +933,8 @@ def main() -> int:
     ap.add_argument("--no-production", action="store_true",
                     help="skip the reference's own timed case (hello row, seed 0x0123456789abcdef)")
     ap.add_argument("--batches", default="1,64,4096")
+    ap.add_argument("--no-device-histories", action="store_true",
+                    help="skip the B=1 steps with histories of 1,000 to 32,000 ids")
     ap.add_argument("--no-cold", action="store_true",
                     help="skip the cold passes of B=1 and B=64 (inputs rotated over more "
                          "than the last-level cache)")
@@ -1029,7 +1031,7 @@ def main() -> int:
         log("timing with the inputs in host memory (PCIe included)")
         host_buffers = time_host_buffers(smp, work[1], work[4096], stream)
     device_histories = None
-    if 1 in work:
+    if 1 in work and not args.no_device_histories:
         log("timing one conversation's step with longer histories (inputs in HBM)")
         device_histories = time_device_histories(smp, work[1], stream)
     smp.close()
