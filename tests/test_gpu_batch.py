@@ -149,6 +149,37 @@ def test_error_rows_and_precedence(sampler):
     assert (det[1:6]["ids"] == 0xFFFFFFFF).all()
 
 
+def test_bad_ids_deep_in_full_context_histories(sampler):
+    """Ids >= vocab at every batch boundary of a 32,768-id history: the end of
+    the first batch of 4,096 ids and the start of the second, the start of
+    the batches requested two at a time after them, the last position, and
+    one just past a row's length (ignored).  The first bad position decides
+    the error (its id is the record's `available`); a non-finite logit
+    still wins.  Tile selection (8 rows) and both slice plans, against the
+    oracle."""
+    w = workloads.make("large", rows=8)
+    lg, hist, hl = w["logits"], w["hist"], w["hist_len"]
+    assert hist.shape[1] == 32768
+    hl[:] = 32768
+    hist[0, [5000, 20000]] = [V + 1, V + 2]       # the first one wins
+    hist[1, 32767] = V + 3                        # the last position
+    hist[2, [8192, 30000]] = [V + 4, 0xFFFFFFFF]  # first batch of the first pair
+    hist[3, 4096] = V + 5                         # first id of the second batch
+    hl[4] = 9000
+    hist[4, 9000] = V + 6                         # past the length: ignored
+    hist[5, 12345] = V + 7
+    lg[5, 77] = np.nan                            # non-finite beats a bad id
+    hl[7] = 4097
+    hist[7, 4096] = V + 8                         # the row's last position
+    hist[7, 4095] = V + 9                         # ... after an earlier one
+    for segments in (0, 1, 7):
+        assert_rows_equal(*run_gpu(sampler, w, segments), *run_oracle(w))
+    tok, det, err = run_gpu(sampler, w)
+    assert err["status"].tolist() == [3, 3, 3, 3, 0, 7, 0, 3]
+    assert err["available"][[0, 1, 2, 3, 7]].tolist() == [V + 1, V + 3, V + 4, V + 5, V + 9]
+    assert tok[4] != s.NO_TOKEN and tok[6] != s.NO_TOKEN
+
+
 def test_inplace_variant_penalises_like_the_reference(sampler):
     import torch
 
