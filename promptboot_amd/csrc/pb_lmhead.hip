@@ -1201,6 +1201,7 @@ constexpr int kRecomputeQ8 = 2;
 constexpr uint32_t kTileWaves = 4;                      // waves that read the tile words
 constexpr uint32_t kHistWaves = 4;                      // waves that build the history bitmap
 constexpr uint32_t kHistGroup = 2;                      // later history batches requested together
+constexpr uint32_t kHistShareFrom = 4;                  // batches from which the tile waves take a share
 constexpr uint32_t kSelectThreads = 64u * (kTileWaves + kHistWaves);
 constexpr int kTileKeys = (kTilesPerRow + 63) / 64;    // 38 tile words per lane
 constexpr int kWaveKeys = (kTileKeys + (int)kTileWaves - 1) / (int)kTileWaves;  // 10 per tile wave
@@ -1655,6 +1656,72 @@ __global__ __launch_bounds__(kSelectThreads) void lm_select_kernel(LmParams p, R
     }
   };
 
+  // ---- the history bitmap: per batch of sixteen ids per thread ----
+  uint32_t my_bad = kNone;
+  // Sixteen ids (four uint4) per thread per batch: their bitmap words are
+  // read together (one LDS round trip), then only the missing bits are
+  // set (Zipf histories repeat a few ids thousands of times).  A batch
+  // whose last position is inside the row is live throughout and takes
+  // no per-element tests; an id >= vocab is looked for once per batch
+  // (the largest id), and the rare batch that holds one records the first
+  // bad position and sets no bit for it.  Positions past the row read id 0
+  // and set nothing.
+  auto batch = [&](uint32_t k0, const v4u (&h)[4]) {
+    uint32_t id[16], bit[16];
+#pragma unroll
+    for (uint32_t u = 0; u < 4; ++u) {
+      id[4 * u] = h[u].x;
+      id[4 * u + 1] = h[u].y;
+      id[4 * u + 2] = h[u].z;
+      id[4 * u + 3] = h[u].w;
+    }
+    if (4u * (k0 + 3u * kHistThreads) + 3u < len) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) bit[e] = 1u << (id[e] & 31u);
+    } else {
+#pragma unroll
+      for (uint32_t e = 0; e < 16; ++e) {
+        const bool live = 4u * (k0 + (e >> 2) * kHistThreads) + (e & 3u) < len;
+        id[e] = live ? id[e] : 0u;
+        bit[e] = live ? 1u << (id[e] & 31u) : 0u;
+      }
+    }
+    uint32_t top_id = 0;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) top_id = max(top_id, id[e]);
+    if (top_id >= kVocab) {
+#pragma unroll
+      for (uint32_t e = 0; e < 16; ++e) {
+        if (id[e] >= kVocab) {
+          const uint32_t pos = 4u * (k0 + (e >> 2) * kHistThreads) + (e & 3u);
+          my_bad = pos < my_bad ? pos : my_bad;
+          id[e] = 0u;
+          bit[e] = 0u;
+        }
+      }
+    }
+    uint32_t cur[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e)
+      cur[e] = __hip_atomic_load(&bm[id[e] >> 5], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const uint32_t need = bit[e] & ~cur[e];
+      if (need != 0u) atomicOr(&bm[id[e] >> 5], need);
+    }
+  };
+  auto load4 = [&](uint32_t k0, v4u (&h)[4]) {
+#pragma unroll
+    for (uint32_t u = 0; u < 4; ++u) h[u] = h4[min(k0 + u * kHistThreads, n4 - 1u)];
+  };
+  // A long history's batches (4,096 ids each) are split: the history waves
+  // take the first hist_split, the tile waves the rest once their first
+  // round is out.
+  constexpr uint32_t kHistStep = 4u * kHistThreads;
+  const uint32_t hist_batches = (n4 + kHistStep - 1u) / kHistStep;
+  const uint32_t hist_split =
+      hist_batches <= kHistShareFrom ? hist_batches : 2u + (hist_batches - 1u) / 2u;
+
   if (tile_wave) {
     if (nf_tile == kNone) {
       uint32_t best = 0;
@@ -1663,66 +1730,21 @@ __global__ __launch_bounds__(kSelectThreads) void lm_select_kernel(LmParams p, R
       thr_first = uniform(bcast32(wave_sort_desc_u32(best, lane), kTopK - 1));
       tile_round(thr_first);
     }
+    if (rp.hist_vec4 && hist_split < hist_batches) {
+      for (uint32_t k0 = tid + hist_split * kHistStep; k0 < n4; k0 += kHistGroup * kHistStep) {
+        v4u more[kHistGroup][4];
+#pragma unroll
+        for (uint32_t s = 0; s < kHistGroup; ++s) load4(k0 + s * kHistStep, more[s]);
+#pragma unroll
+        for (uint32_t s = 0; s < kHistGroup; ++s)
+          if (k0 + s * kHistStep < n4) batch(k0 + s * kHistStep, more[s]);
+      }
+      my_bad = wave_min_u32(my_bad);
+      if (lane == 0 && my_bad != kNone) atomicMin(&bad_hist, my_bad);
+    }
   } else {
     // ---- the history bitmap and the first bad position ----
-    uint32_t my_bad = kNone;
     if (rp.hist_vec4) {
-      // Sixteen ids (four uint4) per thread per batch: their bitmap words are
-      // read together (one LDS round trip), then only the missing bits are
-      // set (Zipf histories repeat a few ids thousands of times).  A batch
-      // whose last position is inside the row is live throughout and takes
-      // no per-element tests; an id >= vocab is looked for once per batch
-      // (the largest id), and the rare batch that holds one records the first
-      // bad position and sets no bit for it.  Positions past the row read id 0
-      // and set nothing.
-      auto batch = [&](uint32_t k0, const v4u (&h)[4]) {
-        uint32_t id[16], bit[16];
-#pragma unroll
-        for (uint32_t u = 0; u < 4; ++u) {
-          id[4 * u] = h[u].x;
-          id[4 * u + 1] = h[u].y;
-          id[4 * u + 2] = h[u].z;
-          id[4 * u + 3] = h[u].w;
-        }
-        if (4u * (k0 + 3u * kHistThreads) + 3u < len) {
-#pragma unroll
-          for (int e = 0; e < 16; ++e) bit[e] = 1u << (id[e] & 31u);
-        } else {
-#pragma unroll
-          for (uint32_t e = 0; e < 16; ++e) {
-            const bool live = 4u * (k0 + (e >> 2) * kHistThreads) + (e & 3u) < len;
-            id[e] = live ? id[e] : 0u;
-            bit[e] = live ? 1u << (id[e] & 31u) : 0u;
-          }
-        }
-        uint32_t top_id = 0;
-#pragma unroll
-        for (int e = 0; e < 16; ++e) top_id = max(top_id, id[e]);
-        if (top_id >= kVocab) {
-#pragma unroll
-          for (uint32_t e = 0; e < 16; ++e) {
-            if (id[e] >= kVocab) {
-              const uint32_t pos = 4u * (k0 + (e >> 2) * kHistThreads) + (e & 3u);
-              my_bad = pos < my_bad ? pos : my_bad;
-              id[e] = 0u;
-              bit[e] = 0u;
-            }
-          }
-        }
-        uint32_t cur[16];
-#pragma unroll
-        for (int e = 0; e < 16; ++e)
-          cur[e] = __hip_atomic_load(&bm[id[e] >> 5], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const uint32_t need = bit[e] & ~cur[e];
-          if (need != 0u) atomicOr(&bm[id[e] >> 5], need);
-        }
-      };
-      auto load4 = [&](uint32_t k0, v4u (&h)[4]) {
-#pragma unroll
-        for (uint32_t u = 0; u < 4; ++u) h[u] = h4[min(k0 + u * kHistThreads, n4 - 1u)];
-      };
       if (uniform(n4) <= 4u * kHistThreads) {
         // the loads made at entry hold the whole history: no batch is
         // requested ahead (a load nothing uses would still be waited for at
@@ -1733,25 +1755,25 @@ __global__ __launch_bounds__(kSelectThreads) void lm_select_kernel(LmParams p, R
         // rest come kHistGroup batches at a time (one memory round trip per
         // group, the first group's behind the first two batches).  The loads
         // are clamped inside the row; a batch past the row's end is not used.
-        constexpr uint32_t kStep = 4u * kHistThreads;
-        const bool groups = uniform(n4) > 2u * kStep;
+        const bool groups = hist_split > 2u;
+        const uint32_t lim = min(n4, ht + hist_split * kHistStep);  // past the tile waves' share
         v4u more[kHistGroup][4];
-        uint32_t k0 = ht + 2u * kStep;
+        uint32_t k0 = ht + 2u * kHistStep;
         if (groups) {
 #pragma unroll
-          for (uint32_t s = 0; s < kHistGroup; ++s) load4(k0 + s * kStep, more[s]);
+          for (uint32_t s = 0; s < kHistGroup; ++s) load4(k0 + s * kHistStep, more[s]);
         }
         batch(ht, hv);
-        if (ht + kStep < n4) batch(ht + kStep, hb);
+        if (ht + kHistStep < n4) batch(ht + kHistStep, hb);
         if (groups) {
-          for (;; k0 += kHistGroup * kStep) {
+          for (;; k0 += kHistGroup * kHistStep) {
 #pragma unroll
             for (uint32_t s = 0; s < kHistGroup; ++s)
-              if (k0 + s * kStep < n4) batch(k0 + s * kStep, more[s]);
-            if (k0 + kHistGroup * kStep >= n4) break;
+              if (k0 + s * kHistStep < lim) batch(k0 + s * kHistStep, more[s]);
+            if (k0 + kHistGroup * kHistStep >= lim) break;
 #pragma unroll
             for (uint32_t s = 0; s < kHistGroup; ++s)
-              load4(k0 + (kHistGroup + s) * kStep, more[s]);
+              load4(k0 + (kHistGroup + s) * kHistStep, more[s]);
           }
         }
       }
