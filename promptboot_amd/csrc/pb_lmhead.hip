@@ -1201,7 +1201,7 @@ constexpr int kRecomputeQ8 = 2;
 constexpr uint32_t kTileWaves = 4;                      // waves that read the tile words
 constexpr uint32_t kHistWaves = 4;                      // waves that build the history bitmap
 constexpr uint32_t kHistGroup = 2;                      // later history batches requested together
-constexpr uint32_t kHistShareFrom = 4;                  // batches from which the tile waves take a share
+constexpr uint32_t kHistShareFrom = 3;                  // batches from which the tile waves take a share
 constexpr uint32_t kSelectThreads = 64u * (kTileWaves + kHistWaves);
 constexpr int kTileKeys = (kTilesPerRow + 63) / 64;    // 38 tile words per lane
 constexpr int kWaveKeys = (kTileKeys + (int)kTileWaves - 1) / (int)kTileWaves;  // 10 per tile wave
